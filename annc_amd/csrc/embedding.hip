@@ -1,0 +1,432 @@
+// embedding.hip -- embedding bags, segment reduction, masked gather and
+// padded pooling on gfx950.
+//
+// Reference semantics (all CPU loops in ANNC):
+//   * KPFusedSparseSegmentReduce
+//     (annc/tensorflow/kernels/embedding_fused_sparse_segment_reduce.cc:87-151):
+//     out[seg] accumulates data[idx] row by row in index order, per dim,
+//     starting from 0.0f; mean multiplies by 1.0f/count.
+//   * sparse_embedding2 kLoop fusion (annc/service/cpu/graph_opt.cc:8-41).
+//   * __pooling (annc/service/cpu/graph_opt.cc:131-176).
+//
+// Bag kernel layout: a bag is owned by a group of G lanes of one wave64
+// (G = dim/4 rounded up to a power of two, 4..64), each lane holding 4
+// consecutive floats of the row, so a row is one contiguous G*16-byte
+// (up to 1 KiB) read and one wave covers 64/G bags.  Every lane adds its
+// rows in index order, which reproduces the reference's summation order
+// exactly: the sum is bit-identical.  Eight row loads are issued before
+// the first add to keep them in flight together.
+#include <hip/hip_runtime.h>
+#include <hipcub/hipcub.hpp>
+
+#include <algorithm>
+
+#include "common.h"
+#include "embedding_impl.h"
+
+namespace annc {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kUnroll = 8;
+
+template <int VEC>
+struct VecT;
+template <>
+struct VecT<4> {
+  typedef float type __attribute__((ext_vector_type(4)));
+};
+template <>
+struct VecT<1> {
+  typedef float type;
+};
+
+template <int VEC>
+__device__ __forceinline__ typename VecT<VEC>::type load_row(const float* p) {
+  return *reinterpret_cast<const typename VecT<VEC>::type*>(p);
+}
+
+template <int VEC>
+__device__ __forceinline__ void store_row(float* p, typename VecT<VEC>::type v) {
+  *reinterpret_cast<typename VecT<VEC>::type*>(p) = v;
+}
+
+template <typename IdxT>
+__device__ __forceinline__ int64_t fetch_id(const IdxT* __restrict__ ids,
+                                            const int32_t* __restrict__ perm, int64_t j) {
+  return perm ? static_cast<int64_t>(ids[perm[j]]) : static_cast<int64_t>(ids[j]);
+}
+
+template <typename IdxT, int G, int VEC, bool MEAN>
+__global__ __launch_bounds__(kThreads) void bag_kernel(
+    const float* __restrict__ table, int64_t rows, int64_t dim, const IdxT* __restrict__ ids,
+    const int32_t* __restrict__ perm, const int64_t* __restrict__ offsets, int64_t num_bags,
+    float* __restrict__ out, int64_t ldo, int* __restrict__ status) {
+  typedef typename VecT<VEC>::type V;
+  const int g = threadIdx.x & (G - 1);
+  const int64_t bag = ((int64_t)blockIdx.x * kThreads + threadIdx.x) / G;
+  if (bag >= num_bags) return;
+  const int64_t beg = offsets[bag];
+  const int64_t end = offsets[bag + 1];
+  bool bad = false;
+  for (int64_t c = (int64_t)g * VEC; c < dim; c += (int64_t)G * VEC) {
+    V acc = V(0.0f);
+    int64_t j = beg;
+    for (; j + kUnroll <= end; j += kUnroll) {
+      int64_t r[kUnroll];
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) r[u] = fetch_id(ids, perm, j + u);
+      V v[kUnroll];
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        const bool ok = static_cast<uint64_t>(r[u]) < static_cast<uint64_t>(rows);
+        bad |= !ok;
+        v[u] = ok ? load_row<VEC>(table + r[u] * dim + c) : V(0.0f);
+      }
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) acc += v[u];
+    }
+    for (; j < end; ++j) {
+      const int64_t r = fetch_id(ids, perm, j);
+      const bool ok = static_cast<uint64_t>(r) < static_cast<uint64_t>(rows);
+      bad |= !ok;
+      if (ok) acc += load_row<VEC>(table + r * dim + c);
+    }
+    if (MEAN) {
+      const int32_t cnt = static_cast<int32_t>(end - beg);
+      if (cnt > 0) {
+        const float inv = 1.0f / static_cast<float>(cnt);
+        acc *= inv;
+      }
+    }
+    store_row<VEC>(out + bag * ldo + c, acc);
+  }
+  if (bad) atomicOr(status, 1);
+}
+
+template <typename IdxT, int G, int VEC>
+int launch_bag_g(const BagArgs& a, hipStream_t s) {
+  const int64_t threads = a.num_bags * G;
+  dim3 grid((unsigned)ceil_div(threads, kThreads));
+  const IdxT* ids = static_cast<const IdxT*>(a.ids);
+  if (a.combiner == ANNC_COMBINER_MEAN)
+    hipLaunchKernelGGL((bag_kernel<IdxT, G, VEC, true>), grid, dim3(kThreads), 0, s, a.table,
+                       a.rows, a.dim, ids, a.perm, a.offsets, a.num_bags, a.out, a.ldo, a.status);
+  else
+    hipLaunchKernelGGL((bag_kernel<IdxT, G, VEC, false>), grid, dim3(kThreads), 0, s, a.table,
+                       a.rows, a.dim, ids, a.perm, a.offsets, a.num_bags, a.out, a.ldo, a.status);
+  ANNC_HIP_TRY(hipGetLastError());
+  return ANNC_OK;
+}
+
+template <typename IdxT, int VEC>
+int launch_bag_vec(const BagArgs& a, hipStream_t s) {
+  const int64_t lanes = ceil_div(a.dim, VEC);
+  if (lanes <= 4) return launch_bag_g<IdxT, 4, VEC>(a, s);
+  if (lanes <= 8) return launch_bag_g<IdxT, 8, VEC>(a, s);
+  if (lanes <= 16) return launch_bag_g<IdxT, 16, VEC>(a, s);
+  if (lanes <= 32) return launch_bag_g<IdxT, 32, VEC>(a, s);
+  return launch_bag_g<IdxT, 64, VEC>(a, s);
+}
+
+template <typename IdxT>
+int launch_bag_idx(const BagArgs& a, hipStream_t s) {
+  auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  const bool vec = a.dim % 4 == 0 && a.ldo % 4 == 0 && al16(a.table) && al16(a.out);
+  return vec ? launch_bag_vec<IdxT, 4>(a, s) : launch_bag_vec<IdxT, 1>(a, s);
+}
+
+// ---------------------------------------------------------------------------
+// Segment-id preprocessing for unsorted segment reduction.
+// ---------------------------------------------------------------------------
+__global__ void seg_scan_kernel(const int64_t* __restrict__ seg, int64_t stride, int64_t n,
+                                long long* __restrict__ minmax, int* __restrict__ unsorted) {
+  long long lo = LLONG_MAX, hi = LLONG_MIN;
+  int unsort = 0;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const long long v = seg[i * stride];
+    lo = v < lo ? v : lo;
+    hi = v > hi ? v : hi;
+    if (i > 0 && v < seg[(i - 1) * stride]) unsort = 1;
+  }
+  for (int off = 32; off > 0; off >>= 1) {
+    const long long l2 = __shfl_xor(lo, off, 64);
+    const long long h2 = __shfl_xor(hi, off, 64);
+    lo = l2 < lo ? l2 : lo;
+    hi = h2 > hi ? h2 : hi;
+    unsort |= __shfl_xor(unsort, off, 64);
+  }
+  if ((threadIdx.x & 63) == 0) {
+    atomicMin(&minmax[0], lo);
+    atomicMax(&minmax[1], hi);
+    if (unsort) atomicOr(unsorted, 1);
+  }
+}
+
+__global__ void init_scan_kernel(long long* minmax, int* unsorted) {
+  minmax[0] = LLONG_MAX;
+  minmax[1] = LLONG_MIN;
+  *unsorted = 0;
+}
+
+// offsets[s] = first position whose segment id is >= s, for s in [0, batch];
+// the segment ids read through `seg` (stride) must be non-decreasing.
+template <typename KeyT>
+__global__ void lower_bound_kernel(const KeyT* __restrict__ seg, int64_t stride, int64_t n,
+                                   int64_t batch, int64_t* __restrict__ offsets) {
+  const int64_t s = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (s > batch) return;
+  int64_t lo = 0, hi = n;
+  while (lo < hi) {
+    const int64_t mid = (lo + hi) >> 1;
+    if (static_cast<int64_t>(seg[mid * stride]) < s)
+      lo = mid + 1;
+    else
+      hi = mid;
+  }
+  offsets[s] = lo;
+}
+
+__global__ void make_keys_kernel(const int64_t* __restrict__ seg, int64_t stride, int64_t n,
+                                 uint32_t* __restrict__ keys, int32_t* __restrict__ vals) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  keys[i] = static_cast<uint32_t>(seg[i * stride]);
+  vals[i] = static_cast<int32_t>(i);
+}
+
+// ---------------------------------------------------------------------------
+// sparse_embedding2 and __pooling
+// ---------------------------------------------------------------------------
+template <typename IdxT>
+__global__ __launch_bounds__(kThreads) void sparse_embedding2_kernel(
+    const float* __restrict__ table, int64_t rows, int64_t dim, const IdxT* __restrict__ ids,
+    int64_t n, int64_t fallback, float* __restrict__ out) {
+  const int64_t t = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (t >= n * dim) return;
+  const int64_t i = t / dim, d = t % dim;
+  const int64_t id = static_cast<int64_t>(ids[i]);
+  const bool valid = id >= 0 && id < rows;
+  const float mask = valid ? 1.0f : 0.0f;
+  out[t] = table[(valid ? id : fallback) * dim + d] * mask;
+}
+
+__global__ __launch_bounds__(kThreads) void pooling_kernel(
+    const int64_t* __restrict__ ids, const float* __restrict__ gathered, int64_t m, int64_t k,
+    int64_t n, int64_t ss0, int64_t ss1, int64_t ss2, int64_t sl0, int64_t sl1, int64_t sl2,
+    float* __restrict__ out) {
+  const int64_t t = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (t >= m * n) return;
+  const int64_t i = t / n, p = t % n;
+  const int64_t* row_ids = ids + i * k;
+  float red = 0.0f;
+  for (int64_t j = 0; j < k; ++j) red += row_ids[j] > 0 ? 1.0f : 0.0f;
+  float sum = 0.0f;
+  const bool in_rows = i >= ss0 && i < sl0 && p >= ss2 && p < sl2;
+  if (in_rows) {
+    const int64_t j0 = ss1 > 0 ? ss1 : 0;
+    const int64_t j1 = sl1 < k ? sl1 : k;
+    for (int64_t j = j0; j < j1; ++j)
+      if (row_ids[j] > 0) sum += gathered[(i * k + j) * n + p];
+  }
+  out[t] = red == 0.0f ? 0.0f : sum / red;
+}
+
+}  // namespace
+
+int launch_bag(const BagArgs& a, hipStream_t s) {
+  return a.ids_is_64 ? launch_bag_idx<int64_t>(a, s) : launch_bag_idx<int32_t>(a, s);
+}
+
+int segment_scan(hipStream_t s, const int64_t* seg, int64_t stride, int64_t n, int64_t* min_out,
+                 int64_t* max_out, bool* sorted) {
+  void* ws = stream_workspace(s, 64);
+  if (!ws) return set_error(ANNC_RESOURCE_EXHAUSTED, "workspace allocation failed");
+  long long* minmax = static_cast<long long*>(ws);
+  int* unsorted = reinterpret_cast<int*>(minmax + 2);
+  hipLaunchKernelGGL(init_scan_kernel, dim3(1), dim3(1), 0, s, minmax, unsorted);
+  if (n > 0) {
+    const int blocks = (int)std::min<int64_t>(1024, ceil_div(n, kThreads));
+    hipLaunchKernelGGL(seg_scan_kernel, dim3(blocks), dim3(kThreads), 0, s, seg, stride, n,
+                       minmax, unsorted);
+  }
+  ANNC_HIP_TRY(hipGetLastError());
+  long long host[3];
+  ANNC_HIP_TRY(hipMemcpyAsync(host, ws, sizeof(long long) * 3, hipMemcpyDeviceToHost, s));
+  ANNC_HIP_TRY(hipStreamSynchronize(s));
+  *min_out = host[0];
+  *max_out = host[1];
+  *sorted = reinterpret_cast<int*>(&host[2])[0] == 0;
+  return ANNC_OK;
+}
+
+int segment_reduce(hipStream_t s, const float* data, int64_t rows, int64_t dim,
+                   const void* indices, int indices_is_64, const int64_t* seg, int64_t stride,
+                   int64_t n, int combiner, int64_t batch, float* out, int sorted_hint) {
+  if (batch <= 0) return ANNC_OK;
+  int* status = stream_status(s);
+  if (!status) return set_error(ANNC_RESOURCE_EXHAUSTED, "status allocation failed");
+  ANNC_REQUIRE(n < (1ll << 31), "too many indices");
+  ANNC_REQUIRE(batch < (1ll << 32), "too many segments");
+
+  BagArgs a{};
+  a.table = data;
+  a.rows = rows;
+  a.dim = dim;
+  a.ids = indices;
+  a.ids_is_64 = indices_is_64;
+  a.num_bags = batch;
+  a.combiner = combiner;
+  a.out = out;
+  a.ldo = dim;
+  a.status = status;
+
+  const size_t off_bytes = sizeof(int64_t) * (size_t)(batch + 1);
+  if (sorted_hint == 1) {
+    int64_t* offsets = static_cast<int64_t*>(stream_workspace(s, off_bytes));
+    if (!offsets) return set_error(ANNC_RESOURCE_EXHAUSTED, "workspace allocation failed");
+    hipLaunchKernelGGL(lower_bound_kernel<int64_t>, dim3((unsigned)ceil_div(batch + 1, kThreads)),
+                       dim3(kThreads), 0, s, seg, stride, n, batch, offsets);
+    ANNC_HIP_TRY(hipGetLastError());
+    a.offsets = offsets;
+    a.perm = nullptr;
+    return launch_bag(a, s);
+  }
+
+  // General order: stable radix sort of (segment id, position), then CSR.
+  int end_bit = 1;
+  while (end_bit < 32 && (1ull << end_bit) < (uint64_t)batch) ++end_bit;
+  size_t temp_bytes = 0;
+  ANNC_HIP_TRY(hipcub::DeviceRadixSort::SortPairs(nullptr, temp_bytes, (const uint32_t*)nullptr,
+                                                  (uint32_t*)nullptr, (const int32_t*)nullptr,
+                                                  (int32_t*)nullptr, (int)n, 0, end_bit, s));
+  auto align = [](size_t x) { return (x + 255) & ~size_t(255); };
+  const size_t nk = align(sizeof(uint32_t) * (size_t)std::max<int64_t>(n, 1));
+  const size_t nv = align(sizeof(int32_t) * (size_t)std::max<int64_t>(n, 1));
+  const size_t total = 2 * nk + 2 * nv + align(off_bytes) + align(temp_bytes);
+  char* ws = static_cast<char*>(stream_workspace(s, total));
+  if (!ws) return set_error(ANNC_RESOURCE_EXHAUSTED, "workspace allocation failed");
+  uint32_t* keys_in = reinterpret_cast<uint32_t*>(ws);
+  uint32_t* keys_out = reinterpret_cast<uint32_t*>(ws + nk);
+  int32_t* vals_in = reinterpret_cast<int32_t*>(ws + 2 * nk);
+  int32_t* vals_out = reinterpret_cast<int32_t*>(ws + 2 * nk + nv);
+  int64_t* offsets = reinterpret_cast<int64_t*>(ws + 2 * nk + 2 * nv);
+  void* temp = ws + 2 * nk + 2 * nv + align(off_bytes);
+  if (n > 0) {
+    hipLaunchKernelGGL(make_keys_kernel, dim3((unsigned)ceil_div(n, kThreads)), dim3(kThreads), 0,
+                       s, seg, stride, n, keys_in, vals_in);
+    ANNC_HIP_TRY(hipGetLastError());
+    ANNC_HIP_TRY(hipcub::DeviceRadixSort::SortPairs(temp, temp_bytes, keys_in, keys_out, vals_in,
+                                                    vals_out, (int)n, 0, end_bit, s));
+  }
+  hipLaunchKernelGGL(lower_bound_kernel<uint32_t>, dim3((unsigned)ceil_div(batch + 1, kThreads)),
+                     dim3(kThreads), 0, s, keys_out, (int64_t)1, n, batch, offsets);
+  ANNC_HIP_TRY(hipGetLastError());
+  a.offsets = offsets;
+  a.perm = vals_out;
+  return launch_bag(a, s);
+}
+
+int launch_sparse_embedding2(hipStream_t s, const float* table, int64_t rows, int64_t dim,
+                             const void* ids, int ids_is_64, int64_t n, int64_t fallback,
+                             float* out) {
+  const int64_t total = n * dim;
+  if (total == 0) return ANNC_OK;
+  dim3 grid((unsigned)ceil_div(total, kThreads));
+  if (ids_is_64)
+    hipLaunchKernelGGL(sparse_embedding2_kernel<int64_t>, grid, dim3(kThreads), 0, s, table, rows,
+                       dim, static_cast<const int64_t*>(ids), n, fallback, out);
+  else
+    hipLaunchKernelGGL(sparse_embedding2_kernel<int32_t>, grid, dim3(kThreads), 0, s, table, rows,
+                       dim, static_cast<const int32_t*>(ids), n, fallback, out);
+  ANNC_HIP_TRY(hipGetLastError());
+  return ANNC_OK;
+}
+
+int launch_pooling(hipStream_t s, const int64_t* ids, const float* gathered, int64_t m, int64_t k,
+                   int64_t n, const int64_t* ss, const int64_t* sl, float* out) {
+  if (m * n == 0) return ANNC_OK;
+  hipLaunchKernelGGL(pooling_kernel, dim3((unsigned)ceil_div(m * n, kThreads)), dim3(kThreads), 0,
+                     s, ids, gathered, m, k, n, ss[0], ss[1], ss[2], sl[0], sl[1], sl[2], out);
+  ANNC_HIP_TRY(hipGetLastError());
+  return ANNC_OK;
+}
+
+}  // namespace annc
+
+extern "C" {
+
+int annc_hip_embedding_bag(void* stream, const float* table, int64_t rows, int64_t dim,
+                           const void* ids, int ids_is_64, const int64_t* offsets,
+                           int64_t num_bags, int combiner, float* out, int64_t ldo) {
+  using namespace annc;
+  ANNC_REQUIRE(rows >= 0 && dim >= 1 && num_bags >= 0, "bad table or bag dimensions");
+  ANNC_REQUIRE(ldo >= dim, "ldo < dim");
+  ANNC_REQUIRE(combiner == ANNC_COMBINER_SUM || combiner == ANNC_COMBINER_MEAN,
+               "combiner must be 0 or 1");
+  if (num_bags == 0) return set_error(ANNC_OK, "");
+  ANNC_REQUIRE(table && ids && offsets && out, "null pointer");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  int* status = stream_status(s);
+  if (!status) return set_error(ANNC_RESOURCE_EXHAUSTED, "status allocation failed");
+  BagArgs a{};
+  a.table = table;
+  a.rows = rows;
+  a.dim = dim;
+  a.ids = ids;
+  a.ids_is_64 = ids_is_64;
+  a.offsets = offsets;
+  a.perm = nullptr;
+  a.num_bags = num_bags;
+  a.combiner = combiner;
+  a.out = out;
+  a.ldo = ldo;
+  a.status = status;
+  int rc = launch_bag(a, s);
+  return rc == ANNC_OK ? set_error(ANNC_OK, "") : rc;
+}
+
+int annc_hip_segment_reduce(void* stream, const float* data, int64_t rows, int64_t dim,
+                            const void* indices, int indices_is_64, const int64_t* seg_ids,
+                            int64_t seg_stride, int64_t n, int combiner, int64_t batch,
+                            float* out) {
+  using namespace annc;
+  ANNC_REQUIRE(rows >= 0 && dim >= 1 && n >= 0 && batch >= 0 && seg_stride >= 1,
+               "bad dimensions");
+  ANNC_REQUIRE(combiner == ANNC_COMBINER_SUM || combiner == ANNC_COMBINER_MEAN,
+               "combiner must be 0 or 1");
+  if (batch == 0) return set_error(ANNC_OK, "");
+  ANNC_REQUIRE(data && out && (n == 0 || (indices && seg_ids)), "null pointer");
+  int rc = segment_reduce(static_cast<hipStream_t>(stream), data, rows, dim, indices,
+                          indices_is_64, seg_ids, seg_stride, n, combiner, batch, out, 0);
+  return rc == ANNC_OK ? set_error(ANNC_OK, "") : rc;
+}
+
+int annc_hip_sparse_embedding2(void* stream, const float* table, int64_t rows, int64_t dim,
+                               const void* ids, int ids_is_64, int64_t n, int64_t fallback_row,
+                               float* out) {
+  using namespace annc;
+  ANNC_REQUIRE(rows >= 1 && dim >= 1 && n >= 0, "bad dimensions");
+  ANNC_REQUIRE(fallback_row >= 0 && fallback_row < rows, "fallback row out of range");
+  if (n == 0) return set_error(ANNC_OK, "");
+  ANNC_REQUIRE(table && ids && out, "null pointer");
+  int rc = launch_sparse_embedding2(static_cast<hipStream_t>(stream), table, rows, dim, ids,
+                                    ids_is_64, n, fallback_row, out);
+  return rc == ANNC_OK ? set_error(ANNC_OK, "") : rc;
+}
+
+int annc_hip_pooling(void* stream, const int64_t* ids, const float* gathered, int64_t m,
+                     int64_t k, int64_t n, const int64_t* slice_starts3,
+                     const int64_t* slice_limits3, float* out) {
+  using namespace annc;
+  ANNC_REQUIRE(m >= 0 && k >= 0 && n >= 0, "bad dimensions");
+  ANNC_REQUIRE(slice_starts3 && slice_limits3, "null slice bounds");
+  if (m * n == 0) return set_error(ANNC_OK, "");
+  ANNC_REQUIRE(ids && gathered && out, "null pointer");
+  int rc = launch_pooling(static_cast<hipStream_t>(stream), ids, gathered, m, k, n, slice_starts3,
+                          slice_limits3, out);
+  return rc == ANNC_OK ? set_error(ANNC_OK, "") : rc;
+}
+
+}  // extern "C"

@@ -1,0 +1,62 @@
+// embedding_impl.h -- internal launchers shared by the embedding, hashing
+// and TF-op entry points.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace annc {
+
+struct BagArgs {
+  const float* table;
+  int64_t rows;
+  int64_t dim;
+  const void* ids;
+  int ids_is_64;
+  const int64_t* offsets;
+  const int32_t* perm;  // optional: row id of position j is ids[perm[j]]
+  int64_t num_bags;
+  int combiner;
+  float* out;
+  int64_t ldo;
+  int* status;
+};
+
+// CSR bag reduction (sum or mean) in index order.
+int launch_bag(const BagArgs& a, hipStream_t s);
+
+// Min, max and sortedness of seg[i*stride], i < n (synchronises `s`).
+int segment_scan(hipStream_t s, const int64_t* seg, int64_t stride, int64_t n, int64_t* min_out,
+                 int64_t* max_out, bool* sorted);
+
+// out[batch, dim] = segment reduction of data rows; segment ids must lie in
+// [0, batch).  sorted_hint = 1 when the ids are known to be non-decreasing.
+int segment_reduce(hipStream_t s, const float* data, int64_t rows, int64_t dim,
+                   const void* indices, int indices_is_64, const int64_t* seg, int64_t stride,
+                   int64_t n, int combiner, int64_t batch, float* out, int sorted_hint);
+
+int launch_sparse_embedding2(hipStream_t s, const float* table, int64_t rows, int64_t dim,
+                             const void* ids, int ids_is_64, int64_t n, int64_t fallback,
+                             float* out);
+
+int launch_pooling(hipStream_t s, const int64_t* ids, const float* gathered, int64_t m, int64_t k,
+                   int64_t n, const int64_t* ss, const int64_t* sl, float* out);
+
+// Hash-bucket helpers (hash.hip).
+struct StringsArgs {
+  const char* bytes;
+  const int64_t* offsets;
+  int64_t n;
+};
+// Unsigned 64-bit division by an invariant divisor (round-up method of
+// Granlund & Montgomery, "Division by invariant integers using
+// multiplication", PLDI 1994, fig. 4.1).
+struct U64Divisor {
+  uint64_t d;
+  uint64_t magic;
+  int shift;  // l - 1; d == 1 uses shift = -1
+};
+U64Divisor make_divisor(uint64_t d);
+
+}  // namespace annc

@@ -1,0 +1,428 @@
+// gemm.hip -- fp32 GEMM on CDNA4 matrix cores (gfx950).
+//
+// Engine behind the XLA custom calls __matmul, __matmul_add,
+// __matmul_add_relu, __batch_matmul and __layout_matmul
+// (annc/service/cpu/gemm_rewriter.cc:136-281), which the reference runs as
+// OpenBLAS / kpgemm sgemm calls followed by scalar epilogue loops.
+//
+// Design (one 256-thread workgroup = 4 wave64 per output tile):
+//   * v_mfma_f32_32x32x2f32: each wave owns BLK_M x BLK_N 32x32 accumulator
+//     blocks (16 fp32 per lane each).
+//   * A tiles [BM x 32] are staged through LDS, double buffered, rows padded
+//     to 36 floats so the 16-byte fragment reads are bank-conflict free.
+//     Each lane half h (lanes 0-31 / 32-63) consumes k = 16h .. 16h+15 of a
+//     32-wide k block, so one ds_read_b128 feeds 4 MFMA steps.
+//   * Row-major B tiles [32 x BN] are staged through LDS (double buffered)
+//     and read one float per lane per step.  layout_matmul-packed B skips
+//     LDS: each wave loads its fragments straight from global memory, one
+//     coalesced 16-byte load per lane per 4 steps, prefetched a block ahead.
+//   * Epilogue fuses the addend matrix (__matmul_add*), a bias vector,
+//     ReLU (std::max(x, 0.f) semantics) or sigmoid before the single store.
+//   * Tiles are numbered so that each XCD (workgroup id mod 8) receives a
+//     contiguous run of tiles sharing A rows, keeping them in its own L2.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+
+#include "common.h"
+#include "layout_pack.h"
+
+namespace annc {
+namespace {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kBK = 32;          // k block
+constexpr int kALd = kBK + 4;    // padded LDS row of the A tile (floats)
+constexpr int kThreads = 256;
+
+struct GemmParams {
+  const float* a;
+  const float* b;
+  const float* e;
+  const float* bias;
+  float* c;
+  int64_t lda, ldb, lde, ldc;
+  int64_t stride_a, stride_b, stride_e, stride_c;
+  int m, n, k;
+  int tiles_m, tiles_n;
+  int epilogue;
+  int a_vec;  // A rows can be read as aligned float4
+  int b_vec;  // row-major B rows can be read as aligned float4
+};
+
+__device__ __forceinline__ float apply_epilogue(float v, int epilogue) {
+  if (epilogue & ANNC_EPI_RELU) v = (v < 0.0f) ? 0.0f : v;
+  if (epilogue & ANNC_EPI_SIGMOID) v = 1.0f / (1.0f + expf(-v));
+  return v;
+}
+
+template <int WAVES_M, int WAVES_N, int BLK_M, int BLK_N, bool PACKED>
+__global__ __launch_bounds__(kThreads) void gemm_mfma_kernel(GemmParams p) {
+  constexpr int BM = WAVES_M * BLK_M * 32;
+  constexpr int BN = WAVES_N * BLK_N * 32;
+  constexpr int A_CHUNKS = BM * kBK / 4 / kThreads;  // float4 per thread per A block
+  constexpr int B_CHUNKS = kBK * BN / 4 / kThreads;  // float4 per thread per B block
+  static_assert(WAVES_M * WAVES_N * 64 == kThreads, "4 waves per workgroup");
+  static_assert(A_CHUNKS >= 1 && B_CHUNKS >= 1, "tile too small");
+
+  __shared__ __attribute__((aligned(16))) float As[2][BM * kALd];
+  __shared__ __attribute__((aligned(16))) float Bs[PACKED ? 1 : 2][PACKED ? 4 : kBK * BN];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave / WAVES_N;
+  const int wn = wave % WAVES_N;
+  const int half = lane >> 5;   // which 16-wide k half this lane feeds
+  const int l32 = lane & 31;
+
+  // XCD-aware tile order: workgroup i runs on XCD i % 8.
+  int tile = blockIdx.x;
+  const int T = p.tiles_m * p.tiles_n;
+  if ((T & 7) == 0) tile = (tile & 7) * (T >> 3) + (tile >> 3);
+  const int m0 = (tile / p.tiles_n) * BM;
+  const int n0 = (tile % p.tiles_n) * BN;
+
+  const int64_t z = blockIdx.z;
+  const float* __restrict__ A = p.a + z * p.stride_a;
+  const float* __restrict__ B = p.b + z * p.stride_b;
+  const int M = p.m, N = p.n, K = p.k;
+  const int KT = (K + kBK - 1) / kBK;
+
+  // ---- global -> register loaders ----
+  f32x4 a_reg[A_CHUNKS];
+  auto load_a = [&](int kt) {
+#pragma unroll
+    for (int c = 0; c < A_CHUNKS; ++c) {
+      const int lin = tid + kThreads * c;
+      const int row = lin >> 3;
+      const int col = (lin & 7) * 4;
+      const int gm = m0 + row;
+      const int gk = kt * kBK + col;
+      if (gm < M && p.a_vec && gk + 3 < K) {
+        a_reg[c] = *reinterpret_cast<const f32x4*>(A + (int64_t)gm * p.lda + gk);
+      } else {
+        f32x4 v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          v[e] = (gm < M && gk + e < K) ? A[(int64_t)gm * p.lda + gk + e] : 0.0f;
+        a_reg[c] = v;
+      }
+    }
+  };
+  auto store_a = [&](int buf) {
+#pragma unroll
+    for (int c = 0; c < A_CHUNKS; ++c) {
+      const int lin = tid + kThreads * c;
+      const int row = lin >> 3;
+      const int col = (lin & 7) * 4;
+      *reinterpret_cast<f32x4*>(&As[buf][row * kALd + col]) = a_reg[c];
+    }
+  };
+
+  f32x4 b_reg[PACKED ? 1 : B_CHUNKS];
+  auto load_b = [&](int kt) {
+#pragma unroll
+    for (int c = 0; c < B_CHUNKS; ++c) {
+      const int lin = tid + kThreads * c;
+      const int row = lin / (BN / 4);
+      const int col = (lin % (BN / 4)) * 4;
+      const int gk = kt * kBK + row;
+      const int gn = n0 + col;
+      if (gk < K && p.b_vec && gn + 3 < N) {
+        b_reg[c] = *reinterpret_cast<const f32x4*>(B + (int64_t)gk * p.ldb + gn);
+      } else {
+        f32x4 v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          v[e] = (gk < K && gn + e < N) ? B[(int64_t)gk * p.ldb + gn + e] : 0.0f;
+        b_reg[c] = v;
+      }
+    }
+  };
+  auto store_b = [&](int buf) {
+#pragma unroll
+    for (int c = 0; c < B_CHUNKS; ++c) {
+      const int lin = tid + kThreads * c;
+      const int row = lin / (BN / 4);
+      const int col = (lin % (BN / 4)) * 4;
+      *reinterpret_cast<f32x4*>(&Bs[buf][row * BN + col]) = b_reg[c];
+    }
+  };
+
+  // Packed B: fragments straight from global memory.
+  const int kf = K & ~31;
+  const int nf = N & ~31;
+  f32x4 bp_cur[PACKED ? BLK_N : 1][4];
+  f32x4 bp_nxt[PACKED ? BLK_N : 1][4];
+  auto load_bp = [&](int kt, f32x4 (&dst)[PACKED ? BLK_N : 1][4]) {
+#pragma unroll
+    for (int bn = 0; bn < (PACKED ? BLK_N : 1); ++bn) {
+      const int pn = (n0 >> 5) + wn * BLK_N + bn;
+      const bool full = (kt * kBK + kBK <= kf) && ((pn + 1) * 32 <= nf);
+      if (full) {
+        const f32x4* src = reinterpret_cast<const f32x4*>(
+            B + ((int64_t)pn * (kf >> 5) + kt) * 1024 + lane * 4);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) dst[bn][q] = src[q * 64];
+      } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          f32x4 v;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int gk = kt * kBK + 16 * half + 4 * q + e;
+            const int gn = pn * 32 + l32;
+            v[e] = (gk < K && gn < N) ? B[layout_pack_offset(gk, gn, K, N)] : 0.0f;
+          }
+          dst[bn][q] = v;
+        }
+      }
+    }
+  };
+
+  f32x16 acc[BLK_M][BLK_N];
+#pragma unroll
+  for (int i = 0; i < BLK_M; ++i)
+#pragma unroll
+    for (int j = 0; j < BLK_N; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  auto compute = [&](int buf) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      f32x4 af[BLK_M];
+      f32x4 bf[BLK_N];
+#pragma unroll
+      for (int i = 0; i < BLK_M; ++i) {
+        const int row = wm * BLK_M * 32 + i * 32 + l32;
+        af[i] = *reinterpret_cast<const f32x4*>(&As[buf][row * kALd + 16 * half + 4 * q]);
+      }
+#pragma unroll
+      for (int j = 0; j < BLK_N; ++j) {
+        if constexpr (PACKED) {
+          bf[j] = bp_cur[j][q];
+        } else {
+          const int col = wn * BLK_N * 32 + j * 32 + l32;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) bf[j][e] = Bs[buf][(16 * half + 4 * q + e) * BN + col];
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+#pragma unroll
+        for (int i = 0; i < BLK_M; ++i)
+#pragma unroll
+          for (int j = 0; j < BLK_N; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i][e], bf[j][e], acc[i][j], 0, 0, 0);
+    }
+  };
+
+  // ---- main loop: one barrier per k block ----
+  load_a(0);
+  if constexpr (PACKED) load_bp(0, bp_cur); else load_b(0);
+  store_a(0);
+  if constexpr (!PACKED) store_b(0);
+  __syncthreads();
+
+  for (int kt = 0; kt < KT; ++kt) {
+    const int cur = kt & 1;
+    const bool more = kt + 1 < KT;
+    if (more) {
+      load_a(kt + 1);
+      if constexpr (PACKED) load_bp(kt + 1, bp_nxt); else load_b(kt + 1);
+    }
+    compute(cur);
+    if (more) {
+      store_a(cur ^ 1);
+      if constexpr (PACKED) {
+#pragma unroll
+        for (int j = 0; j < BLK_N; ++j)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) bp_cur[j][q] = bp_nxt[j][q];
+      } else {
+        store_b(cur ^ 1);
+      }
+    }
+    __syncthreads();
+  }
+
+  // ---- fused epilogue ----
+  const float* __restrict__ E = p.e ? p.e + z * p.stride_e : nullptr;
+  float* __restrict__ C = p.c + z * p.stride_c;
+#pragma unroll
+  for (int i = 0; i < BLK_M; ++i) {
+#pragma unroll
+    for (int j = 0; j < BLK_N; ++j) {
+      const int col = n0 + wn * BLK_N * 32 + j * 32 + l32;
+      if (col >= N) continue;
+      const float bias = p.bias ? p.bias[col] : 0.0f;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = m0 + wm * BLK_M * 32 + i * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+        if (row >= M) continue;
+        float v = acc[i][j][r];
+        if (E) v += E[(int64_t)row * p.lde + col];
+        if (p.bias) v += bias;
+        C[(int64_t)row * p.ldc + col] = apply_epilogue(v, p.epilogue);
+      }
+    }
+  }
+}
+
+// Skinny-N path (N <= 4): one wave per output row, lanes stride over k.
+// For N < 32 the packed layout is row-major (region 3), so both forms share it.
+__global__ __launch_bounds__(kThreads) void gemv_kernel(GemmParams p) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+  const int64_t z = blockIdx.z;
+  if (row >= p.m) return;
+  const float* __restrict__ A = p.a + z * p.stride_a + row * p.lda;
+  const float* __restrict__ B = p.b + z * p.stride_b;
+  float part[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  const int N = p.n, K = p.k;
+  int kk = lane * 4;
+  if (p.a_vec) {
+    for (; kk + 3 < K; kk += 256) {
+      const f32x4 av = *reinterpret_cast<const f32x4*>(A + kk);
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          if (j < N) part[j] += av[e] * B[(int64_t)(kk + e) * p.ldb + j];
+    }
+  }
+  for (; kk < K; kk += 256) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      if (kk + e < K) {
+        const float av = A[kk + e];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          if (j < N) part[j] += av * B[(int64_t)(kk + e) * p.ldb + j];
+      }
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) part[j] += __shfl_xor(part[j], off, 64);
+  }
+  if (lane < N) {
+    float v = part[0];
+#pragma unroll
+    for (int j = 1; j < 4; ++j)
+      if (lane == j) v = part[j];
+    if (p.e) v += p.e[z * p.stride_e + row * p.lde + lane];
+    if (p.bias) v += p.bias[lane];
+    p.c[z * p.stride_c + row * p.ldc + lane] = apply_epilogue(v, p.epilogue);
+  }
+}
+
+__global__ void pack_rhs_kernel(const float* __restrict__ src, float* __restrict__ dst, int64_t K,
+                                int64_t N) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= K * N) return;
+  const int64_t k = i / N, n = i % N;
+  dst[layout_pack_offset(k, n, K, N)] = src[i];
+}
+
+template <int WM, int WN, int BMB, int BNB, bool PACKED>
+int launch_tile(const GemmParams& p0, int64_t batch, hipStream_t stream) {
+  constexpr int BM = WM * BMB * 32, BN = WN * BNB * 32;
+  GemmParams p = p0;
+  p.tiles_m = (p.m + BM - 1) / BM;
+  p.tiles_n = (p.n + BN - 1) / BN;
+  dim3 grid(p.tiles_m * p.tiles_n, 1, (unsigned)batch);
+  hipLaunchKernelGGL((gemm_mfma_kernel<WM, WN, BMB, BNB, PACKED>), grid, dim3(kThreads), 0,
+                     stream, p);
+  ANNC_HIP_TRY(hipGetLastError());
+  return ANNC_OK;
+}
+
+template <bool PACKED>
+int launch_gemm(const GemmParams& p, int64_t batch, hipStream_t stream) {
+  // Largest tile that still gives every CU a workgroup (256 CUs on MI355X).
+  const int64_t cus = 256;
+  auto tiles = [&](int bm, int bn) {
+    return ((int64_t)(p.m + bm - 1) / bm) * ((p.n + bn - 1) / bn) * batch;
+  };
+  if (tiles(128, 128) >= cus) return launch_tile<2, 2, 2, 2, PACKED>(p, batch, stream);
+  if (tiles(64, 128) >= cus) return launch_tile<2, 2, 1, 2, PACKED>(p, batch, stream);
+  return launch_tile<2, 2, 1, 1, PACKED>(p, batch, stream);
+}
+
+}  // namespace
+}  // namespace annc
+
+extern "C" {
+
+int annc_hip_gemm(void* stream, int64_t batch, int64_t m, int64_t n, int64_t k, const float* a,
+                  int64_t lda, int64_t stride_a, const float* b, int64_t ldb, int64_t stride_b,
+                  int b_packed, const float* addend, int64_t lde, int64_t stride_e,
+                  const float* bias, int epilogue, float* c, int64_t ldc, int64_t stride_c) {
+  using namespace annc;
+  ANNC_REQUIRE(batch >= 0 && m >= 0 && n >= 0 && k >= 0, "negative GEMM dimension");
+  ANNC_REQUIRE(m < (1ll << 31) && n < (1ll << 31) && k < (1ll << 31) && batch < 65536,
+               "GEMM dimension too large");
+  if (batch == 0 || m == 0 || n == 0) return set_error(ANNC_OK, "");
+  ANNC_REQUIRE(c != nullptr, "null output");
+  ANNC_REQUIRE(k == 0 || (a != nullptr && b != nullptr), "null operand");
+  ANNC_REQUIRE(b_packed || ldb >= n, "ldb < n");
+  ANNC_REQUIRE(lda >= k && ldc >= n, "leading dimension too small");
+  ANNC_REQUIRE(addend == nullptr || lde >= n, "lde < n");
+  ANNC_REQUIRE((epilogue & ~(ANNC_EPI_RELU | ANNC_EPI_SIGMOID)) == 0, "unknown epilogue bits");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+
+  GemmParams p{};
+  p.a = a;
+  p.b = b;
+  p.e = addend;
+  p.bias = bias;
+  p.c = c;
+  p.lda = lda;
+  p.ldb = b_packed ? n : ldb;  // packed with N < 32 is row-major [K, N]
+  p.lde = lde;
+  p.ldc = ldc;
+  p.stride_a = stride_a;
+  p.stride_b = stride_b;
+  p.stride_e = stride_e;
+  p.stride_c = stride_c;
+  p.m = (int)m;
+  p.n = (int)n;
+  p.k = (int)k;
+  p.epilogue = epilogue;
+  auto aligned16 = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
+  p.a_vec = (lda % 4 == 0) && (stride_a % 4 == 0) && aligned16(a);
+  p.b_vec = (ldb % 4 == 0) && (stride_b % 4 == 0) && aligned16(b);
+
+  if (n <= 4) {
+    dim3 grid((unsigned)ceil_div(m, kThreads / 64), 1, (unsigned)batch);
+    hipLaunchKernelGGL(gemv_kernel, grid, dim3(kThreads), 0, s, p);
+    ANNC_HIP_TRY(hipGetLastError());
+    return set_error(ANNC_OK, "");
+  }
+  if (b_packed) {
+    ANNC_REQUIRE(aligned16(b) && stride_b % 4 == 0, "packed B must be 16-byte aligned");
+    return launch_gemm<true>(p, batch, s);
+  }
+  return launch_gemm<false>(p, batch, s);
+}
+
+int annc_hip_layout_matmul_pack_rhs(void* stream, int64_t k, int64_t n, const float* src,
+                                    float* dst) {
+  using namespace annc;
+  ANNC_REQUIRE(k >= 0 && n >= 0, "negative dimension");
+  ANNC_REQUIRE(src != nullptr && dst != nullptr && src != dst, "bad pointers");
+  const int64_t total = k * n;
+  if (total == 0) return set_error(ANNC_OK, "");
+  hipLaunchKernelGGL(pack_rhs_kernel, dim3((unsigned)ceil_div(total, 256)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), src, dst, k, n);
+  ANNC_HIP_TRY(hipGetLastError());
+  return set_error(ANNC_OK, "");
+}
+
+}  // extern "C"

@@ -1,0 +1,568 @@
+// hash.hip -- FarmHash Fingerprint64 on gfx950 and the hash-bucket embedding
+// ops built on it.
+//
+// Fingerprint64 is farmhashna::Hash64 from google/farmhash (the
+// @farmhash_archive TensorFlow 2.15 links), which ANNC reaches through
+// util::Fingerprint64 / tensorflow::Fingerprint64
+// (python/tensorflow/kernels/fused_embedding_with_hash_bucket.cc:63,
+//  fused_dnn_embedding_with_hash_bucket.cc:30, fused_sparse_embedding.cc:36).
+// Two device formulations:
+//   * fp64_bytes: any string in global memory (byte loads; all length
+//     branches including the 64-byte block loop);
+//   * fp64_decimal: the decimal text of an int64 (AsString semantics, the
+//     op pattern replaced at python/annc/optimize/rec_embedding.py:549-557)
+//     built directly in three 64-bit registers -- at most 20 bytes, so only
+//     the 0-16 and 17-32 byte branches exist -- with no memory traffic.
+// CDNA has no 64x64-bit multiplier; the 64-bit products compile to 32-bit
+// v_mul_lo/v_mul_hi sequences, and `% num_buckets` uses a precomputed
+// invariant-divisor reciprocal instead of a 64-bit division loop.
+#include <hip/hip_runtime.h>
+#include <hipcub/hipcub.hpp>
+
+#include <algorithm>
+
+#include "common.h"
+#include "embedding_impl.h"
+
+namespace annc {
+
+U64Divisor make_divisor(uint64_t d) {
+  U64Divisor r{d, 0, -1};
+  if (d <= 1) return r;
+  const int l = 64 - __builtin_clzll(d - 1);  // ceil(log2 d), 1..64
+  const uint64_t two_l_minus_d = (l == 64 ? 0ull : (1ull << l)) - d;  // mod 2^64
+  const unsigned __int128 num = static_cast<unsigned __int128>(two_l_minus_d) << 64;
+  r.magic = static_cast<uint64_t>(num / d) + 1;
+  r.shift = l - 1;
+  return r;
+}
+
+namespace {
+
+constexpr uint64_t kC0 = 0xc3a5c85c97cb3127ULL;
+constexpr uint64_t kC1 = 0xb492b66fbe98f273ULL;
+constexpr uint64_t kC2 = 0x9ae16a3b2f90404fULL;
+constexpr int kThreads = 256;
+constexpr int kMaxFields = 64;
+
+__device__ __forceinline__ uint64_t rotr(uint64_t v, int s) { return (v >> s) | (v << (64 - s)); }
+__device__ __forceinline__ uint64_t smix(uint64_t v) { return v ^ (v >> 47); }
+
+__device__ __forceinline__ uint64_t mix16(uint64_t u, uint64_t v, uint64_t mul) {
+  uint64_t a = (u ^ v) * mul;
+  a ^= a >> 47;
+  uint64_t b = (v ^ a) * mul;
+  b ^= b >> 47;
+  return b * mul;
+}
+
+__device__ __forceinline__ uint64_t mod_invariant(uint64_t n, const U64Divisor& dv) {
+  if (dv.shift < 0) return 0;  // d == 1
+  const uint64_t t1 = __umul64hi(dv.magic, n);
+  const uint64_t q = (t1 + ((n - t1) >> 1)) >> dv.shift;
+  return n - q * dv.d;
+}
+
+// ---------------------------------------------------------------------------
+// Strings in memory.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint64_t le64(const unsigned char* p) {
+  uint64_t r = 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) r |= static_cast<uint64_t>(p[i]) << (8 * i);
+  return r;
+}
+__device__ __forceinline__ uint64_t le32(const unsigned char* p) {
+  uint64_t r = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) r |= static_cast<uint64_t>(p[i]) << (8 * i);
+  return r;
+}
+
+struct Pair {
+  uint64_t x, y;
+};
+
+__device__ __forceinline__ Pair weak_seeds(const unsigned char* s, uint64_t a, uint64_t b) {
+  const uint64_t w = le64(s), x = le64(s + 8), y = le64(s + 16), z = le64(s + 24);
+  a += w;
+  b = rotr(b + a + z, 21);
+  const uint64_t c = a;
+  a += x;
+  a += y;
+  b += rotr(a, 44);
+  return Pair{a + z, b + c};
+}
+
+__device__ uint64_t fp64_bytes(const unsigned char* s, uint64_t len) {
+  if (len <= 16) {
+    if (len >= 8) {
+      const uint64_t mul = kC2 + len * 2;
+      const uint64_t a = le64(s) + kC2;
+      const uint64_t b = le64(s + len - 8);
+      return mix16(rotr(b, 37) * mul + a, (rotr(a, 25) + b) * mul, mul);
+    }
+    if (len >= 4) {
+      const uint64_t mul = kC2 + len * 2;
+      return mix16(len + (le32(s) << 3), le32(s + len - 4), mul);
+    }
+    if (len > 0) {
+      const uint32_t y = static_cast<uint32_t>(s[0]) + (static_cast<uint32_t>(s[len >> 1]) << 8);
+      const uint32_t z = static_cast<uint32_t>(len) + (static_cast<uint32_t>(s[len - 1]) << 2);
+      return smix(y * kC2 ^ z * kC0) * kC2;
+    }
+    return kC2;
+  }
+  if (len <= 32) {
+    const uint64_t mul = kC2 + len * 2;
+    const uint64_t a = le64(s) * kC1;
+    const uint64_t b = le64(s + 8);
+    const uint64_t c = le64(s + len - 8) * mul;
+    const uint64_t d = le64(s + len - 16) * kC2;
+    return mix16(rotr(a + b, 43) + rotr(c, 30) + d, a + rotr(b + kC2, 18) + c, mul);
+  }
+  if (len <= 64) {
+    const uint64_t mul = kC2 + len * 2;
+    const uint64_t a = le64(s) * kC2;
+    const uint64_t b = le64(s + 8);
+    const uint64_t c = le64(s + len - 8) * mul;
+    const uint64_t d = le64(s + len - 16) * kC2;
+    const uint64_t y = rotr(a + b, 43) + rotr(c, 30) + d;
+    const uint64_t z = mix16(y, a + rotr(b + kC2, 18) + c, mul);
+    const uint64_t e = le64(s + 16) * mul;
+    const uint64_t f = le64(s + 24);
+    const uint64_t g = (y + le64(s + len - 32)) * mul;
+    const uint64_t h = (z + le64(s + len - 24)) * mul;
+    return mix16(rotr(e + f, 43) + rotr(g, 30) + h, e + rotr(f + a, 18) + g, mul);
+  }
+  const uint64_t seed = 81;
+  uint64_t x = seed;
+  uint64_t y = seed * kC1 + 113;
+  uint64_t z = smix(y * kC2 + 113) * kC2;
+  Pair v{0, 0}, w{0, 0};
+  x = x * kC2 + le64(s);
+  const unsigned char* end = s + ((len - 1) / 64) * 64;
+  const unsigned char* last64 = end + ((len - 1) & 63) - 63;
+  do {
+    x = rotr(x + y + v.x + le64(s + 8), 37) * kC1;
+    y = rotr(y + v.y + le64(s + 48), 42) * kC1;
+    x ^= w.y;
+    y += v.x + le64(s + 40);
+    z = rotr(z + w.x, 33) * kC1;
+    v = weak_seeds(s, v.y * kC1, x + w.x);
+    w = weak_seeds(s + 32, z + w.y, y + le64(s + 16));
+    const uint64_t t = z;
+    z = x;
+    x = t;
+    s += 64;
+  } while (s != end);
+  const uint64_t mul = kC1 + ((z & 0xff) << 1);
+  s = last64;
+  w.x += ((len - 1) & 63);
+  v.x += w.x;
+  w.x += v.x;
+  x = rotr(x + y + v.x + le64(s + 8), 37) * mul;
+  y = rotr(y + v.y + le64(s + 48), 42) * mul;
+  x ^= w.y * 9;
+  y += v.x * 9 + le64(s + 40);
+  z = rotr(z + w.x, 33) * mul;
+  v = weak_seeds(s, v.y * mul, x + w.x);
+  w = weak_seeds(s + 32, z + w.y, y + le64(s + 16));
+  return mix16(mix16(v.x, w.x, mul) + smix(y) * kC0 + x, mix16(v.y, w.y, mul) + z, mul);
+}
+
+// ---------------------------------------------------------------------------
+// Decimal text of an int64 held in registers.
+// ---------------------------------------------------------------------------
+struct Text24 {
+  uint64_t w0, w1, w2;  // little-endian bytes: w0 holds characters 0..7
+  uint32_t len;
+};
+
+// x < 10^width rendered as `width` ASCII digits, first digit in byte 0.
+template <int WIDTH>
+__device__ __forceinline__ uint64_t ascii_digits(uint32_t x) {
+  uint64_t r = 0;
+#pragma unroll
+  for (int i = WIDTH - 1; i >= 0; --i) {
+    const uint32_t q = x / 10u;
+    r |= static_cast<uint64_t>(0x30u + (x - q * 10u)) << (8 * i);
+    x = q;
+  }
+  return r;
+}
+
+__device__ __forceinline__ uint32_t count_digits8(uint32_t x) {
+  return 1u + (x >= 10u) + (x >= 100u) + (x >= 1000u) + (x >= 10000u) + (x >= 100000u) +
+         (x >= 1000000u) + (x >= 10000000u);
+}
+
+__device__ __forceinline__ Text24 int64_text(int64_t v) {
+  const bool neg = v < 0;
+  const uint64_t u = neg ? (0ull - static_cast<uint64_t>(v)) : static_cast<uint64_t>(v);
+  const uint64_t q1 = u / 100000000ull;
+  const uint32_t lo = static_cast<uint32_t>(u - q1 * 100000000ull);
+  const uint64_t q2 = q1 / 100000000ull;
+  const uint32_t mid = static_cast<uint32_t>(q1 - q2 * 100000000ull);
+  const uint32_t hi = static_cast<uint32_t>(q2);  // <= 922
+  uint32_t nd;
+  if (hi)
+    nd = 16u + 1u + (hi >= 10u) + (hi >= 100u);
+  else if (mid)
+    nd = 8u + count_digits8(mid);
+  else
+    nd = count_digits8(lo);
+  // 19 zero-padded characters: hi(3) mid(8) lo(8).
+  const uint64_t d3 = ascii_digits<3>(hi);
+  const uint64_t m8 = ascii_digits<8>(mid);
+  const uint64_t l8 = ascii_digits<8>(lo);
+  const uint64_t p0 = d3 | (m8 << 24);
+  const uint64_t p1 = (m8 >> 40) | (l8 << 24);
+  const uint64_t p2 = l8 >> 40;
+  // Drop the 19 - nd leading zeros: 192-bit right shift by 8*(19-nd) bits.
+  const uint32_t bits = 8u * (19u - nd);
+  const uint32_t q = bits >> 6, r = bits & 63u;
+  const uint64_t x0 = q == 0 ? p0 : (q == 1 ? p1 : p2);
+  const uint64_t x1 = q == 0 ? p1 : (q == 1 ? p2 : 0ull);
+  const uint64_t x2 = q == 0 ? p2 : 0ull;
+  Text24 t;
+  t.w0 = r ? (x0 >> r) | (x1 << (64 - r)) : x0;
+  t.w1 = r ? (x1 >> r) | (x2 << (64 - r)) : x1;
+  t.w2 = x2 >> r;
+  t.len = nd;
+  if (neg) {
+    t.w2 = (t.w2 << 8) | (t.w1 >> 56);
+    t.w1 = (t.w1 << 8) | (t.w0 >> 56);
+    t.w0 = (t.w0 << 8) | 0x2Dull;  // '-'
+    t.len = nd + 1;
+  }
+  return t;
+}
+
+// Eight bytes of the text starting at byte offset o (0 <= o <= 16); bytes
+// past the text read as zero.
+__device__ __forceinline__ uint64_t text_fetch64(const Text24& t, uint32_t o) {
+  const uint32_t q = o >> 3, r = (o & 7u) * 8u;
+  const uint64_t a = q == 0 ? t.w0 : (q == 1 ? t.w1 : t.w2);
+  const uint64_t b = q == 0 ? t.w1 : (q == 1 ? t.w2 : 0ull);
+  return r ? (a >> r) | (b << (64 - r)) : a;
+}
+
+__device__ __forceinline__ uint64_t fp64_text(const Text24& t) {
+  const uint64_t len = t.len;  // 1..20
+  if (len <= 16) {
+    if (len >= 8) {
+      const uint64_t mul = kC2 + len * 2;
+      const uint64_t a = text_fetch64(t, 0) + kC2;
+      const uint64_t b = text_fetch64(t, (uint32_t)len - 8);
+      return mix16(rotr(b, 37) * mul + a, (rotr(a, 25) + b) * mul, mul);
+    }
+    if (len >= 4) {
+      const uint64_t mul = kC2 + len * 2;
+      const uint64_t a = t.w0 & 0xffffffffull;
+      const uint64_t b = text_fetch64(t, (uint32_t)len - 4) & 0xffffffffull;
+      return mix16(len + (a << 3), b, mul);
+    }
+    const uint32_t c0 = static_cast<uint32_t>(t.w0 & 0xff);
+    const uint32_t cm = static_cast<uint32_t>((t.w0 >> (8 * (len >> 1))) & 0xff);
+    const uint32_t cl = static_cast<uint32_t>((t.w0 >> (8 * (len - 1))) & 0xff);
+    const uint32_t y = c0 + (cm << 8);
+    const uint32_t z = static_cast<uint32_t>(len) + (cl << 2);
+    return smix(y * kC2 ^ z * kC0) * kC2;
+  }
+  const uint64_t mul = kC2 + len * 2;
+  const uint64_t a = t.w0 * kC1;
+  const uint64_t b = t.w1;
+  const uint64_t c = text_fetch64(t, (uint32_t)len - 8) * mul;
+  const uint64_t d = text_fetch64(t, (uint32_t)len - 16) * kC2;
+  return mix16(rotr(a + b, 43) + rotr(c, 30) + d, a + rotr(b + kC2, 18) + c, mul);
+}
+
+// ---------------------------------------------------------------------------
+// Kernels
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint64_t string_len(const unsigned char* p, int64_t span, int nul) {
+  if (!nul) return static_cast<uint64_t>(span);
+  int64_t i = 0;
+  while (i < span && p[i] != 0) ++i;
+  return static_cast<uint64_t>(i);
+}
+
+__global__ __launch_bounds__(kThreads) void fingerprint_kernel(const char* __restrict__ bytes,
+                                                               const int64_t* __restrict__ offsets,
+                                                               int64_t n, int nul,
+                                                               uint64_t* __restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (i >= n) return;
+  const unsigned char* p = reinterpret_cast<const unsigned char*>(bytes) + offsets[i];
+  out[i] = fp64_bytes(p, string_len(p, offsets[i + 1] - offsets[i], nul));
+}
+
+// bucket of every string; empty strings (span 0) get `empty_value`.
+__global__ __launch_bounds__(kThreads) void bucket_strings_kernel(
+    const char* __restrict__ bytes, const int64_t* __restrict__ offsets, int64_t n, int nul,
+    U64Divisor dv, int64_t empty_value, int64_t* __restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (i >= n) return;
+  const int64_t span = offsets[i + 1] - offsets[i];
+  if (span == 0 && empty_value != 0) {
+    out[i] = empty_value;
+    return;
+  }
+  const unsigned char* p = reinterpret_cast<const unsigned char*>(bytes) + offsets[i];
+  out[i] = static_cast<int64_t>(mod_invariant(fp64_bytes(p, string_len(p, span, nul)), dv));
+}
+
+__global__ __launch_bounds__(kThreads) void bucket_int64_kernel(const int64_t* __restrict__ ids,
+                                                                int64_t n, U64Divisor dv,
+                                                                int64_t* __restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (i >= n) return;
+  out[i] = static_cast<int64_t>(mod_invariant(fp64_text(int64_text(ids[i])), dv));
+}
+
+// out[i,:] = table[bucket[i],:] (exact copy) or zeros when bucket[i] is
+// negative or >= rows.
+__global__ __launch_bounds__(kThreads) void gather_rows_kernel(const float* __restrict__ table,
+                                                               int64_t rows, int64_t dim,
+                                                               const int64_t* __restrict__ bucket,
+                                                               int64_t n, float* __restrict__ out) {
+  const int64_t t = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (t >= n * dim) return;
+  const int64_t i = t / dim, d = t % dim;
+  const int64_t b = bucket[i];
+  out[t] = (b >= 0 && b < rows) ? table[b * dim + d] : 0.0f;
+}
+
+struct FieldSet {
+  const float* table[kMaxFields];
+  U64Divisor div[kMaxFields];
+};
+
+// Fused multi-field hash -> bucket -> gather -> pool.  A bag is owned by a
+// group of G lanes (4 floats of the row each).  The group hashes up to G
+// ids at once (one per lane), then every lane walks the bag in index order,
+// taking each bucket from the lane that hashed it.
+template <int G, bool MEAN>
+__global__ __launch_bounds__(kThreads) void hashed_bags_kernel(
+    FieldSet fs, int64_t field0, int64_t nfields, int64_t batch, int64_t dim,
+    const int64_t* __restrict__ ids, const int64_t* __restrict__ offsets,
+    float* __restrict__ out, int64_t ldo, int64_t* __restrict__ buckets_out) {
+  typedef float f32x4 __attribute__((ext_vector_type(4)));
+  const int g = threadIdx.x & (G - 1);
+  const int64_t local = ((int64_t)blockIdx.x * kThreads + threadIdx.x) / G;
+  if (local >= nfields * batch) return;
+  const int64_t fl = local / batch;  // field within this launch
+  const int64_t b = local - fl * batch;
+  const int64_t bag = (field0 + fl) * batch + b;
+  const int64_t beg = offsets[bag];
+  const int64_t end = offsets[bag + 1];
+  const float* __restrict__ table = fs.table[fl];
+  const U64Divisor dv = fs.div[fl];
+  float* __restrict__ dst = out + b * ldo + (field0 + fl) * dim;
+  // Every lane of the group runs the same chunk and id loops (the shuffles
+  // read buckets from all G lanes); lanes past `dim` only skip the row math.
+  for (int64_t base = 0; base < dim; base += (int64_t)G * 4) {
+    const int64_t c = base + (int64_t)g * 4;
+    const bool active = c < dim;
+    f32x4 acc = f32x4(0.0f);
+    for (int64_t j0 = beg; j0 < end; j0 += G) {
+      int64_t mine = 0;
+      if (j0 + g < end) {
+        mine = static_cast<int64_t>(mod_invariant(fp64_text(int64_text(ids[j0 + g])), dv));
+        if (buckets_out && base == 0) buckets_out[j0 + g] = mine;
+      }
+      const int cnt = (int)((end - j0) < G ? (end - j0) : G);
+      for (int u = 0; u < cnt; ++u) {
+        const int64_t r = __shfl(mine, u, G);
+        if (active) acc += *reinterpret_cast<const f32x4*>(table + r * dim + c);
+      }
+    }
+    if (MEAN) {
+      const int32_t cnt = static_cast<int32_t>(end - beg);
+      if (cnt > 0) acc *= 1.0f / static_cast<float>(cnt);
+    }
+    if (active) *reinterpret_cast<f32x4*>(dst + c) = acc;
+  }
+}
+
+template <int G>
+void launch_hashed_g(const FieldSet& fs, int64_t f0, int64_t nf, int64_t batch, int64_t dim,
+                     const int64_t* ids, const int64_t* offsets, int combiner, float* out,
+                     int64_t ldo, int64_t* buckets_out, hipStream_t s) {
+  dim3 grid((unsigned)ceil_div(nf * batch * G, kThreads));
+  if (combiner == ANNC_COMBINER_MEAN)
+    hipLaunchKernelGGL((hashed_bags_kernel<G, true>), grid, dim3(kThreads), 0, s, fs, f0, nf,
+                       batch, dim, ids, offsets, out, ldo, buckets_out);
+  else
+    hipLaunchKernelGGL((hashed_bags_kernel<G, false>), grid, dim3(kThreads), 0, s, fs, f0, nf,
+                       batch, dim, ids, offsets, out, ldo, buckets_out);
+}
+
+// KPFusedSparseEmbedding support: keep[i] = empty || bucket > 0.
+__global__ void sparse_embedding_flags_kernel(const int64_t* __restrict__ offsets,
+                                              const int64_t* __restrict__ bucket, int64_t n,
+                                              int32_t* __restrict__ keep) {
+  const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (i >= n) return;
+  const bool empty = offsets[i + 1] == offsets[i];
+  keep[i] = (empty || bucket[i] > 0) ? 1 : 0;
+}
+
+__global__ void sparse_embedding_scatter_kernel(const int64_t* __restrict__ offsets,
+                                                const int64_t* __restrict__ bucket,
+                                                const int32_t* __restrict__ keep,
+                                                const int32_t* __restrict__ pos, int64_t n,
+                                                int64_t* __restrict__ indices,
+                                                int64_t* __restrict__ values,
+                                                uint8_t* __restrict__ empty) {
+  const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (i >= n) return;
+  indices[2 * i] = i;
+  indices[2 * i + 1] = 0;
+  if (keep[i]) {
+    const bool e = offsets[i + 1] == offsets[i];
+    values[pos[i]] = e ? 0 : bucket[i];
+    empty[pos[i]] = e ? 1 : 0;
+  }
+}
+
+}  // namespace
+
+// Internal launchers used by the TF-op entry points (tf_ops.cpp).
+int launch_bucket_strings(hipStream_t s, const char* bytes, const int64_t* offsets, int64_t n,
+                          int64_t num_buckets, int nul, int64_t empty_value, int64_t* out) {
+  if (n == 0) return ANNC_OK;
+  hipLaunchKernelGGL(bucket_strings_kernel, dim3((unsigned)ceil_div(n, kThreads)), dim3(kThreads),
+                     0, s, bytes, offsets, n, nul, make_divisor((uint64_t)num_buckets),
+                     empty_value, out);
+  ANNC_HIP_TRY(hipGetLastError());
+  return ANNC_OK;
+}
+
+int launch_gather_rows(hipStream_t s, const float* table, int64_t rows, int64_t dim,
+                       const int64_t* bucket, int64_t n, float* out) {
+  if (n * dim == 0) return ANNC_OK;
+  hipLaunchKernelGGL(gather_rows_kernel, dim3((unsigned)ceil_div(n * dim, kThreads)),
+                     dim3(kThreads), 0, s, table, rows, dim, bucket, n, out);
+  ANNC_HIP_TRY(hipGetLastError());
+  return ANNC_OK;
+}
+
+int run_sparse_embedding(hipStream_t s, const int64_t* offsets, const int64_t* bucket, int64_t n,
+                         int32_t* keep, int32_t* pos, int64_t* indices, int64_t* values,
+                         uint8_t* empty, int64_t* num_values) {
+  if (n == 0) {
+    *num_values = 0;
+    return ANNC_OK;
+  }
+  const dim3 grid((unsigned)ceil_div(n, kThreads));
+  hipLaunchKernelGGL(sparse_embedding_flags_kernel, grid, dim3(kThreads), 0, s, offsets, bucket, n,
+                     keep);
+  ANNC_HIP_TRY(hipGetLastError());
+  size_t temp_bytes = 0;
+  ANNC_HIP_TRY(hipcub::DeviceScan::ExclusiveSum(nullptr, temp_bytes, keep, pos, (int)n, s));
+  void* temp = stream_workspace(s, temp_bytes);
+  if (!temp) return set_error(ANNC_RESOURCE_EXHAUSTED, "workspace allocation failed");
+  ANNC_HIP_TRY(hipcub::DeviceScan::ExclusiveSum(temp, temp_bytes, keep, pos, (int)n, s));
+  hipLaunchKernelGGL(sparse_embedding_scatter_kernel, grid, dim3(kThreads), 0, s, offsets, bucket,
+                     keep, pos, n, indices, values, empty);
+  ANNC_HIP_TRY(hipGetLastError());
+  int32_t last[2];
+  ANNC_HIP_TRY(hipMemcpyAsync(&last[0], pos + n - 1, sizeof(int32_t), hipMemcpyDeviceToHost, s));
+  ANNC_HIP_TRY(hipMemcpyAsync(&last[1], keep + n - 1, sizeof(int32_t), hipMemcpyDeviceToHost, s));
+  ANNC_HIP_TRY(hipStreamSynchronize(s));
+  *num_values = (int64_t)last[0] + last[1];
+  return ANNC_OK;
+}
+
+}  // namespace annc
+
+extern "C" {
+
+int annc_hip_fingerprint64(void* stream, const char* bytes, const int64_t* offsets, int64_t n,
+                           int nul_terminated, uint64_t* out) {
+  using namespace annc;
+  ANNC_REQUIRE(n >= 0, "negative count");
+  if (n == 0) return set_error(ANNC_OK, "");
+  ANNC_REQUIRE(bytes && offsets && out, "null pointer");
+  hipLaunchKernelGGL(fingerprint_kernel, dim3((unsigned)ceil_div(n, kThreads)), dim3(kThreads), 0,
+                     static_cast<hipStream_t>(stream), bytes, offsets, n, nul_terminated, out);
+  ANNC_HIP_TRY(hipGetLastError());
+  return set_error(ANNC_OK, "");
+}
+
+int annc_hip_hash_bucket_strings(void* stream, const char* bytes, const int64_t* offsets,
+                                 int64_t n, int64_t num_buckets, int nul_terminated,
+                                 int64_t* buckets) {
+  using namespace annc;
+  ANNC_REQUIRE(n >= 0, "negative count");
+  ANNC_REQUIRE(num_buckets >= 1, "num_buckets must be >= 1");
+  if (n == 0) return set_error(ANNC_OK, "");
+  ANNC_REQUIRE(bytes && offsets && buckets, "null pointer");
+  int rc = launch_bucket_strings(static_cast<hipStream_t>(stream), bytes, offsets, n, num_buckets,
+                                 nul_terminated, 0, buckets);
+  return rc == ANNC_OK ? set_error(ANNC_OK, "") : rc;
+}
+
+int annc_hip_hash_bucket_int64(void* stream, const int64_t* ids, int64_t n, int64_t num_buckets,
+                               int64_t* buckets) {
+  using namespace annc;
+  ANNC_REQUIRE(n >= 0, "negative count");
+  ANNC_REQUIRE(num_buckets >= 1, "num_buckets must be >= 1");
+  if (n == 0) return set_error(ANNC_OK, "");
+  ANNC_REQUIRE(ids && buckets, "null pointer");
+  hipLaunchKernelGGL(bucket_int64_kernel, dim3((unsigned)ceil_div(n, kThreads)), dim3(kThreads), 0,
+                     static_cast<hipStream_t>(stream), ids, n,
+                     make_divisor(static_cast<uint64_t>(num_buckets)), buckets);
+  ANNC_HIP_TRY(hipGetLastError());
+  return set_error(ANNC_OK, "");
+}
+
+int annc_hip_hashed_embedding_bags(void* stream, int64_t num_fields, int64_t batch, int64_t dim,
+                                   const float* const* tables, const int64_t* table_rows,
+                                   const int64_t* num_buckets, const int64_t* ids,
+                                   const int64_t* offsets, int combiner, float* out, int64_t ldo,
+                                   int64_t* buckets_out) {
+  using namespace annc;
+  ANNC_REQUIRE(num_fields >= 0 && batch >= 0 && dim >= 1, "bad dimensions");
+  ANNC_REQUIRE(combiner == ANNC_COMBINER_SUM || combiner == ANNC_COMBINER_MEAN,
+               "combiner must be 0 or 1");
+  ANNC_REQUIRE(ldo >= num_fields * dim, "ldo < num_fields * dim");
+  if (num_fields == 0 || batch == 0) return set_error(ANNC_OK, "");
+  ANNC_REQUIRE(tables && table_rows && num_buckets && ids && offsets && out, "null pointer");
+  ANNC_REQUIRE(dim % 4 == 0 && ldo % 4 == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0,
+               "hashed bags need dim and ldo multiples of 4 and a 16-byte aligned output");
+  for (int64_t f = 0; f < num_fields; ++f) {
+    ANNC_REQUIRE(num_buckets[f] >= 1, "num_buckets must be >= 1 (field %lld)", (long long)f);
+    ANNC_REQUIRE(num_buckets[f] <= table_rows[f],
+                 "num_buckets %lld exceeds the %lld table rows of field %lld",
+                 (long long)num_buckets[f], (long long)table_rows[f], (long long)f);
+    ANNC_REQUIRE(tables[f] && (reinterpret_cast<uintptr_t>(tables[f]) & 15) == 0,
+                 "table of field %lld is null or not 16-byte aligned", (long long)f);
+  }
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t lanes = dim / 4;
+  for (int64_t f0 = 0; f0 < num_fields; f0 += kMaxFields) {
+    const int64_t nf = std::min<int64_t>(kMaxFields, num_fields - f0);
+    FieldSet fs{};
+    for (int64_t i = 0; i < nf; ++i) {
+      fs.table[i] = tables[f0 + i];
+      fs.div[i] = make_divisor(static_cast<uint64_t>(num_buckets[f0 + i]));
+    }
+    if (lanes <= 4)
+      launch_hashed_g<4>(fs, f0, nf, batch, dim, ids, offsets, combiner, out, ldo, buckets_out, s);
+    else if (lanes <= 8)
+      launch_hashed_g<8>(fs, f0, nf, batch, dim, ids, offsets, combiner, out, ldo, buckets_out, s);
+    else if (lanes <= 16)
+      launch_hashed_g<16>(fs, f0, nf, batch, dim, ids, offsets, combiner, out, ldo, buckets_out, s);
+    else if (lanes <= 32)
+      launch_hashed_g<32>(fs, f0, nf, batch, dim, ids, offsets, combiner, out, ldo, buckets_out, s);
+    else
+      launch_hashed_g<64>(fs, f0, nf, batch, dim, ids, offsets, combiner, out, ldo, buckets_out, s);
+    ANNC_HIP_TRY(hipGetLastError());
+  }
+  return set_error(ANNC_OK, "");
+}
+
+}  // extern "C"

@@ -1,0 +1,203 @@
+// runtime.cpp -- errors, per-stream state and host-operand staging.
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <string>
+#include <utility>
+
+#include "common.h"
+
+namespace annc {
+namespace {
+
+thread_local std::string g_last_error;
+
+struct StreamState {
+  int* status = nullptr;
+  void* workspace = nullptr;
+  size_t workspace_bytes = 0;
+};
+
+std::mutex g_mu;
+// Keyed by (device, stream): the NULL stream exists once per device.
+std::map<std::pair<int, hipStream_t>, StreamState> g_streams;
+std::map<int, hipStream_t> g_lib_streams;
+
+int current_device() {
+  int dev = 0;
+  (void)hipGetDevice(&dev);
+  return dev;
+}
+
+}  // namespace
+
+int set_error(int code, const char* fmt, ...) {
+  if (code == ANNC_OK) {
+    g_last_error.clear();
+    return code;
+  }
+  char buf[1024];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+void clear_error() { g_last_error.clear(); }
+
+int* stream_status(hipStream_t stream) {
+  std::lock_guard<std::mutex> lock(g_mu);
+  StreamState& st = g_streams[{current_device(), stream}];
+  if (!st.status) {
+    if (hipMalloc(&st.status, sizeof(int)) != hipSuccess) {
+      st.status = nullptr;
+      return nullptr;
+    }
+    if (hipMemset(st.status, 0, sizeof(int)) != hipSuccess) return nullptr;
+  }
+  return st.status;
+}
+
+void* stream_workspace(hipStream_t stream, size_t bytes) {
+  std::lock_guard<std::mutex> lock(g_mu);
+  StreamState& st = g_streams[{current_device(), stream}];
+  if (bytes <= st.workspace_bytes) return st.workspace;
+  if (st.workspace) {
+    (void)hipFree(st.workspace);  // synchronises the device: prior users are done
+    st.workspace = nullptr;
+    st.workspace_bytes = 0;
+  }
+  size_t want = bytes < (1u << 20) ? (1u << 20) : bytes + bytes / 4;
+  if (hipMalloc(&st.workspace, want) != hipSuccess) {
+    st.workspace = nullptr;
+    return nullptr;
+  }
+  st.workspace_bytes = want;
+  return st.workspace;
+}
+
+hipStream_t lib_stream() {
+  std::lock_guard<std::mutex> lock(g_mu);
+  int dev = current_device();
+  auto it = g_lib_streams.find(dev);
+  if (it != g_lib_streams.end()) return it->second;
+  hipStream_t s = nullptr;
+  if (hipStreamCreateWithFlags(&s, hipStreamNonBlocking) != hipSuccess) s = nullptr;
+  g_lib_streams[dev] = s;
+  return s;
+}
+
+bool is_device_ptr(const void* p) {
+  if (!p) return false;
+  hipPointerAttribute_t attr;
+  std::memset(&attr, 0, sizeof(attr));
+  hipError_t e = hipPointerGetAttributes(&attr, p);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();  // unregistered host memory: not an error here
+    return false;
+  }
+  return attr.type == hipMemoryTypeDevice || attr.type == hipMemoryTypeManaged;
+}
+
+int read_i64(const void* src, int64_t count, int64_t* dst) {
+  if (count <= 0) return ANNC_OK;
+  if (!src) return set_error(ANNC_INVALID_ARGUMENT, "null shape operand");
+  if (is_device_ptr(src)) {
+    ANNC_HIP_TRY(hipMemcpy(dst, src, sizeof(int64_t) * count, hipMemcpyDeviceToHost));
+  } else {
+    std::memcpy(dst, src, sizeof(int64_t) * count);
+  }
+  return ANNC_OK;
+}
+
+Staging::Staging(hipStream_t stream) : stream_(stream) {}
+
+Staging::~Staging() {
+  for (void* p : owned_) (void)hipFree(p);
+}
+
+void* Staging::alloc(size_t bytes) {
+  void* p = nullptr;
+  if (bytes == 0) bytes = 4;
+  hipError_t e = hipMalloc(&p, bytes);
+  if (e != hipSuccess) {
+    status_ = set_error(ANNC_RESOURCE_EXHAUSTED, "hipMalloc(%zu) failed: %s", bytes,
+                        hipGetErrorString(e));
+    return nullptr;
+  }
+  owned_.push_back(p);
+  return p;
+}
+
+const void* Staging::in(const void* p, size_t bytes) {
+  if (!p || status_ != ANNC_OK) return p;
+  if (is_device_ptr(p)) return p;
+  void* d = alloc(bytes);
+  if (!d) return nullptr;
+  hipError_t e = hipMemcpyAsync(d, p, bytes, hipMemcpyHostToDevice, stream_);
+  if (e != hipSuccess) {
+    status_ = set_error(ANNC_INTERNAL, "host-to-device copy failed: %s", hipGetErrorString(e));
+    return nullptr;
+  }
+  return d;
+}
+
+void* Staging::out(void* p, size_t bytes) {
+  if (!p || status_ != ANNC_OK) return p;
+  if (is_device_ptr(p)) return p;
+  void* d = alloc(bytes);
+  if (!d) return nullptr;
+  pending_.push_back({p, d, bytes});
+  return d;
+}
+
+void* Staging::scratch(size_t bytes) {
+  if (status_ != ANNC_OK) return nullptr;
+  return alloc(bytes);
+}
+
+int Staging::finish() {
+  if (status_ != ANNC_OK) return status_;
+  for (const Pending& q : pending_) {
+    hipError_t e = hipMemcpyAsync(q.host, q.dev, q.bytes, hipMemcpyDeviceToHost, stream_);
+    if (e != hipSuccess)
+      return status_ = set_error(ANNC_INTERNAL, "device-to-host copy failed: %s",
+                                 hipGetErrorString(e));
+  }
+  hipError_t e = hipStreamSynchronize(stream_);
+  if (e != hipSuccess)
+    return status_ = set_error(ANNC_INTERNAL, "stream synchronize failed: %s",
+                               hipGetErrorString(e));
+  pending_.clear();
+  return ANNC_OK;
+}
+
+}  // namespace annc
+
+extern "C" {
+
+const char* annc_hip_last_error(void) { return annc::g_last_error.c_str(); }
+
+const char* annc_hip_version(void) { return "annc-hip 0.1.0 (gfx950)"; }
+
+int annc_hip_stream_status(void* stream) {
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  int* st = annc::stream_status(s);
+  if (!st) return annc::set_error(ANNC_INTERNAL, "status word allocation failed");
+  ANNC_HIP_TRY(hipStreamSynchronize(s));
+  int host = 0;
+  ANNC_HIP_TRY(hipMemcpy(&host, st, sizeof(int), hipMemcpyDeviceToHost));
+  if (host != 0) {
+    ANNC_HIP_TRY(hipMemset(st, 0, sizeof(int)));
+    return annc::set_error(ANNC_INVALID_ARGUMENT,
+                           "row id out of range of the embedding table in a kernel on this stream");
+  }
+  annc::clear_error();
+  return ANNC_OK;
+}
+
+}  // extern "C"

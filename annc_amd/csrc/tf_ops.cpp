@@ -1,0 +1,225 @@
+// tf_ops.cpp -- C entry points mirroring ANNC's TensorFlow custom ops.
+//
+// TensorFlow is not part of this build, so each REGISTER_OP becomes one C
+// function with the same inputs, attributes and OP_REQUIRES messages; the
+// arithmetic runs on the GPU kernels of embedding.hip / hash.hip.  Operand
+// pointers may be host or device memory; calls are synchronous.
+#include <cstring>
+#include <vector>
+
+#include "common.h"
+#include "embedding_impl.h"
+
+namespace annc {
+int launch_bucket_strings(hipStream_t s, const char* bytes, const int64_t* offsets, int64_t n,
+                          int64_t num_buckets, int nul, int64_t empty_value, int64_t* out);
+int launch_gather_rows(hipStream_t s, const float* table, int64_t rows, int64_t dim,
+                       const int64_t* bucket, int64_t n, float* out);
+int run_sparse_embedding(hipStream_t s, const int64_t* offsets, const int64_t* bucket, int64_t n,
+                         int32_t* keep, int32_t* pos, int64_t* indices, int64_t* values,
+                         uint8_t* empty, int64_t* num_values);
+
+namespace {
+
+int read_i32(const int32_t* src, int64_t count, int32_t* dst) {
+  if (count <= 0) return ANNC_OK;
+  if (is_device_ptr(src)) {
+    ANNC_HIP_TRY(hipMemcpy(dst, src, sizeof(int32_t) * count, hipMemcpyDeviceToHost));
+  } else {
+    std::memcpy(dst, src, sizeof(int32_t) * count);
+  }
+  return ANNC_OK;
+}
+
+int write_i32(int32_t* dst, int32_t v) {
+  if (!dst) return ANNC_OK;
+  if (is_device_ptr(dst)) {
+    ANNC_HIP_TRY(hipMemcpy(dst, &v, sizeof(v), hipMemcpyHostToDevice));
+  } else {
+    *dst = v;
+  }
+  return ANNC_OK;
+}
+
+// Total byte count of a strings operand = offsets[n].
+int strings_bytes(const int64_t* offsets, int64_t n, int64_t* total) {
+  return read_i64(offsets + n, 1, total);
+}
+
+// Hash-bucket embedding shared by the three dense-output ops.
+int embed_hash_bucket(const char* bytes, const int64_t* offsets, int64_t batch,
+                      const float* weight, int64_t rows, int64_t dim, int64_t num_buckets, int nul,
+                      float* output) {
+  ANNC_REQUIRE(num_buckets >= 1, "num_buckets must be >= 1");
+  ANNC_REQUIRE(batch >= 0 && rows >= 0 && dim >= 0, "bad dimensions");
+  if (batch == 0 || dim == 0) return set_error(ANNC_OK, "");
+  ANNC_REQUIRE(bytes && offsets && weight && output, "null pointer");
+  int64_t total = 0;
+  int rc = strings_bytes(offsets, batch, &total);
+  if (rc != ANNC_OK) return rc;
+  hipStream_t s = lib_stream();
+  if (!s) return set_error(ANNC_INTERNAL, "no HIP stream");
+  Staging st(s);
+  const char* d_bytes = static_cast<const char*>(st.in(bytes, (size_t)(total > 0 ? total : 1)));
+  const int64_t* d_off = static_cast<const int64_t*>(st.in(offsets, sizeof(int64_t) * (batch + 1)));
+  const float* d_w = static_cast<const float*>(st.in(weight, sizeof(float) * rows * dim));
+  float* d_out = static_cast<float*>(st.out(output, sizeof(float) * batch * dim));
+  int64_t* bucket = static_cast<int64_t*>(st.scratch(sizeof(int64_t) * batch));
+  if (st.status() != ANNC_OK) return st.status();
+  rc = launch_bucket_strings(s, d_bytes, d_off, batch, num_buckets, nul, -1, bucket);
+  if (rc == ANNC_OK) rc = launch_gather_rows(s, d_w, rows, dim, bucket, batch, d_out);
+  if (rc != ANNC_OK) return rc;
+  rc = st.finish();
+  return rc == ANNC_OK ? set_error(ANNC_OK, "") : rc;
+}
+
+}  // namespace
+}  // namespace annc
+
+extern "C" {
+
+int annc_kp_fused_sparse_segment_reduce(const float* data, int data_rank, const int64_t* data_dims,
+                                        const void* indices, int indices_is_64,
+                                        int64_t num_indices, const int64_t* slice_input,
+                                        int slice_rank, const int64_t* slice_dims,
+                                        const int32_t* begin, int64_t begin_elems,
+                                        const int32_t* begin_1, int64_t begin_1_elems,
+                                        int combiner, int64_t* out_rows, float* output,
+                                        int32_t* slice_output) {
+  using namespace annc;
+  // OpKernel constructor (embedding_fused_sparse_segment_reduce.cc:33-34).
+  ANNC_REQUIRE(combiner == 0 || combiner == 1, "combiner must be 0 or 1");
+  // Compute() checks, same order and text (:45-57).
+  ANNC_REQUIRE(data_rank == 2, "input must be 2-D");
+  ANNC_REQUIRE(slice_rank == 2, "slice input must be 2-D");
+  ANNC_REQUIRE(begin_elems == 2, "begin must have 2 elements");
+  ANNC_REQUIRE(begin_1_elems == 1, "begin_1 must have 1 element");
+  ANNC_REQUIRE(data_dims && slice_dims && begin && begin_1, "null shape operand");
+  int32_t b[2], b1 = 0;
+  int rc = read_i32(begin, 2, b);
+  if (rc == ANNC_OK) rc = read_i32(begin_1, 1, &b1);
+  if (rc != ANNC_OK) return rc;
+  const int64_t rows = data_dims[0], dim = data_dims[1];
+  const int32_t col = b[1];
+  ANNC_REQUIRE(col >= 0 && col < slice_dims[1], "Column index out of range");
+  ANNC_REQUIRE(num_indices == slice_dims[0],
+               "indices and slice_input.dim_zie(0) should have same size");
+  ANNC_REQUIRE(num_indices == 0 || (indices && slice_input), "null operand");
+
+  hipStream_t s = lib_stream();
+  if (!s) return set_error(ANNC_INTERNAL, "no HIP stream");
+  Staging st(s);
+  const int64_t* d_slice = static_cast<const int64_t*>(
+      st.in(slice_input, sizeof(int64_t) * (size_t)(slice_dims[0] * slice_dims[1])));
+  if (st.status() != ANNC_OK) return st.status();
+  int64_t seg_min = 0, seg_max = 0;
+  bool sorted = true;
+  rc = segment_scan(s, d_slice + col, slice_dims[1], num_indices, &seg_min, &seg_max, &sorted);
+  if (rc != ANNC_OK) return rc;
+  // max_seg_id starts at 0 (:64-71): batch >= 1 even with no indices.
+  const int64_t max_seg = num_indices > 0 && seg_max > 0 ? seg_max : 0;
+  ANNC_REQUIRE(num_indices == 0 || seg_min >= 0, "segment id %lld out of range",
+               (long long)seg_min);
+  const int64_t batch = max_seg + 1;
+  if (out_rows) *out_rows = batch;
+  if (!output) return set_error(ANNC_OK, "");
+
+  const float* d_data = static_cast<const float*>(st.in(data, sizeof(float) * rows * dim));
+  const void* d_idx = st.in(indices, (indices_is_64 ? 8 : 4) * (size_t)num_indices);
+  float* d_out = static_cast<float*>(st.out(output, sizeof(float) * batch * dim));
+  if (st.status() != ANNC_OK) return st.status();
+  int* status = stream_status(s);
+  if (!status) return set_error(ANNC_RESOURCE_EXHAUSTED, "status allocation failed");
+  ANNC_HIP_TRY(hipMemsetAsync(status, 0, sizeof(int), s));
+  if (dim > 0) {
+    rc = segment_reduce(s, d_data, rows, dim, d_idx, indices_is_64, d_slice + col, slice_dims[1],
+                        num_indices, combiner, batch, d_out, sorted ? 1 : 0);
+    if (rc != ANNC_OK) return rc;
+  }
+  rc = st.finish();
+  if (rc != ANNC_OK) return rc;
+  int bad = 0;
+  ANNC_HIP_TRY(hipMemcpy(&bad, status, sizeof(int), hipMemcpyDeviceToHost));
+  if (bad) {
+    ANNC_HIP_TRY(hipMemset(status, 0, sizeof(int)));
+    return set_error(ANNC_INVALID_ARGUMENT, "indices out of range of the %lld data rows",
+                     (long long)rows);
+  }
+  // slice_output: batch when begin_1 == 0, else the embedding size (:81-83).
+  rc = write_i32(slice_output, b1 == 0 ? static_cast<int32_t>(batch) : static_cast<int32_t>(dim));
+  return rc == ANNC_OK ? set_error(ANNC_OK, "") : rc;
+}
+
+int annc_kp_fused_embedding_with_hash_bucket(const char* bytes, const int64_t* offsets,
+                                             int64_t batch, const float* weight, int64_t rows,
+                                             int64_t dim, int64_t num_buckets, int combiner,
+                                             float* output) {
+  (void)combiner;  // accepted and ignored (fused_embedding_with_hash_bucket.cc:61-77)
+  using namespace annc;
+  ANNC_REQUIRE(num_buckets <= rows || batch == 0,
+               "num_buckets (%lld) exceeds the weight rows (%lld)", (long long)num_buckets,
+               (long long)rows);
+  return embed_hash_bucket(bytes, offsets, batch, weight, rows, dim, num_buckets, 0, output);
+}
+
+int annc_kp_fused_dnn_embedding_with_hash_bucket(const char* bytes, const int64_t* offsets,
+                                                 int64_t batch, const float* weight, int64_t rows,
+                                                 int64_t dim, int64_t num_buckets,
+                                                 float* output) {
+  return annc::embed_hash_bucket(bytes, offsets, batch, weight, rows, dim, num_buckets, 1, output);
+}
+
+int annc_kp_fused_linear_embedding_with_hash_bucket(const char* bytes, const int64_t* offsets,
+                                                    int64_t batch, const float* weight,
+                                                    int64_t rows, int64_t dim,
+                                                    int64_t num_buckets, float* output) {
+  return annc::embed_hash_bucket(bytes, offsets, batch, weight, rows, dim, num_buckets, 1, output);
+}
+
+int annc_kp_fused_sparse_embedding(const char* bytes, const int64_t* offsets, int64_t n,
+                                   int64_t num_buckets, int64_t* output_indices,
+                                   int64_t* output_values, uint8_t* empty_row_indicator,
+                                   int64_t* output_shape, int64_t* num_values) {
+  using namespace annc;
+  ANNC_REQUIRE(num_buckets >= 1, "num_buckets must be >= 1");
+  ANNC_REQUIRE(n >= 0, "negative count");
+  ANNC_REQUIRE(num_values != nullptr, "null num_values");
+  int64_t shape[2] = {n, 1};
+  if (output_shape) {
+    if (is_device_ptr(output_shape)) {
+      ANNC_HIP_TRY(hipMemcpy(output_shape, shape, sizeof(shape), hipMemcpyHostToDevice));
+    } else {
+      output_shape[0] = n;
+      output_shape[1] = 1;
+    }
+  }
+  if (n == 0) {
+    *num_values = 0;
+    return set_error(ANNC_OK, "");
+  }
+  ANNC_REQUIRE(bytes && offsets && output_indices && output_values && empty_row_indicator,
+               "null pointer");
+  int64_t total = 0;
+  int rc = strings_bytes(offsets, n, &total);
+  if (rc != ANNC_OK) return rc;
+  hipStream_t s = lib_stream();
+  if (!s) return set_error(ANNC_INTERNAL, "no HIP stream");
+  Staging st(s);
+  const char* d_bytes = static_cast<const char*>(st.in(bytes, (size_t)(total > 0 ? total : 1)));
+  const int64_t* d_off = static_cast<const int64_t*>(st.in(offsets, sizeof(int64_t) * (n + 1)));
+  int64_t* d_idx = static_cast<int64_t*>(st.out(output_indices, sizeof(int64_t) * 2 * n));
+  int64_t* d_val = static_cast<int64_t*>(st.out(output_values, sizeof(int64_t) * n));
+  uint8_t* d_empty = static_cast<uint8_t*>(st.out(empty_row_indicator, (size_t)n));
+  int64_t* bucket = static_cast<int64_t*>(st.scratch(sizeof(int64_t) * n));
+  int32_t* keep = static_cast<int32_t*>(st.scratch(sizeof(int32_t) * n));
+  int32_t* pos = static_cast<int32_t*>(st.scratch(sizeof(int32_t) * n));
+  if (st.status() != ANNC_OK) return st.status();
+  rc = launch_bucket_strings(s, d_bytes, d_off, n, num_buckets, 1, 0, bucket);
+  if (rc == ANNC_OK)
+    rc = run_sparse_embedding(s, d_off, bucket, n, keep, pos, d_idx, d_val, d_empty, num_values);
+  if (rc != ANNC_OK) return rc;
+  rc = st.finish();
+  return rc == ANNC_OK ? set_error(ANNC_OK, "") : rc;
+}
+
+}  // extern "C"

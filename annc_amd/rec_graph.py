@@ -1,0 +1,165 @@
+"""Recommendation-model graphs assembled from the fused operators.
+
+These are the graphs the reference reaches through XLA clustering of a TF
+Serving model (SURVEY call stacks 3.2-3.4): dense layers lowered to
+__layout_matmul / __matmul_add_relu custom calls plus bias/activation loop
+fusions, and hashed categorical fields lowered to the embed_hash_bucket op
+family.  Here every layer is one gfx950 kernel with the bias and activation
+fused into the GEMM epilogue, all buffers are allocated once per batch size,
+and the tower runs back to back on one stream.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+from typing import Sequence
+
+import numpy as np
+import torch
+
+from . import _lib
+from . import device as dev
+
+
+class CapturedGraph:
+    """A callable captured once into a HIP graph and replayed.
+
+    Every launch of the wrapped callable goes to the capture stream (the
+    library reads torch's current stream), so one replay re-issues the whole
+    sequence with no host work per kernel.  Buffers must be allocated before
+    capture (the graphs above keep theirs per batch size); nothing in the
+    captured kernels allocates or memsets.
+    """
+
+    def __init__(self, fn, *args, warmup: int = 2):
+        self.stream = torch.cuda.Stream()  # default priority
+        self.stream.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(self.stream):
+            for _ in range(warmup):
+                self.out = fn(*args)
+        torch.cuda.current_stream().wait_stream(self.stream)
+        torch.cuda.synchronize()
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph, stream=self.stream):
+            self.out = fn(*args)
+        torch.cuda.synchronize()
+
+    def replay(self):
+        self.graph.replay()
+        return self.out
+
+    __call__ = replay
+
+
+@dataclass
+class DenseLayer:
+    weight: dev.PackedWeight | torch.Tensor  # packed [k, n] or row-major [k, n]
+    bias: torch.Tensor                        # [n]
+    activation: int                           # _lib.EPI_*
+
+
+class MLPTower:
+    """relu(x W1 + b1) ... -> sigmoid(h Wl + bl) with pre-packed weights."""
+
+    def __init__(self, weights: Sequence[np.ndarray], biases: Sequence[np.ndarray],
+                 device: torch.device | str = "cuda", packed: bool = True,
+                 final_activation: int = _lib.EPI_SIGMOID):
+        self.device = torch.device(device)
+        self.layers: list[DenseLayer] = []
+        for i, (w, b) in enumerate(zip(weights, biases)):
+            wt = torch.as_tensor(np.ascontiguousarray(w, dtype=np.float32)).to(self.device)
+            if packed:
+                wt = dev.pack_weight(wt)
+            act = final_activation if i == len(weights) - 1 else _lib.EPI_RELU
+            bt = torch.as_tensor(np.ascontiguousarray(b, dtype=np.float32)).to(self.device)
+            self.layers.append(DenseLayer(wt, bt, act))
+        self._buffers: dict[int, list[torch.Tensor]] = {}
+
+    @property
+    def widths(self) -> list[int]:
+        return [(l.weight.n if isinstance(l.weight, dev.PackedWeight) else l.weight.shape[1])
+                for l in self.layers]
+
+    def flops(self, batch: int) -> int:
+        total = 0
+        for l in self.layers:
+            w = l.weight
+            k, n = (w.k, w.n) if isinstance(w, dev.PackedWeight) else tuple(w.shape)
+            total += 2 * batch * k * n
+        return total
+
+    def buffers(self, batch: int) -> list[torch.Tensor]:
+        bufs = self._buffers.get(batch)
+        if bufs is None:
+            bufs = [torch.empty((batch, n), dtype=torch.float32, device=self.device)
+                    for n in self.widths]
+            self._buffers[batch] = bufs
+        return bufs
+
+    def forward(self, x: torch.Tensor, stream=None) -> torch.Tensor:
+        """x: [batch, k0] (any row stride).  Returns the final [batch, 1] buffer."""
+        bufs = self.buffers(x.shape[0])
+        h = x
+        for layer, out in zip(self.layers, bufs):
+            dev.gemm(h, layer.weight, bias=layer.bias, epilogue=layer.activation, out=out,
+                     stream=stream)
+            h = out
+        return h
+
+    __call__ = forward
+
+
+@dataclass
+class WideDeepConfig:
+    num_fields: int = 26
+    dim: int = 32
+    table_rows: int = 100_000
+    num_buckets: int = 100_000
+    num_dense: int = 13
+    hidden: tuple = (1024, 512, 256)
+    combiner: int = _lib.COMBINER_MEAN
+
+
+class WideDeepGraph:
+    """Hashed categorical fields + dense features -> concat -> MLP -> sigmoid.
+
+    The concat buffer is [batch, F*dim + num_dense] with its row padded to a
+    multiple of 4 floats so every row starts 16-byte aligned; the embedding
+    kernel writes its columns in place and the first GEMM reads the first
+    F*dim + num_dense columns through the padded leading dimension.
+    Column order: field 0 .. field F-1 embeddings, then the dense features.
+    """
+
+    def __init__(self, cfg: WideDeepConfig, tables: Sequence[torch.Tensor],
+                 weights: Sequence[np.ndarray], biases: Sequence[np.ndarray],
+                 device: torch.device | str = "cuda"):
+        self.cfg = cfg
+        self.device = torch.device(device)
+        self.tables = [t.to(self.device).contiguous() for t in tables]
+        self.concat_width = cfg.num_fields * cfg.dim + cfg.num_dense
+        self.ld = (self.concat_width + 3) // 4 * 4
+        self.tower = MLPTower(weights, biases, device=self.device, packed=True)
+        self._concat: dict[int, torch.Tensor] = {}
+
+    def concat_buffer(self, batch: int) -> torch.Tensor:
+        buf = self._concat.get(batch)
+        if buf is None:
+            buf = torch.zeros((batch, self.ld), dtype=torch.float32, device=self.device)
+            self._concat[batch] = buf
+        return buf
+
+    def flops(self, batch: int) -> int:
+        return self.tower.flops(batch)
+
+    def forward(self, ids: torch.Tensor, offsets: torch.Tensor, dense: torch.Tensor,
+                stream=None) -> torch.Tensor:
+        batch = dense.shape[0]
+        cfg = self.cfg
+        buf = self.concat_buffer(batch)
+        emb_cols = cfg.num_fields * cfg.dim
+        dev.hashed_embedding_bags(self.tables, [cfg.num_buckets] * cfg.num_fields, ids, offsets,
+                                  batch, cfg.combiner, out=buf[:, :emb_cols], stream=stream)
+        buf[:, emb_cols:self.concat_width].copy_(dense)
+        x = buf[:, :self.concat_width]
+        return self.tower.forward(x, stream=stream)
+
+    __call__ = forward

@@ -1,0 +1,148 @@
+"""Python mirror of ANNC's TensorFlow custom ops on the gfx950 library.
+
+TensorFlow is not installed, so each REGISTER_OP is a function with the same
+inputs, attributes and error messages; arrays may be numpy (host memory, as
+TF CPU tensors) or torch CUDA tensors.  Invalid inputs raise
+``InvalidArgumentError`` carrying the reference's OP_REQUIRES text.
+"""
+from __future__ import annotations
+
+from typing import Sequence
+
+import numpy as np
+
+from . import _lib
+from ._lib import InvalidArgumentError, check, ptr
+
+__all__ = [
+    "kp_fused_sparse_segment_reduce",
+    "kp_fused_embedding_with_hash_bucket",
+    "kp_fused_dnn_embedding_with_hash_bucket",
+    "kp_fused_linear_embedding_with_hash_bucket",
+    "kp_fused_sparse_embedding",
+    "InvalidArgumentError",
+]
+
+
+def _is_torch(x) -> bool:
+    return type(x).__module__.startswith("torch")
+
+
+def _dims(x) -> np.ndarray:
+    return np.asarray(tuple(x.shape), dtype=np.int64)
+
+
+def _empty_like_kind(ref, shape, np_dtype):
+    if _is_torch(ref):
+        import torch
+
+        tdt = {np.float32: torch.float32, np.int32: torch.int32}[np_dtype]
+        return torch.empty(shape, dtype=tdt, device=ref.device)
+    return np.empty(shape, dtype=np_dtype)
+
+
+def _as_host_i32(x) -> np.ndarray:
+    if _is_torch(x):
+        x = x.detach().cpu().numpy()
+    return np.ascontiguousarray(np.asarray(x, dtype=np.int32))
+
+
+def _contig(x):
+    if _is_torch(x):
+        return x.contiguous()
+    return np.ascontiguousarray(x)
+
+
+def kp_fused_sparse_segment_reduce(data, indices, slice_input, begin, begin_1, combiner: int = 1):
+    """KPFusedSparseSegmentReduce
+    (annc/tensorflow/ops/embedding_fused_ops.cc:29-39,
+     annc/tensorflow/kernels/embedding_fused_sparse_segment_reduce.cc:27-164).
+
+    Returns (output [max_seg+1, D] float32, slice_output int32 scalar).
+    """
+    lib = _lib.lib()
+    data = _contig(data)
+    indices = _contig(indices)
+    slice_input = _contig(slice_input)
+    begin_h = _as_host_i32(begin).reshape(-1)
+    begin1_h = _as_host_i32(begin_1).reshape(-1)
+    idx64 = str(indices.dtype).endswith("int64")
+    if not idx64 and not str(indices.dtype).endswith("int32"):
+        raise TypeError("indices must be int32 or int64 (attr Tidx)")
+    ddims = _dims(data)
+    sdims = _dims(slice_input)
+    num_indices = int(indices.shape[0]) if len(indices.shape) else 0
+    rows = np.zeros(1, dtype=np.int64)
+    args = (ptr(data), len(data.shape), ptr(ddims), ptr(indices), 1 if idx64 else 0, num_indices,
+            ptr(slice_input), len(slice_input.shape), ptr(sdims), ptr(begin_h), begin_h.size,
+            ptr(begin1_h), begin1_h.size, int(combiner), ptr(rows))
+    check(lib.annc_kp_fused_sparse_segment_reduce(*args, None, None))
+    batch = int(rows[0])
+    dim = int(ddims[1])
+    out = _empty_like_kind(data, (batch, dim), np.float32)
+    slice_out = np.zeros(1, dtype=np.int32)
+    check(lib.annc_kp_fused_sparse_segment_reduce(*args, ptr(out), ptr(slice_out)))
+    return out, np.int32(slice_out[0])
+
+
+def _pack_strings(strings: Sequence[bytes | str]):
+    enc = [s.encode() if isinstance(s, str) else bytes(s) for s in strings]
+    offsets = np.zeros(len(enc) + 1, dtype=np.int64)
+    if enc:
+        np.cumsum([len(s) for s in enc], out=offsets[1:])
+    blob = np.frombuffer(b"".join(enc) + b"\0", dtype=np.uint8).copy()
+    return blob, offsets
+
+
+def _dense_hash_op(fn_name, strings, weight, num_buckets, *extra):
+    if num_buckets < 1:
+        raise InvalidArgumentError(_lib.INVALID_ARGUMENT, "num_buckets must be >= 1")
+    blob, offsets = _pack_strings(strings)
+    weight = _contig(weight)
+    rows, dim = int(weight.shape[0]), int(weight.shape[1])
+    out = _empty_like_kind(weight, (len(offsets) - 1, dim), np.float32)
+    fn = getattr(_lib.lib(), fn_name)
+    check(fn(ptr(blob), ptr(offsets), len(offsets) - 1, ptr(weight), rows, dim, int(num_buckets),
+             *extra, ptr(out)))
+    return out
+
+
+def kp_fused_embedding_with_hash_bucket(strings, weight, num_buckets: int, combiner: int = 0):
+    """KPFusedEmbeddingWithHashBucket
+    (python/tensorflow/kernels/fused_embedding_with_hash_bucket.cc:15-83)."""
+    return _dense_hash_op("annc_kp_fused_embedding_with_hash_bucket", strings, weight,
+                          num_buckets, int(combiner))
+
+
+def kp_fused_dnn_embedding_with_hash_bucket(strings, weight, num_buckets: int):
+    """KPFusedDnnEmbeddingWithHashBucket (fused_dnn_embedding_with_hash_bucket.cc:10-62)."""
+    return _dense_hash_op("annc_kp_fused_dnn_embedding_with_hash_bucket", strings, weight,
+                          num_buckets)
+
+
+def kp_fused_linear_embedding_with_hash_bucket(strings, weight, num_buckets: int):
+    """KPFusedLinearEmbeddingWithHashBucket (fused_linear_embdedding_with_hash_bucket.cc:13-72)."""
+    return _dense_hash_op("annc_kp_fused_linear_embedding_with_hash_bucket", strings, weight,
+                          num_buckets)
+
+
+def kp_fused_sparse_embedding(strings, num_buckets: int):
+    """KPFusedSparseEmbedding (fused_sparse_embedding.cc:10-87).
+
+    Returns (indices int64[n,2], values int64[v], empty_row_indicator bool[v],
+    dense_shape int64[2]).
+    """
+    if num_buckets < 1:
+        raise InvalidArgumentError(_lib.INVALID_ARGUMENT, "num_buckets must be >= 1")
+    blob, offsets = _pack_strings(strings)
+    n = len(offsets) - 1
+    indices = np.empty((n, 2), dtype=np.int64)
+    values = np.empty(max(n, 1), dtype=np.int64)
+    empty = np.empty(max(n, 1), dtype=np.uint8)
+    shape = np.empty(2, dtype=np.int64)
+    nv = np.zeros(1, dtype=np.int64)
+    check(_lib.lib().annc_kp_fused_sparse_embedding(ptr(blob), ptr(offsets), n, int(num_buckets),
+                                                    ptr(indices), ptr(values), ptr(empty),
+                                                    ptr(shape), ptr(nv)))
+    v = int(nv[0])
+    return indices, values[:v].copy(), empty[:v].astype(bool), shape

@@ -1,0 +1,370 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X fused-operator path (one GPU).
+
+Headline (`value`): BASELINE.json configs[1], the layout_matmul MLP tower
+1024-512-256-1 at batch 4096 in fp32, as whole-tower TFLOP/s.  One step =
+one forward of the tower (3 kernels, bias/ReLU/sigmoid fused), replayed from
+a HIP graph on device-resident inputs.
+
+`roofline` is the dominant kernel (layer 1, 4096x512x1024 packed-weight
+GEMM + bias + ReLU): 2*M*N*K flops per launch over its average duration,
+timed with HIP events on the stream the launches run on.
+
+`components` reports the other configurations (fused __matmul_add_relu,
+embedding bag GB/s, hashed multi-field bags GB/s, end-to-end wide&deep
+samples/s); `cpu_baseline` times the oracle's OpenBLAS path on the host.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-components] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import re
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "embedding-bag GB/s, fused-matmul TFLOPS, e2e rec-model samples/s @ batch 4096"
+HBM_PEAK_GBS = 8000.0
+FP32_MFMA_PEAK_TFLOPS = 157.3
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def graph_time_ms(make_fn, launches: int, replays: int):
+    """Average ms per launch of fn, launched `launches` times per HIP graph."""
+    import torch
+    from annc_amd.rec_graph import CapturedGraph
+
+    def many():
+        out = None
+        for i in range(launches):
+            out = make_fn(i)
+        return out
+
+    g = CapturedGraph(many)
+    g.replay()
+    torch.cuda.synchronize()
+    s = torch.cuda.current_stream()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(s)
+    for _ in range(replays):
+        g.replay()
+    e1.record(s)
+    e1.synchronize()
+    return e0.elapsed_time(e1) / (launches * replays)
+
+
+def read_traffic(kernel_tag: str):
+    """HBM bytes per launch from a committed rocprofv3 --pmc summary, if any."""
+    path = os.path.join(ROOT, "profiles", f"{kernel_tag}_pmc.md")
+    if not os.path.exists(path):
+        return None
+    m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", open(path).read())
+    return float(m.group(1)) if m else None
+
+
+# ---------------------------------------------------------------- headline
+def bench_tower(args, device):
+    import numpy as np
+    import torch
+    from annc_amd import workloads, EPI_RELU
+    from annc_amd import device as dev
+    from annc_amd.rec_graph import CapturedGraph, MLPTower
+
+    w = workloads.config2(seed=0)
+    tower = MLPTower(w.weights, w.biases, device=device, packed=True)
+    x = torch.from_numpy(w.x).to(device)
+    batch = x.shape[0]
+    flops = tower.flops(batch)
+    step = CapturedGraph(tower, x)
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    s = torch.cuda.current_stream()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(s)
+    for _ in range(args.steps):
+        step()
+    e1.record(s)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = e0.elapsed_time(e1) / args.steps
+    log(f"tower: {ms * 1e3:.1f} us/step ({wall / args.steps * 1e3:.1f} us wall)")
+
+    # dominant kernel: layer 1 alone, back to back
+    l1 = tower.layers[0]
+    out1 = tower.buffers(batch)[0]
+    k1_ms = graph_time_ms(lambda i: dev.gemm(x, l1.weight, bias=l1.bias, epilogue=EPI_RELU,
+                                             out=out1), launches=50, replays=10)
+    m, k = x.shape
+    n = l1.weight.n
+    k1_flops = 2.0 * m * n * k
+    achieved = k1_flops / (k1_ms * 1e-3) / 1e12
+    roofline = {
+        "kernel": "gemm_mfma_kernel<2,2,1,2,packed> (layer 1: 4096x512x1024 + bias + ReLU)",
+        "bound": "mfma",
+        "achieved": round(achieved, 3),
+        "peak": FP32_MFMA_PEAK_TFLOPS,
+        "unit": "TFLOP/s",
+        "frac": round(achieved / FP32_MFMA_PEAK_TFLOPS, 4),
+        "traffic": read_traffic("gemm_layer1"),
+        "avg_launch_us": round(k1_ms * 1e3, 3),
+        "flops_per_launch": k1_flops,
+    }
+    log(f"layer1 gemm: {k1_ms * 1e3:.2f} us, {achieved:.1f} TFLOP/s")
+    per_layer = []
+    h = x
+    for i, layer in enumerate(tower.layers):
+        o = tower.buffers(batch)[i]
+        ms_i = graph_time_ms(lambda j, h=h, layer=layer, o=o: dev.gemm(
+            h, layer.weight, bias=layer.bias, epilogue=layer.activation, out=o),
+            launches=50, replays=4)
+        kk, nn = layer.weight.k, layer.weight.n
+        per_layer.append({"m": batch, "n": nn, "k": kk, "us": round(ms_i * 1e3, 2),
+                          "tflops": round(2.0 * batch * nn * kk / (ms_i * 1e-3) / 1e12, 2)})
+        h = o
+    value = flops / (ms * 1e-3) / 1e12
+    return {"value": value, "ms": ms, "flops": flops, "batch": batch, "roofline": roofline,
+            "per_layer": per_layer, "inputs": w}
+
+
+# ---------------------------------------------------------------- components
+def bench_config1(device):
+    import torch
+    from annc_amd import workloads, xla
+    w = workloads.config1(seed=0)
+    d = [torch.from_numpy(a).to(device) for a in (w.z, w.e, w.a, w.b)]
+    out = torch.empty((512, 256), dtype=torch.float32, device=device)
+    # device-resident operands through the XLA custom-call ABI (synchronous)
+    for _ in range(5):
+        xla.matmul_add_relu(*d, out)
+    reps = 50
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        xla.matmul_add_relu(*d, out)
+    sync_us = (time.perf_counter() - t0) / reps * 1e6
+    from annc_amd import device as dev, EPI_RELU
+    a, e, b = d[2], d[1], d[3]
+    k_ms = graph_time_ms(lambda i: dev.gemm(a, b, addend=e, epilogue=EPI_RELU, out=out),
+                         launches=100, replays=5)
+    flops = 2.0 * 512 * 256 * 256
+    return {"workload": "configs[0] __matmul_add_relu 512x256x256 fp32",
+            "kernel_us": round(k_ms * 1e3, 3),
+            "kernel_tflops": round(flops / (k_ms * 1e-3) / 1e12, 3),
+            "custom_call_sync_us": round(sync_us, 1),
+            "note": "launch-bound: 67.1 MFLOP is 0.43 us at peak"}
+
+
+def bench_config3(device):
+    import numpy as np
+    import torch
+    from annc_amd import workloads
+    from annc_amd import device as dev
+    w = workloads.config3(seed=0)
+    table = torch.from_numpy(w.table).to(device)
+    ids = torch.from_numpy(w.ids).to(device)
+    offs = torch.from_numpy(w.offsets).to(device)
+    nnz, bags, dim = int(w.offsets[-1]), w.offsets.size - 1, w.table.shape[1]
+    alg_bytes = 8 * nnz + 8 * (bags + 1) + 4 * dim * nnz + 4 * dim * bags
+    uniq = int(np.unique(w.ids).size)
+    uniq_bytes = 8 * nnz + 8 * (bags + 1) + 4 * dim * uniq + 4 * dim * bags
+    out = torch.empty((bags, dim), dtype=torch.float32, device=device)
+    res = {"workload": "configs[2] embedding bag: table 1e6x64 fp32, 4096 bags, Poisson(20) "
+                       "lengths, Zipf(1.05) int64 ids, CSR",
+           "nnz": nnz, "unique_rows": uniq, "algorithmic_bytes": alg_bytes,
+           "unique_row_bytes": uniq_bytes}
+    for name, comb in (("sum", 0), ("mean", 1)):
+        k_ms = graph_time_ms(lambda i: dev.embedding_bag(table, ids, offs, comb, out=out),
+                             launches=200, replays=5)
+        gbs = alg_bytes / (k_ms * 1e-3) / 1e9
+        res[name] = {"kernel_us": round(k_ms * 1e3, 3), "GBps": round(gbs, 1),
+                     "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+                     "unique_GBps": round(uniq_bytes / (k_ms * 1e-3) / 1e9, 1)}
+        log(f"bag {name}: {k_ms * 1e3:.2f} us, {gbs:.0f} GB/s")
+    # cache-defeating variant: rotate 3 table copies (768 MB > 256 MB MALL)
+    copies = [table] + [table.clone() for _ in range(2)]
+    k_ms = graph_time_ms(lambda i: dev.embedding_bag(copies[i % 3], ids, offs, 0, out=out),
+                         launches=201, replays=5)
+    res["sum_rotating_3_tables"] = {"kernel_us": round(k_ms * 1e3, 3),
+                                    "GBps": round(alg_bytes / (k_ms * 1e-3) / 1e9, 1)}
+    dev.stream_status()
+    del copies
+    return res, w
+
+
+def bench_config4(device):
+    import torch
+    from annc_amd import workloads
+    from annc_amd import device as dev
+    w = workloads.config4(seed=0)
+    tables = [torch.from_numpy(t).to(device) for t in w.tables]
+    ids = torch.from_numpy(w.ids).to(device)
+    offs = torch.from_numpy(w.offsets).to(device)
+    nf = len(tables)
+    out = torch.empty((w.batch, nf * w.dim), dtype=torch.float32, device=device)
+    nnz = int(w.offsets[-1])
+    alg_bytes = 8 * nnz + 8 * (nf * w.batch + 1) + 4 * w.dim * nnz + 4 * w.batch * nf * w.dim
+    nb = [w.num_buckets] * nf
+    k_ms = graph_time_ms(lambda i: dev.hashed_embedding_bags(tables, nb, ids, offs, w.batch, 1,
+                                                             out=out),
+                         launches=50, replays=5)
+    gbs = alg_bytes / (k_ms * 1e-3) / 1e9
+    log(f"hashed bags: {k_ms * 1e3:.2f} us, {gbs:.0f} GB/s")
+    return {"workload": "configs[3] 26 fields x batch 8192, int64 ids -> decimal -> "
+                        "Fingerprint64 % 1e5 -> gather [1e5x16] -> mean, out [8192x416]",
+            "nnz": nnz, "algorithmic_bytes": alg_bytes, "kernel_us": round(k_ms * 1e3, 3),
+            "GBps": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+            "ids_per_s": round(nnz / (k_ms * 1e-3), 1)}
+
+
+def bench_config5(device, steps: int):
+    import torch
+    from annc_amd import workloads
+    from annc_amd.rec_graph import CapturedGraph, WideDeepConfig, WideDeepGraph
+    w = workloads.config5(seed=0)
+    h = w.hashed
+    graph = WideDeepGraph(WideDeepConfig(), [torch.from_numpy(t) for t in h.tables], w.weights,
+                          w.biases, device=device)
+    ids = torch.from_numpy(h.ids).to(device)
+    offs = torch.from_numpy(h.offsets).to(device)
+    dense = torch.from_numpy(w.dense).to(device)
+    step = CapturedGraph(graph, ids, offs, dense)
+    for _ in range(5):
+        step()
+    torch.cuda.synchronize()
+    s = torch.cuda.current_stream()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(s)
+    for _ in range(steps):
+        step()
+    e1.record(s)
+    e1.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    sps = h.batch / (ms * 1e-3)
+    log(f"e2e wide&deep: {ms * 1e3:.1f} us/step, {sps:.0f} samples/s")
+    return {"workload": "configs[4] wide&deep: 26 hashed fields dim 32 (Zipf ids, bags 1-5) + 13 "
+                        "dense -> concat [4096x845] -> 1024-512-256-1 -> sigmoid",
+            "ms_per_step": round(ms, 4), "samples_per_s": round(sps, 1),
+            "gemm_tflops": round(graph.flops(h.batch) / (ms * 1e-3) / 1e12, 2)}
+
+
+# ---------------------------------------------------------------- CPU baseline
+def cpu_cores() -> int:
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(1, min(n, int(os.environ.get("OMP_NUM_THREADS", n))))
+
+
+def cpu_baseline(inputs, bag_inputs):
+    """Oracle (OpenBLAS 0.3.29 sgemm + loops) on the host: the whole config-2
+    tower at batch 4096, median of 5 after one warm-up, 1 thread and all cores."""
+    import numpy as np
+    from oracle import ora
+
+    x, ws, bs = inputs.x, inputs.weights, inputs.biases
+    flops = 2.0 * x.shape[0] * sum(w.shape[0] * w.shape[1] for w in ws)
+    res = {}
+    for threads in (1, cpu_cores()):
+        ora.set_threads(threads)
+        ora.mlp_tower(x, ws, bs)
+        ts = []
+        for _ in range(5):
+            t0 = time.perf_counter()
+            ora.mlp_tower(x, ws, bs)
+            ts.append(time.perf_counter() - t0)
+        res[threads] = flops / statistics.median(ts) / 1e12
+    cores = cpu_cores()
+    out = {"value": round(res[cores], 4), "unit": "TFLOP/s", "cores": cores, "kind": "port",
+           "sample": "full configs[1] tower (batch 4096, 5.37 GFLOP) x5 reps, median; "
+                     "OpenBLAS 0.3.29 sgemm + bias/ReLU/sigmoid loops",
+           "single_thread_value": round(res[1], 4), "blas": ora.blas_config()}
+    if bag_inputs is not None:
+        w = bag_inputs
+        bags, dim = w.offsets.size - 1, w.table.shape[1]
+        nnz = int(w.offsets[-1])
+        alg = 8 * nnz + 8 * (bags + 1) + 4 * dim * nnz + 4 * dim * bags
+        bag = {}
+        for threads in (1, cores):
+            ora.embedding_bag(w.table, w.ids, w.offsets, 0, threads=threads)
+            ts = []
+            for _ in range(5):
+                t0 = time.perf_counter()
+                ora.embedding_bag(w.table, w.ids, w.offsets, 0, threads=threads)
+                ts.append(time.perf_counter() - t0)
+            bag[f"threads_{threads}_GBps"] = round(alg / statistics.median(ts) / 1e9, 2)
+        out["embedding_bag_config3_sum"] = bag
+    return out
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=500)
+    ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--no-components", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build targets one GPU; --gpus must be 1 "
+                                   "(the sharding plan is described in DESIGN.md)"}))
+        return 2
+    import torch
+    if not torch.cuda.is_available():
+        print(json.dumps({"error": "no GPU visible"}))
+        return 1
+    device = torch.device("cuda:0")
+    torch.cuda.set_device(device)
+
+    tower = bench_tower(args, device)
+    components = {}
+    bag_inputs = None
+    if not args.no_components:
+        components["matmul_add_relu_config1"] = bench_config1(device)
+        components["embedding_bag_config3"], bag_inputs = bench_config3(device)
+        components["hashed_bags_config4"] = bench_config4(device)
+        components["wide_deep_e2e_config5"] = bench_config5(device, steps=100)
+        torch.cuda.empty_cache()
+    components["tower_layers_config2"] = tower["per_layer"]
+    cpu = None if args.no_cpu else cpu_baseline(tower["inputs"], bag_inputs)
+
+    line = {
+        "metric": METRIC,
+        "value": round(tower["value"], 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(tower["ms"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (numpy PCG64 seed 0), random-init Glorot-uniform weights",
+        "config": {"workload": "configs[1]: layout_matmul MLP tower 1024-512-256-1, fp32, "
+                               "batch 4096, pre-packed weights, bias+ReLU fused, sigmoid out",
+                   "batch": tower["batch"], "flops_per_step": tower["flops"],
+                   "step": "one HIP-graph replay of the 3-layer forward"},
+        "roofline": tower["roofline"],
+        "cpu_baseline": cpu,
+        "components": components,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,252 @@
+/*
+ * annc_hip.h -- C-ABI of the MI355X (gfx950) fused-operator library.
+ *
+ * Drop-in boundary for ANNC's fused-operator hot path.  Every symbol is
+ * extern "C", takes plain pointers and sizes, and never throws.  Integer
+ * status codes follow TensorFlow's error-code numbering (0 = OK,
+ * 3 = INVALID_ARGUMENT, 8 = RESOURCE_EXHAUSTED, 13 = INTERNAL); the message
+ * for the last failure on the calling thread is returned by
+ * annc_hip_last_error().
+ *
+ * Pointer classes:
+ *   - "any" pointers may be host memory or HIP device memory; the library
+ *     inspects them (hipPointerGetAttributes) and stages host data through
+ *     the device on an internal stream, synchronising before it returns.
+ *     This is the contract of the XLA-CPU custom calls and the TF CPU ops.
+ *   - "device" pointers must be device memory; those entry points enqueue on
+ *     the caller's stream (a hipStream_t passed as void*, NULL = the
+ *     library's per-device stream) and return without synchronising.
+ */
+#ifndef ANNC_HIP_H_
+#define ANNC_HIP_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ------------------------------------------------------------------------ */
+/* Status                                                                    */
+/* ------------------------------------------------------------------------ */
+enum {
+  ANNC_OK = 0,
+  ANNC_INVALID_ARGUMENT = 3,
+  ANNC_RESOURCE_EXHAUSTED = 8,
+  ANNC_INTERNAL = 13,
+};
+
+/* Message of the last failed call on this thread ("" when none). */
+const char* annc_hip_last_error(void);
+
+/* Library version string. */
+const char* annc_hip_version(void);
+
+/* Synchronises `stream` and returns ANNC_INVALID_ARGUMENT if any kernel
+ * enqueued on it since the previous call met an out-of-range row id (those
+ * rows contribute zero); clears the flag.  The reference leaves such ids
+ * undefined (embedding_fused_sparse_segment_reduce.cc:92-110 reads them
+ * unchecked). */
+int annc_hip_stream_status(void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* ANNC_FLAGS  (replaces annc::ANNCFlags / annc::get_annc_flags,             */
+/*              annc/service/cpu/annc_flags.h:25-39, annc_flags.cc:10-130)   */
+/* ------------------------------------------------------------------------ */
+/* 1 if `name` is enabled in the process-wide flag set parsed once from the
+ * ANNC_FLAGS environment variable (annc_flags.cc:85-93, 164-172). */
+int annc_flag_enabled(const char* name);
+/* Resets the process-wide flag set to its defaults and parses `flags` with
+ * the ANNC_FLAGS grammar (annc_flags.cc:95-162).  NULL or "" keeps defaults. */
+void annc_flags_reset(const char* flags);
+/* Writes "name=0|1\n" lines for every stored flag (sorted) into buf; returns
+ * the number of bytes needed (excluding the terminator). */
+int64_t annc_flags_dump(char* buf, int64_t len);
+
+/* ------------------------------------------------------------------------ */
+/* XLA-CPU custom-call targets (annc/service/cpu/kdnn_rewriter.h:140-155).    */
+/* Same names, same operand order, same shape-info encoding                  */
+/* (annc/service/hlo_util.h:14-21: s64[2*rank] = dims..., minor_to_major...). */
+/* `out` and `in[*]` are "any" pointers; the call is synchronous.            */
+/* ------------------------------------------------------------------------ */
+/* gemm_rewriter.cc:161-185  in = {A f32[m,k], B f32[k,n], shape(A), shape(B)} */
+void __matmul(void* out, const void** in);
+/* gemm_rewriter.cc:218-247  in = {E f32[m,n], A, B, shape(E), shape(A), shape(B)} ; out = A.B + E */
+void __matmul_add(void* out, const void** in);
+/* gemm_rewriter.cc:249-281  in = {Z, E, A, B, shape(Z), shape(E), shape(A), shape(B)} ; out = max(A.B + E, 0) */
+void __matmul_add_relu(void* out, const void** in);
+/* gemm_rewriter.cc:187-216  in = {A f32[b,m,k], B f32[b,k,n], shape(A), shape(B)} */
+void __batch_matmul(void* out, const void** in);
+/* gemm_rewriter.cc:136-159  in = {A f32[m,k], Bpk (layout_matmul-packed [k,n]), shape(A), shape(B)} */
+void __layout_matmul(void* out, const void** in);
+/* graph_opt.cc:131-176  in = {ids s64[m,k], gathered f32[m,k,n], slice_starts s64[3],
+ *                             slice_limits s64[3], shape(ids), shape(gathered)} ; out f32[m,n] */
+void __pooling(void* out, void** in);
+
+/* Function pointer of a custom-call target by its registered name, or NULL.
+ * Equivalent of the lookup XLA performs after
+ * XLA_CPU_REGISTER_CUSTOM_CALL_TARGET (kdnn_rewriter.h:148-155). */
+void* annc_custom_call_target(const char* name);
+/* Calls cb(name, fn, user) once per target, in the order of
+ * REGISTER_ALL_GEMM_KERNELS (kdnn_rewriter.h:148-155, minus the
+ * never-registered __reduce_mean); returns the number of targets. */
+int annc_register_custom_call_targets(void (*cb)(const char* name, void* fn, void* user),
+                                      void* user);
+
+/* ------------------------------------------------------------------------ */
+/* layout_matmul pre-pack (replaces annc-opt FormageChange kn->kn4,          */
+/* python/annc/optimize/data_pack.py:24-149, constant_folding.py:77-88).     */
+/* The packed array has exactly k*n elements (annc-opt re-saves variables in */
+/* their original shape, constant_folding.py:85), laid out in MFMA fragment  */
+/* order for the gfx950 kernel; format tag "mfma_f32_32x32x2_k16".           */
+/* ------------------------------------------------------------------------ */
+const char* annc_layout_matmul_rhs_format(void);
+/* Host pointers.  Returns ANNC_OK or ANNC_INVALID_ARGUMENT. */
+int annc_layout_matmul_pack_rhs(int64_t k, int64_t n, const float* src_kn, float* dst_packed);
+int annc_layout_matmul_unpack_rhs(int64_t k, int64_t n, const float* src_packed, float* dst_kn);
+/* Device-side pack of a device-resident row-major [k,n] weight. */
+int annc_hip_layout_matmul_pack_rhs(void* stream, int64_t k, int64_t n, const float* src_kn,
+                                    float* dst_packed);
+
+/* ------------------------------------------------------------------------ */
+/* Device GEMM (engine behind __matmul* / __batch_matmul / __layout_matmul)  */
+/*   C[z] = epi( A[z] . B[z] (+ E[z]) (+ bias) )   row-major, fp32 MFMA       */
+/* b_packed = 1: B is in annc_layout_matmul_pack_rhs order (ldb ignored).    */
+/* epilogue bits: ANNC_EPI_RELU = max(x, 0) as std::max(x, 0.f)              */
+/* (gemm_rewriter.cc:278-280); ANNC_EPI_SIGMOID = 1/(1+exp(-x)).             */
+/* addend (lde, stride_e) and bias (length n) may be NULL.  All device.      */
+/* ------------------------------------------------------------------------ */
+enum { ANNC_EPI_NONE = 0, ANNC_EPI_RELU = 1, ANNC_EPI_SIGMOID = 2 };
+int annc_hip_gemm(void* stream, int64_t batch, int64_t m, int64_t n, int64_t k,
+                  const float* a, int64_t lda, int64_t stride_a,
+                  const float* b, int64_t ldb, int64_t stride_b, int b_packed,
+                  const float* addend, int64_t lde, int64_t stride_e,
+                  const float* bias, int epilogue,
+                  float* c, int64_t ldc, int64_t stride_c);
+
+/* ------------------------------------------------------------------------ */
+/* Embedding bags and segment reduction (all device pointers)                */
+/* ------------------------------------------------------------------------ */
+enum { ANNC_COMBINER_SUM = 0, ANNC_COMBINER_MEAN = 1 };
+
+/* CSR embedding bag: out[b, :] = reduce_{j in [offsets[b], offsets[b+1])}
+ * table[ids[j], :], summed per dim in j order starting from 0.0f; mean
+ * multiplies by 1.0f/count and leaves empty bags at 0
+ * (embedding_fused_sparse_segment_reduce.cc:87-151).  ids are int32
+ * (ids_is_64 = 0) or int64.  out row stride ldo >= dim. */
+int annc_hip_embedding_bag(void* stream, const float* table, int64_t rows, int64_t dim,
+                           const void* ids, int ids_is_64, const int64_t* offsets,
+                           int64_t num_bags, int combiner, float* out, int64_t ldo);
+
+/* Segment reduction with arbitrary (unsorted) segment ids, the engine of
+ * KPFusedSparseSegmentReduce: out[seg_ids[i*seg_stride], :] += data[indices[i], :]
+ * in index order; out has `batch` rows (rows without ids stay 0).  Segment
+ * ids must lie in [0, batch). */
+int annc_hip_segment_reduce(void* stream, const float* data, int64_t rows, int64_t dim,
+                            const void* indices, int indices_is_64, const int64_t* seg_ids,
+                            int64_t seg_stride, int64_t n, int combiner, int64_t batch,
+                            float* out);
+
+/* sparse_embedding2 kLoop fusion (graph_opt.cc:8-41 with the bound checks of
+ * bisheng-cpu/embedding_simplify.cc:62-81):
+ * out[i,:] = table[valid ? ids[i] : fallback_row, :] * (float)valid,
+ * valid = 0 <= ids[i] < rows. */
+int annc_hip_sparse_embedding2(void* stream, const float* table, int64_t rows, int64_t dim,
+                               const void* ids, int ids_is_64, int64_t n, int64_t fallback_row,
+                               float* out);
+
+/* __pooling on device pointers (graph_opt.cc:131-176).  shapes: ids [m,k],
+ * gathered [m,k,n], out [m,n]. */
+int annc_hip_pooling(void* stream, const int64_t* ids, const float* gathered, int64_t m,
+                     int64_t k, int64_t n, const int64_t* slice_starts3,
+                     const int64_t* slice_limits3, float* out);
+
+/* ------------------------------------------------------------------------ */
+/* Hashing: FarmHash Fingerprint64 (farmhashna::Hash64, google/farmhash as  */
+/* pinned by TensorFlow 2.15) and StringToHashBucketFast semantics          */
+/* bucket = Fingerprint64(bytes) % num_buckets (unsigned).                  */
+/* Strings are given as bytes + offsets[n+1] (int64).  All device pointers. */
+/* ------------------------------------------------------------------------ */
+int annc_hip_fingerprint64(void* stream, const char* bytes, const int64_t* offsets, int64_t n,
+                           int nul_terminated, uint64_t* out);
+int annc_hip_hash_bucket_strings(void* stream, const char* bytes, const int64_t* offsets,
+                                 int64_t n, int64_t num_buckets, int nul_terminated,
+                                 int64_t* buckets);
+/* AsString(int64) (decimal, '-' for negatives) fused with the hash. */
+int annc_hip_hash_bucket_int64(void* stream, const int64_t* ids, int64_t n, int64_t num_buckets,
+                               int64_t* buckets);
+
+/* Multi-field hashed embedding bags (hash -> bucket -> gather -> pool):
+ * for field f and sample b, bag (f,b) = ids[offsets[f*batch+b] .. offsets[f*batch+b+1]),
+ * bucket = Fingerprint64(AsString(id)) % num_buckets[f], rows gathered from
+ * tables[f] ([table_rows[f], dim], num_buckets[f] <= table_rows[f]) and
+ * reduced with the segment-reduce order; written to
+ * out[b, f*dim .. f*dim+dim) with row stride ldo.  tables/table_rows/
+ * num_buckets are HOST arrays of num_fields entries (tables[f] are device
+ * pointers); ids/offsets/out are device pointers.  buckets_out (device,
+ * optional) receives the bucket id of every input id. */
+int annc_hip_hashed_embedding_bags(void* stream, int64_t num_fields, int64_t batch, int64_t dim,
+                                   const float* const* tables, const int64_t* table_rows,
+                                   const int64_t* num_buckets, const int64_t* ids,
+                                   const int64_t* offsets, int combiner, float* out, int64_t ldo,
+                                   int64_t* buckets_out);
+
+/* ------------------------------------------------------------------------ */
+/* TensorFlow custom ops (TF is absent: one C entry per op, same inputs,    */
+/* attrs and error messages).  "any" pointers, synchronous.                 */
+/* ------------------------------------------------------------------------ */
+/* KPFusedSparseSegmentReduce (annc/tensorflow/ops/embedding_fused_ops.cc:29-39,
+ * kernels/embedding_fused_sparse_segment_reduce.cc:27-164).
+ * Inputs: data f32 (data_rank, data_dims), indices int32|int64 [N],
+ * slice_input int64 (slice_rank, slice_dims), begin int32[begin_elems],
+ * begin_1 int32[begin_1_elems]; attr combiner (0 sum, 1 mean).
+ * Phase 1 (output == NULL): validates and stores the output row count
+ * (max segment id + 1) in *out_rows.  Phase 2: also writes output
+ * [*out_rows, data_dims[1]] and the scalar slice_output.
+ * Errors: the reference OP_REQUIRES messages verbatim. */
+int annc_kp_fused_sparse_segment_reduce(const float* data, int data_rank, const int64_t* data_dims,
+                                        const void* indices, int indices_is_64,
+                                        int64_t num_indices, const int64_t* slice_input,
+                                        int slice_rank, const int64_t* slice_dims,
+                                        const int32_t* begin, int64_t begin_elems,
+                                        const int32_t* begin_1, int64_t begin_1_elems,
+                                        int combiner, int64_t* out_rows, float* output,
+                                        int32_t* slice_output);
+
+/* KPFusedEmbeddingWithHashBucket
+ * (python/tensorflow/kernels/fused_embedding_with_hash_bucket.cc:15-83):
+ * out[i,:] = weight[Fingerprint64(s_i) % num_buckets, :] for non-empty s_i,
+ * zeros for empty s_i; combiner is accepted and ignored as in the reference.
+ * num_buckets must not exceed weight rows (the reference reads past the
+ * table otherwise). */
+int annc_kp_fused_embedding_with_hash_bucket(const char* bytes, const int64_t* offsets,
+                                             int64_t batch, const float* weight, int64_t rows,
+                                             int64_t dim, int64_t num_buckets, int combiner,
+                                             float* output);
+/* KPFusedDnnEmbeddingWithHashBucket / KPFusedLinearEmbeddingWithHashBucket
+ * (fused_dnn_embedding_with_hash_bucket.cc:10-62,
+ *  fused_linear_embdedding_with_hash_bucket.cc:13-72): hash of the
+ * NUL-terminated prefix, rows with bucket >= rows left at zero. */
+int annc_kp_fused_dnn_embedding_with_hash_bucket(const char* bytes, const int64_t* offsets,
+                                                 int64_t batch, const float* weight, int64_t rows,
+                                                 int64_t dim, int64_t num_buckets, float* output);
+int annc_kp_fused_linear_embedding_with_hash_bucket(const char* bytes, const int64_t* offsets,
+                                                    int64_t batch, const float* weight,
+                                                    int64_t rows, int64_t dim,
+                                                    int64_t num_buckets, float* output);
+/* KPFusedSparseEmbedding (fused_sparse_embedding.cc:10-87): outputs
+ * indices int64[n,2], values int64[*num_values], empty_row_indicator
+ * uint8[*num_values], dense_shape int64[2] = {n, 1}.  A non-empty string
+ * whose bucket is 0 adds an index row but no value (reference behaviour);
+ * the reference's out-of-range reads past *num_values are not reproduced. */
+int annc_kp_fused_sparse_embedding(const char* bytes, const int64_t* offsets, int64_t n,
+                                   int64_t num_buckets, int64_t* output_indices,
+                                   int64_t* output_values, uint8_t* empty_row_indicator,
+                                   int64_t* output_shape, int64_t* num_values);
+
+#ifdef __cplusplus
+}  /* extern "C" */
+#endif
+
+#endif  /* ANNC_HIP_H_ */

@@ -1,0 +1,155 @@
+"""GPU parity: embedding bags, segment reduction, masked gather, pooling.
+
+Bit-exact against the CPU oracle (same summation order per dim)."""
+import json
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from annc_amd import tf_ops, workloads, xla
+from annc_amd import device as dev
+from oracle import ora
+from tests.gpu_util import device, note, to_dev, to_host
+
+pytestmark = pytest.mark.gpu
+GOLD = json.load(open(os.path.join(os.path.dirname(__file__), "golden",
+                                   "segment_reduce_reference_gtest.json")))
+
+
+@pytest.mark.parametrize("combiner", [0, 1])
+@pytest.mark.parametrize("idx_dtype", [np.int64, np.int32])
+def test_bag_config3_bit_exact(combiner, idx_dtype):
+    note(f"bag config3 combiner={combiner} idx={idx_dtype.__name__}")
+    w = workloads.config3(seed=0)
+    ids = w.ids.astype(idx_dtype)
+    ref = ora.embedding_bag(w.table, ids, w.offsets, combiner, threads=8)
+    out = dev.embedding_bag(to_dev(w.table), to_dev(ids), to_dev(w.offsets), combiner)
+    dev.stream_status()
+    np.testing.assert_array_equal(to_host(out), ref)
+
+
+@pytest.mark.parametrize("dim", [1, 3, 4, 8, 16, 20, 32, 64, 100, 128, 256, 260, 512])
+def test_bag_dims_bit_exact(dim):
+    note(f"bag dim={dim}")
+    g = workloads.rng(dim)
+    rows = 5000
+    table = g.standard_normal((rows, dim)).astype(np.float32)
+    lens = np.clip(g.poisson(9, size=300), 0, 40)
+    lens[:5] = [0, 1, 40, 0, 8]  # empty, single, long bags
+    offsets = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    ids = g.integers(0, rows, size=int(offsets[-1])).astype(np.int64)
+    for combiner in (0, 1):
+        ref = ora.embedding_bag(table, ids, offsets, combiner)
+        out = dev.embedding_bag(to_dev(table), to_dev(ids), to_dev(offsets), combiner)
+        np.testing.assert_array_equal(to_host(out), ref)
+
+
+def test_bag_strided_output_and_no_bags():
+    note("bag strided output")
+    g = workloads.rng(1)
+    table = g.standard_normal((100, 16)).astype(np.float32)
+    offsets = np.array([0, 3, 3, 7], dtype=np.int64)
+    ids = g.integers(0, 100, size=7).astype(np.int64)
+    wide = torch.full((3, 40), 7.0, device=device())
+    dev.embedding_bag(to_dev(table), to_dev(ids), to_dev(offsets), 1, out=wide[:, 8:24])
+    h = to_host(wide)
+    np.testing.assert_array_equal(h[:, 8:24], ora.embedding_bag(table, ids, offsets, 1))
+    assert (h[:, :8] == 7).all() and (h[:, 24:] == 7).all()
+    empty = dev.embedding_bag(to_dev(table), to_dev(ids), to_dev(np.zeros(1, np.int64)), 0)
+    assert empty.shape == (0, 16)
+
+
+def test_bag_out_of_range_ids_flagged():
+    note("bag out-of-range ids")
+    table = np.ones((10, 8), dtype=np.float32)
+    ids = np.array([1, 10, -1, 2], dtype=np.int64)
+    offsets = np.array([0, 2, 4], dtype=np.int64)
+    out = dev.embedding_bag(to_dev(table), to_dev(ids), to_dev(offsets), 0)
+    with pytest.raises(Exception, match="out of range"):
+        dev.stream_status()
+    np.testing.assert_array_equal(to_host(out), np.ones((2, 8), np.float32))
+    dev.stream_status()  # flag cleared
+
+
+@pytest.mark.parametrize("case", GOLD["cases"], ids=lambda c: c["name"])
+@pytest.mark.parametrize("where", ["host", "device"])
+def test_tf_segment_reduce_reference_goldens(case, where):
+    note(f"segment reduce golden {case['name']} {where}")
+    data = np.asarray(case["data"], dtype=np.float32)
+    idx = np.asarray(case["indices"], dtype=np.int32)
+    sl = np.asarray(case["slice_input"], dtype=np.int64)
+    begin = np.asarray(case["begin"], np.int32)
+    begin1 = np.asarray(case["begin_1"], np.int32)
+    if where == "device":
+        data, idx, sl = to_dev(data), to_dev(idx), to_dev(sl)
+    out, so = tf_ops.kp_fused_sparse_segment_reduce(data, idx, sl, begin, begin1, case["combiner"])
+    out = to_host(out) if where == "device" else out
+    np.testing.assert_array_equal(out, np.asarray(case["expected"], np.float32))
+    assert int(so) == case["expected_slice_output"]
+
+
+@pytest.mark.parametrize("sorted_segments", [True, False])
+@pytest.mark.parametrize("combiner", [0, 1])
+def test_tf_segment_reduce_random(sorted_segments, combiner):
+    note(f"segment reduce random sorted={sorted_segments} combiner={combiner}")
+    g = workloads.rng(21)
+    rows, dim, n = 20000, 24, 50000
+    data = g.standard_normal((rows, dim)).astype(np.float32)
+    idx = g.integers(0, rows, size=n).astype(np.int64)
+    seg = g.integers(0, 3000, size=n).astype(np.int64)
+    if sorted_segments:
+        seg.sort()
+    slice_input = np.stack([np.zeros(n, np.int64), seg, seg * 7], axis=1)
+    out, so = tf_ops.kp_fused_sparse_segment_reduce(data, idx, slice_input,
+                                                    np.array([0, 1], np.int32),
+                                                    np.array([0], np.int32), combiner)
+    batch = int(seg.max()) + 1
+    assert out.shape == (batch, dim) and int(so) == batch
+    np.testing.assert_array_equal(out, ora.segment_reduce(data, idx, seg, batch, combiner))
+
+
+def test_tf_segment_reduce_empty_indices():
+    note("segment reduce empty")
+    out, so = tf_ops.kp_fused_sparse_segment_reduce(
+        np.ones((3, 4), np.float32), np.zeros(0, np.int32), np.zeros((0, 2), np.int64),
+        np.array([0, 1], np.int32), np.array([1], np.int32), 1)
+    np.testing.assert_array_equal(out, np.zeros((1, 4), np.float32))  # max_seg starts at 0
+    assert int(so) == 4
+
+
+def test_device_segment_reduce_unsorted():
+    note("device segment reduce")
+    g = workloads.rng(8)
+    data = g.standard_normal((500, 12)).astype(np.float32)
+    idx = g.integers(0, 500, size=4000).astype(np.int32)
+    seg = g.integers(0, 700, size=4000).astype(np.int64)
+    out = dev.segment_reduce(to_dev(data), to_dev(idx), to_dev(seg), 700, 1)
+    np.testing.assert_array_equal(to_host(out), ora.segment_reduce(data, idx, seg, 700, 1))
+
+
+def test_sparse_embedding2_bit_exact():
+    note("sparse_embedding2")
+    g = workloads.rng(3)
+    table = g.standard_normal((1000, 16)).astype(np.float32)
+    ids = g.integers(-50, 1050, size=3000).astype(np.int64)
+    out = dev.sparse_embedding2(to_dev(table), to_dev(ids), fallback_row=0)
+    got = to_host(out)
+    ref = ora.sparse_embedding2(table, ids, 0)
+    np.testing.assert_array_equal(got, ref)
+    assert (np.signbit(got) == np.signbit(ref)).all()
+
+
+@pytest.mark.parametrize("ss,sl", [((0, 0, 0), (64, 30, 16)), ((3, 2, 1), (60, 25, 12))])
+def test_pooling_bit_exact(ss, sl):
+    note(f"pooling {ss} {sl}")
+    g = workloads.rng(4)
+    ids = g.integers(-2, 50, size=(64, 30)).astype(np.int64)
+    ids[5] = 0
+    gathered = g.standard_normal((64, 30, 16)).astype(np.float32)
+    ref = ora.pooling(ids, gathered, ss, sl)
+    np.testing.assert_array_equal(to_host(dev.pooling(to_dev(ids), to_dev(gathered), ss, sl)), ref)
+    out = np.empty((64, 16), np.float32)
+    xla.pooling(ids, gathered, ss, sl, out)  # __pooling custom call on host buffers
+    np.testing.assert_array_equal(out, ref)

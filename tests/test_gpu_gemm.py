@@ -1,0 +1,160 @@
+"""GPU parity: fp32 MFMA GEMM custom calls against OpenBLAS 0.3.29.
+
+Tolerance per element: |got - ref| <= 1e-4*|ref| + 1e-4*(|A||B| + |E|)."""
+import numpy as np
+import pytest
+import torch
+
+from annc_amd import EPI_NONE, EPI_RELU, EPI_SIGMOID, workloads, xla
+from annc_amd import device as dev
+from annc_amd.rec_graph import MLPTower, WideDeepConfig, WideDeepGraph
+from oracle import ora
+from tests.gpu_util import assert_gemm_close, device, gemm_bound, note, to_dev, to_host
+
+pytestmark = pytest.mark.gpu
+
+
+def test_config1_matmul_add_relu_custom_call_host_and_device():
+    note("config1 __matmul_add_relu")
+    w = workloads.config1(seed=0)
+    ref = ora.matmul_add_relu(w.e, w.a, w.b)
+    bound = gemm_bound(w.a, w.b, w.e)
+    out = np.empty_like(ref)
+    xla.matmul_add_relu(w.z, w.e, w.a, w.b, out)  # host pointers: staged
+    assert_gemm_close(out, ref, bound)
+    assert (out >= 0).all()
+    d = [to_dev(x) for x in (w.z, w.e, w.a, w.b)]
+    dout = torch.empty(ref.shape, dtype=torch.float32, device=device())
+    xla.matmul_add_relu(*d, dout)  # device pointers: in place
+    assert_gemm_close(to_host(dout), ref, bound)
+
+
+@pytest.mark.parametrize("seed", [1, 2, 3, 4])
+def test_config1_seeds(seed):
+    note(f"config1 seed {seed}")
+    w = workloads.config1(seed=seed)
+    out = np.empty((512, 256), np.float32)
+    xla.matmul_add_relu(w.z, w.e, w.a, w.b, out)
+    assert_gemm_close(out, ora.matmul_add_relu(w.e, w.a, w.b), gemm_bound(w.a, w.b, w.e))
+
+
+SHAPES = [(512, 256, 256), (1, 1, 1), (33, 65, 17), (64, 128, 32), (100, 300, 845),
+          (4096, 512, 1024), (257, 129, 63), (5, 700, 3), (128, 128, 1), (96, 40, 1000),
+          (4096, 1, 256), (7, 3, 50)]
+
+
+@pytest.mark.parametrize("m,n,k", SHAPES)
+def test_matmul_and_matmul_add(m, n, k):
+    note(f"__matmul/__matmul_add {m}x{n}x{k}")
+    g = workloads.rng(m + n + k)
+    a = g.standard_normal((m, k)).astype(np.float32)
+    b = g.standard_normal((k, n)).astype(np.float32)
+    e = g.standard_normal((m, n)).astype(np.float32)
+    out = np.empty((m, n), np.float32)
+    xla.matmul(a, b, out)
+    assert_gemm_close(out, ora.matmul(a, b), gemm_bound(a, b))
+    xla.matmul_add(e, a, b, out)
+    assert_gemm_close(out, ora.matmul_add(e, a, b), gemm_bound(a, b, e))
+
+
+@pytest.mark.parametrize("m,n,k", [(512, 256, 256), (4096, 512, 1024), (100, 300, 845),
+                                   (64, 96, 31), (40, 33, 12), (300, 20, 64)])
+def test_layout_matmul_packed(m, n, k):
+    note(f"__layout_matmul {m}x{n}x{k}")
+    g = workloads.rng(m * 7 + n)
+    a = g.standard_normal((m, k)).astype(np.float32)
+    w = g.standard_normal((k, n)).astype(np.float32)
+    packed = dev.pack_weight_host(w)
+    ref = ora.matmul(a, w)
+    out = np.empty((m, n), np.float32)
+    xla.layout_matmul(a, packed, k, n, out)
+    assert_gemm_close(out, ref, gemm_bound(a, w))
+    # device packer produces the same bytes
+    pw = dev.pack_weight(to_dev(w))
+    np.testing.assert_array_equal(to_host(pw.data), packed)
+    got = dev.gemm(to_dev(a), pw)
+    assert_gemm_close(to_host(got), ref, gemm_bound(a, w))
+
+
+@pytest.mark.parametrize("batch,m,n,k", [(3, 40, 50, 60), (8, 64, 64, 64), (2, 8, 8, 8),
+                                         (5, 100, 13, 200)])
+def test_batch_matmul(batch, m, n, k):
+    note(f"__batch_matmul {batch}x{m}x{n}x{k}")
+    g = workloads.rng(batch * m)
+    a = g.standard_normal((batch, m, k)).astype(np.float32)
+    b = g.standard_normal((batch, k, n)).astype(np.float32)
+    out = np.empty((batch, m, n), np.float32)
+    xla.batch_matmul(a, b, out)
+    ref = ora.batch_matmul(a, b)
+    for i in range(batch):
+        assert_gemm_close(out[i], ref[i], gemm_bound(a[i], b[i]))
+
+
+@pytest.mark.parametrize("epi", [EPI_NONE, EPI_RELU, EPI_SIGMOID])
+@pytest.mark.parametrize("packed", [False, True])
+def test_bias_epilogues_and_padded_lda(epi, packed):
+    note(f"epilogue {epi} packed={packed}")
+    g = workloads.rng(epi * 2 + packed)
+    m, k, n, ld = 300, 845, 200, 848
+    buf = g.standard_normal((m, ld)).astype(np.float32)
+    a = buf[:, :k]
+    w = g.standard_normal((k, n)).astype(np.float32) * np.float32(0.05)
+    bias = g.standard_normal(n).astype(np.float32)
+    act = {EPI_NONE: 0, EPI_RELU: 1, EPI_SIGMOID: 2}[epi]
+    ref = ora.dense_layer(np.ascontiguousarray(a), w, bias, act)
+    wt = dev.pack_weight(to_dev(w)) if packed else to_dev(w)
+    got = to_host(dev.gemm(to_dev(buf)[:, :k], wt, bias=to_dev(bias), epilogue=epi))
+    bound = gemm_bound(a, w, np.broadcast_to(bias, (m, n)))
+    if epi == EPI_SIGMOID:
+        np.testing.assert_allclose(got, ref, rtol=1e-4, atol=1e-5)
+    else:
+        assert_gemm_close(got, ref, bound)
+
+
+def test_relu_propagates_nan_and_clamps():
+    note("relu semantics")
+    a = np.zeros((32, 32), np.float32)
+    a[0, 0] = np.nan
+    b = np.eye(32, dtype=np.float32)
+    e = np.zeros((32, 32), np.float32)
+    e[1, 1] = -0.0
+    e[2, 2] = -3.0
+    out = np.empty((32, 32), np.float32)
+    xla.matmul_add_relu(np.zeros_like(e), e, a, b, out)
+    assert np.isnan(out[0, 0])  # std::max(NaN, 0.f) returns NaN
+    assert out[2, 2] == 0.0
+
+
+def test_config2_mlp_tower():
+    note("config2 MLP tower")
+    w = workloads.config2(seed=0)
+    tower = MLPTower(w.weights, w.biases, device=device(), packed=True)
+    x = to_dev(w.x)
+    y = to_host(tower(x))
+    # layer by layer against the oracle fed with the GPU's previous layer
+    h = w.x
+    for i, layer in enumerate(tower.layers):
+        out = to_host(tower.buffers(x.shape[0])[i])
+        act = 2 if i == len(tower.layers) - 1 else 1
+        ref = ora.dense_layer(h, w.weights[i], w.biases[i], act)
+        if act == 2:
+            np.testing.assert_allclose(out, ref, rtol=1e-4, atol=1e-6)
+        else:
+            assert_gemm_close(out, ref, gemm_bound(h, w.weights[i],
+                                                   np.broadcast_to(w.biases[i], ref.shape)))
+        h = out
+    np.testing.assert_allclose(y, ora.mlp_tower(w.x, w.weights, w.biases), rtol=1e-3, atol=1e-5)
+
+
+def test_config5_wide_deep_graph():
+    note("config5 wide&deep")
+    w = workloads.config5(seed=0)
+    h = w.hashed
+    cfg = WideDeepConfig()
+    graph = WideDeepGraph(cfg, [to_dev(t) for t in h.tables], w.weights, w.biases, device=device())
+    y = to_host(graph(to_dev(h.ids), to_dev(h.offsets), to_dev(w.dense)))
+    emb = ora.hashed_embedding_bags(h.tables, h.num_buckets, h.ids, h.offsets, h.batch, 1, threads=8)
+    x = np.concatenate([emb, w.dense], axis=1)
+    concat = to_host(graph.concat_buffer(h.batch))[:, :x.shape[1]]
+    np.testing.assert_array_equal(concat, x)  # embeddings bit-exact, dense copied
+    np.testing.assert_allclose(y, ora.mlp_tower(x, w.weights, w.biases), rtol=1e-3, atol=1e-5)

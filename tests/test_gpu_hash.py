@@ -1,0 +1,127 @@
+"""GPU parity: FarmHash Fingerprint64, hash buckets, hashed embedding ops.
+
+Bucket ids and gather indices bit-exact; pooled rows bit-exact (same order)."""
+import json
+import os
+
+import numpy as np
+import pytest
+
+from annc_amd import tf_ops, workloads
+from annc_amd import device as dev
+from oracle import ora
+from tests.gpu_util import device, note, to_dev, to_host
+
+pytestmark = pytest.mark.gpu
+VECS = json.load(open(os.path.join(os.path.dirname(__file__), "golden",
+                                   "farmhash_fingerprint64_vectors.json")))
+
+
+def _u64(x):
+    return np.asarray(x).astype(np.int64).view(np.uint64)
+
+
+def test_fingerprint_published_vectors_on_gpu():
+    note("fingerprint published vectors")
+    strs = []
+    for v in VECS["vectors"]:
+        if "input_repeat" in v:
+            s, n = v["input_repeat"]
+            strs.append((s * n).encode())
+        else:
+            strs.append(v["input"].encode())
+    data, off = dev.strings_to_device(strs, device())
+    got = _u64(to_host(dev.fingerprint64(data, off)))
+    assert [int(x) for x in got] == [v["fingerprint"] for v in VECS["vectors"]]
+
+
+def test_fingerprint_all_lengths_match_oracle():
+    note("fingerprint lengths 0..300")
+    g = workloads.rng(12)
+    strs = [g.integers(0, 256, size=n, dtype=np.uint8).tobytes() for n in range(0, 301)]
+    strs += [g.integers(0, 256, size=int(n), dtype=np.uint8).tobytes()
+             for n in g.integers(0, 2000, size=200)]
+    data, off = dev.strings_to_device(strs, device())
+    got = _u64(to_host(dev.fingerprint64(data, off)))
+    np.testing.assert_array_equal(got, ora.fingerprint64_batch(strs))
+    gotn = _u64(to_host(dev.fingerprint64(data, off, nul_terminated=True)))
+    np.testing.assert_array_equal(gotn, ora.fingerprint64_batch(strs, nul_terminated=True))
+
+
+EDGE_IDS = [0, 1, -1, 9, 10, 11, 99, 100, 101, -9, -10, 999_999, 1_000_000, 12345678,
+            99_999_999, 100_000_000, 100_000_001, 10**15, 10**16 - 1, 10**16, 10**16 + 1,
+            10**17, 10**18, 2**63 - 1, -2**63, -2**63 + 1, -(10**18), 4_294_967_295,
+            4_294_967_296, -4_294_967_296]
+
+
+@pytest.mark.parametrize("num_buckets", [1, 2, 7, 10, 100_000, 2**31 - 1, 2**32 + 15,
+                                         2**62 + 3, 2**63 - 1])
+def test_hash_bucket_int64_bit_exact(num_buckets):
+    note(f"hash bucket int64 nb={num_buckets}")
+    g = workloads.rng(num_buckets % 997)
+    ids = np.concatenate([np.asarray(EDGE_IDS, dtype=np.int64),
+                          g.integers(-2**63, 2**63 - 1, size=20000, dtype=np.int64),
+                          g.integers(0, 10**6, size=5000, dtype=np.int64)])
+    got = to_host(dev.hash_bucket_int64(to_dev(ids), num_buckets))
+    np.testing.assert_array_equal(got, ora.hash_bucket_int64(ids, num_buckets))
+
+
+def test_hash_bucket_strings_bit_exact():
+    note("hash bucket strings")
+    strs = [str(i).encode() for i in range(-500, 500)] + [b"", b"hello", b"x" * 40, b"y" * 90]
+    data, off = dev.strings_to_device(strs, device())
+    got = to_host(dev.hash_bucket_strings(data, off, 1000))
+    np.testing.assert_array_equal(got, ora.hash_bucket_strings(strs, 1000))
+    v = VECS["hash_bucket_vectors"][0]
+    d2, o2 = dev.strings_to_device(v["inputs"], device())
+    assert to_host(dev.hash_bucket_strings(d2, o2, v["num_buckets"])).tolist() == v["buckets"]
+
+
+def test_hashed_bags_config4_bit_exact():
+    note("hashed bags config4")
+    w = workloads.config4(seed=0)
+    ref, ref_buckets = ora.hashed_embedding_bags(w.tables, w.num_buckets, w.ids, w.offsets,
+                                                 w.batch, 1, threads=8, with_buckets=True)
+    tables = [to_dev(t) for t in w.tables]
+    buckets = to_dev(np.full(w.ids.size, -7, dtype=np.int64))
+    out = dev.hashed_embedding_bags(tables, [w.num_buckets] * len(tables), to_dev(w.ids),
+                                    to_dev(w.offsets), w.batch, 1, buckets_out=buckets)
+    np.testing.assert_array_equal(to_host(buckets), ref_buckets)
+    np.testing.assert_array_equal(to_host(out), ref)
+
+
+@pytest.mark.parametrize("dim", [4, 16, 32, 64, 128, 264])
+def test_hashed_bags_dims_sum(dim):
+    note(f"hashed bags dim={dim}")
+    g = workloads.rng(dim + 1)
+    nf, batch, rows = 3, 257, 777
+    ids, offsets = workloads.hashed_structure(g, nf, batch, lo=0, hi=9)
+    tables = [g.standard_normal((rows, dim)).astype(np.float32) for _ in range(nf)]
+    ref = ora.hashed_embedding_bags(tables, rows - 5, ids, offsets, batch, 0)
+    out = dev.hashed_embedding_bags([to_dev(t) for t in tables], [rows - 5] * nf, to_dev(ids),
+                                    to_dev(offsets), batch, 0)
+    np.testing.assert_array_equal(to_host(out), ref)
+
+
+def test_tf_embedding_with_hash_bucket_ops():
+    note("tf hash bucket ops")
+    g = workloads.rng(5)
+    weight = g.standard_normal((1000, 8)).astype(np.float32)
+    strs = [str(int(v)).encode() for v in g.integers(-10**12, 10**12, size=3000)]
+    strs[::97] = [b""] * len(strs[::97])
+    strs[5] = b"ab\0cd"
+    out = tf_ops.kp_fused_embedding_with_hash_bucket(strs, weight, 1000, combiner=1)
+    np.testing.assert_array_equal(out, ora.embedding_with_hash_bucket(strs, weight, 1000))
+    for fn in (tf_ops.kp_fused_dnn_embedding_with_hash_bucket,
+               tf_ops.kp_fused_linear_embedding_with_hash_bucket):
+        got = fn(strs, weight[:600], 1000)  # buckets >= rows stay zero
+        np.testing.assert_array_equal(got, ora.dnn_embedding_with_hash_bucket(strs, weight[:600], 1000))
+
+
+def test_tf_sparse_embedding():
+    note("tf sparse embedding")
+    strs = [str(i).encode() for i in range(2000)] + [b""] * 3 + [b"\0x"]
+    got = tf_ops.kp_fused_sparse_embedding(strs, 7)
+    ref = ora.sparse_embedding(strs, 7)
+    for a, b in zip(got, ref):
+        np.testing.assert_array_equal(a, b)

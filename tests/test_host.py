@@ -1,0 +1,179 @@
+"""Host-side logic of the library: exports, ANNC_FLAGS, pre-pack, validation.
+
+CPU only: nothing here launches a kernel.
+"""
+import json
+import os
+import re
+
+import numpy as np
+import pytest
+
+from annc_amd import _lib, flags, tf_ops, xla
+from annc_amd import device as dev
+from oracle import ora
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _header_functions():
+    text = open(os.path.join(ROOT, "include", "annc_hip.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    names = re.findall(r"^[A-Za-z_][\w\s\*]*?\b(\w+)\s*\(", text, flags=re.M)
+    return sorted(set(n for n in names if n not in ("extern", "if")))
+
+
+def test_library_exports_every_header_symbol():
+    lib = _lib.lib()
+    names = _header_functions()
+    assert "__matmul_add_relu" in names and "annc_hip_gemm" in names
+    for n in names:
+        assert hasattr(lib, n), f"missing export {n}"
+    # and the Python binding declares a prototype for each of them
+    assert sorted(_lib.exported_names()) == names
+
+
+def test_custom_call_registry():
+    assert xla.registered_targets() == ["__matmul", "__batch_matmul", "__matmul_add",
+                                        "__matmul_add_relu", "__pooling", "__layout_matmul"]
+    lib = _lib.lib()
+    for t in xla.TARGETS:
+        assert lib.annc_custom_call_target(t.encode())
+    assert not lib.annc_custom_call_target(b"__reduce_mean")
+
+
+# ------------------------------------------------------------------ flags
+FLAG_CASES = [
+    "",
+    "--matmul",
+    "--layout-matmul --matmul-add-relu",
+    "--gemm-opt",
+    "--graph-opt",
+    "--gemm-opt=false",
+    "--matmul=1 --pooling=true --sps-emd-2=0",
+    "--matmul=yes",
+    "--matmul= --pooling",
+    "--annc-pass=false",
+    "   --matmul    --batch-matmul   ",
+    "--unknown-flag --matmul",
+    "--matmul bogus --pooling",
+    "-matmul --pooling",
+    "--matmul\t--pooling",
+    "--matmul=true=1",
+    "--",
+    "--gemm-opt --matmul=false",
+]
+ALL_FLAGS = list(flags.FLAG_NAMES) + ["unknown-flag", "gemm-opt", "graph-opt", ""]
+
+EXPECTED = {
+    "": {"annc-pass"},
+    "--matmul": {"matmul", "annc-pass"},
+    "--gemm-opt": {"matmul", "layout-matmul", "disable-tf-matmul-fusion", "annc-pass"},
+    "--graph-opt": {"sps-emd-2", "annc-pass"},
+    "--gemm-opt=false": {"matmul", "layout-matmul", "disable-tf-matmul-fusion", "annc-pass"},
+    "--matmul=yes": {"annc-pass"},
+    "--annc-pass=false": set(),
+    "--unknown-flag --matmul": {"unknown-flag", "matmul", "annc-pass"},
+    "--matmul bogus --pooling": {"matmul", "annc-pass"},
+    "--gemm-opt --matmul=false": {"layout-matmul", "disable-tf-matmul-fusion", "annc-pass"},
+}
+
+
+@pytest.mark.parametrize("s", FLAG_CASES)
+def test_flags_grammar(s):
+    flags.reset(s)
+    got = {n for n in ALL_FLAGS if flags.is_enabled(n)}
+    if s in EXPECTED:
+        assert got == EXPECTED[s]
+    ref = [ora.ref_flag_enabled(s, n) for n in ALL_FLAGS]
+    if ref[0] is not None:  # oracle/_ref built from the reference's annc_flags.cc
+        assert got == {n for n, r in zip(ALL_FLAGS, ref) if r}
+    flags.reset(None)
+
+
+def test_flags_env_default_set():
+    flags.reset(None)
+    assert flags.dump() == {n: n == "annc-pass" for n in flags.FLAG_NAMES}
+
+
+# ------------------------------------------------------------------ pre-pack
+def _offset_model(k, n, K, N):
+    """Independent statement of the packed position (per region)."""
+    kf, nf = K // 32 * 32, N // 32 * 32
+    if n >= nf:
+        return nf * K + k * (N - nf) + (n - nf)
+    if k >= kf:
+        return nf * kf + (k - kf) * nf + n
+    block = (n // 32) * (kf // 32) + k // 32
+    lane = 32 * ((k % 32) // 16) + n % 32
+    step = k % 16
+    return block * 1024 + (step // 4) * 256 + lane * 4 + step % 4
+
+
+@pytest.mark.parametrize("k,n", [(1, 1), (32, 32), (64, 96), (845, 1024), (33, 31), (100, 70),
+                                 (1024, 512), (31, 64), (12, 12)])
+def test_pack_is_a_bijection_with_the_documented_order(k, n):
+    w = np.arange(k * n, dtype=np.float32).reshape(k, n)
+    p = dev.pack_weight_host(w)
+    assert p.size == k * n
+    assert np.array_equal(np.sort(p), w.reshape(-1))  # a permutation
+    np.testing.assert_array_equal(dev.unpack_weight_host(p, k, n), w)
+    g = np.random.Generator(np.random.PCG64(k * 1000 + n))
+    for kk, nn in zip(g.integers(0, k, 64), g.integers(0, n, 64)):
+        assert p[_offset_model(int(kk), int(nn), k, n)] == w[kk, nn]
+
+
+def test_pack_small_n_is_row_major():
+    w = np.random.default_rng(0).standard_normal((40, 20)).astype(np.float32)
+    np.testing.assert_array_equal(dev.pack_weight_host(w), w.reshape(-1))
+
+
+def test_fragment_block_is_mfma_b_operand():
+    # lanes 0-31 of the first float4 hold k = 0..3 of columns 0..31
+    w = np.arange(64 * 64, dtype=np.float32).reshape(64, 64)
+    p = dev.pack_weight_host(w)
+    blk = p[:1024].reshape(4, 64, 4)  # [q][lane][e]
+    for lane in range(64):
+        for q in range(4):
+            for e in range(4):
+                assert blk[q, lane, e] == w[16 * (lane // 32) + 4 * q + e, lane % 32]
+
+
+def test_rhs_format_tag():
+    assert _lib.lib().annc_layout_matmul_rhs_format().decode() == "mfma_f32_32x32x2_k16"
+
+
+# ------------------------------------------------------------------ TF-op validation
+_GOLD = json.load(open(os.path.join(ROOT, "tests", "golden", "segment_reduce_reference_gtest.json")))
+
+
+@pytest.mark.parametrize("case", _GOLD["error_cases"], ids=lambda c: c["name"])
+def test_segment_reduce_error_messages(case):
+    data = np.arange(np.prod(case["data_shape"]), dtype=np.float32).reshape(case["data_shape"])
+    idx = np.zeros(case["indices_shape"], dtype=np.int32)
+    sl = np.ones(case["slice_shape"], dtype=np.int64)
+    with pytest.raises(tf_ops.InvalidArgumentError) as ei:
+        tf_ops.kp_fused_sparse_segment_reduce(data, idx, sl, np.array(case["begin"], np.int32),
+                                              np.array(case["begin_1"], np.int32),
+                                              case["combiner"])
+    assert case["message"] in str(ei.value)
+
+
+def test_segment_reduce_bad_combiner():
+    with pytest.raises(tf_ops.InvalidArgumentError, match="combiner must be 0 or 1"):
+        tf_ops.kp_fused_sparse_segment_reduce(np.zeros((2, 2), np.float32), np.zeros(1, np.int32),
+                                              np.zeros((1, 2), np.int64), np.array([0, 0], np.int32),
+                                              np.array([0], np.int32), combiner=2)
+
+
+def test_hash_ops_reject_zero_buckets():
+    with pytest.raises(tf_ops.InvalidArgumentError):
+        tf_ops.kp_fused_embedding_with_hash_bucket([b"a"], np.zeros((4, 2), np.float32), 0)
+    with pytest.raises(tf_ops.InvalidArgumentError):
+        tf_ops.kp_fused_sparse_embedding([b"a"], 0)
+
+
+def test_shape_info_encoding():
+    # hlo_util.h:14-21 -- dims then minor_to_major; row-major [512,256] -> {512,256,1,0}
+    assert xla.shape_info((512, 256)).tolist() == [512, 256, 1, 0]
+    assert xla.shape_info((2, 3, 4)).tolist() == [2, 3, 4, 2, 1, 0]

@@ -1,0 +1,245 @@
+"""Pins the CPU oracle before it is trusted as the GPU checker (CPU only)."""
+import json
+import os
+
+import numpy as np
+import pytest
+
+from oracle import ora
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+def _load(name):
+    with open(os.path.join(GOLDEN, name)) as f:
+        return json.load(f)
+
+
+# ------------------------------------------------------------ FarmHash
+def _vec_input(v):
+    if "input_repeat" in v:
+        s, n = v["input_repeat"]
+        return (s * n).encode()
+    return v["input"].encode()
+
+
+@pytest.mark.parametrize("vec", _load("farmhash_fingerprint64_vectors.json")["vectors"],
+                         ids=lambda v: v.get("input", str(v.get("input_repeat"))))
+def test_fingerprint64_published_vectors(vec):
+    assert ora.fingerprint64(_vec_input(vec)) == vec["fingerprint"]
+
+
+def test_hash_bucket_published_vector():
+    for v in _load("farmhash_fingerprint64_vectors.json")["hash_bucket_vectors"]:
+        got = ora.hash_bucket_strings(v["inputs"], v["num_buckets"])
+        assert got.tolist() == v["buckets"]
+
+
+def test_fingerprint_batch_matches_scalar_and_nul_prefix():
+    strs = [b"", b"x", b"hello world, farmhash", b"ab\0cd", b"z" * 70]
+    fp = ora.fingerprint64_batch(strs)
+    assert [int(x) for x in fp] == [ora.fingerprint64(s) for s in strs]
+    # NUL-terminated hashing (tensorflow::Fingerprint64(const char*)) sees the prefix.
+    fpn = ora.fingerprint64_batch(strs, nul_terminated=True)
+    assert int(fpn[3]) == ora.fingerprint64(b"ab")
+    assert int(fpn[4]) == ora.fingerprint64(b"z" * 70)
+
+
+@pytest.mark.parametrize("v", [0, 1, -1, 9, 10, -10, 99999999, 100000000, 10**16 - 1, 10**16,
+                               2**63 - 1, -2**63, 1234567890123456789, -987654321])
+def test_format_int64_is_decimal(v):
+    assert ora.format_int64(v) == str(v).encode()
+
+
+def test_hash_bucket_int64_is_hash_of_decimal_text():
+    g = np.random.Generator(np.random.PCG64(3))
+    ids = g.integers(-2**63, 2**63 - 1, size=200, dtype=np.int64)
+    got = ora.hash_bucket_int64(ids, 100_000)
+    want = [ora.fingerprint64(str(int(v)).encode()) % 100_000 for v in ids]
+    assert got.tolist() == want
+
+
+def _gm_mod(n, d):
+    """Granlund-Montgomery round-up reciprocal, as make_divisor/mod_invariant use it."""
+    if d == 1:
+        return 0
+    l = (d - 1).bit_length()
+    magic = (((1 << l) - d) << 64) // d + 1
+    assert magic < 2**64
+    t1 = (magic * n) >> 64
+    q = (t1 + ((n - t1) >> 1)) >> (l - 1)
+    return n - q * d
+
+
+@pytest.mark.parametrize("d", [1, 2, 3, 7, 10, 100_000, 2**32 - 1, 2**32 + 15, 2**63 - 25, 2**63,
+                               2**63 + 1, 2**64 - 1])
+def test_invariant_divisor_mod(d):
+    g = np.random.Generator(np.random.PCG64(d % 1000))
+    ns = [0, 1, d - 1, d, d + 1, 2**64 - 1, 2**63, 2**63 - 1]
+    ns += [int(x) for x in g.integers(0, 2**64 - 1, size=300, dtype=np.uint64)]
+    for n in ns:
+        n %= 2**64
+        assert _gm_mod(n, d) == n % d
+
+
+# ------------------------------------------------------------ segment reduce
+def _brute_segment(data, indices, seg, batch, combiner):
+    """float32 scalar loop: out[seg] += row, in index order; mean *= 1/count."""
+    out = np.zeros((batch, data.shape[1]), dtype=np.float32)
+    cnt = np.zeros(batch, dtype=np.int64)
+    for i in range(len(indices)):
+        s = int(seg[i])
+        cnt[s] += 1
+        for d in range(data.shape[1]):
+            out[s, d] = np.float32(out[s, d] + data[indices[i], d])
+    if combiner == 1:
+        for s in range(batch):
+            if cnt[s]:
+                inv = np.float32(1.0) / np.float32(cnt[s])
+                out[s] = (out[s] * inv).astype(np.float32)
+    return out
+
+
+@pytest.mark.parametrize("case", _load("segment_reduce_reference_gtest.json")["cases"],
+                         ids=lambda c: c["name"])
+def test_segment_reduce_reference_goldens(case):
+    data = np.asarray(case["data"], dtype=np.float32)
+    idx = np.asarray(case["indices"], dtype=np.int32)
+    sl = np.asarray(case["slice_input"], dtype=np.int64)
+    seg = sl[:, case["begin"][1]]
+    batch = int(seg.max()) + 1
+    out = ora.segment_reduce(data, idx, seg, batch, case["combiner"])
+    np.testing.assert_array_equal(out, np.asarray(case["expected"], dtype=np.float32))
+
+
+@pytest.mark.parametrize("combiner", [0, 1])
+def test_segment_reduce_matches_brute_force(combiner):
+    g = np.random.Generator(np.random.PCG64(7))
+    data = g.standard_normal((50, 5)).astype(np.float32)
+    n = 200
+    indices = g.integers(0, 50, size=n).astype(np.int64)
+    seg = g.integers(0, 30, size=n).astype(np.int64)  # unsorted on purpose
+    out = ora.segment_reduce(data, indices, seg, 30, combiner)
+    np.testing.assert_array_equal(out, _brute_segment(data, indices, seg, 30, combiner))
+
+
+@pytest.mark.parametrize("combiner", [0, 1])
+def test_embedding_bag_equals_segment_reduce(combiner):
+    g = np.random.Generator(np.random.PCG64(11))
+    table = g.standard_normal((1000, 12)).astype(np.float32)
+    lens = g.integers(0, 9, size=64)
+    offsets = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    ids = g.integers(0, 1000, size=int(offsets[-1])).astype(np.int64)
+    seg = np.repeat(np.arange(64), lens).astype(np.int64)
+    a = ora.embedding_bag(table, ids, offsets, combiner)
+    b = ora.segment_reduce(table, ids, seg, 64, combiner)
+    np.testing.assert_array_equal(a, b)
+    # thread count does not change the per-bag order
+    np.testing.assert_array_equal(a, ora.embedding_bag(table, ids, offsets, combiner, threads=4))
+
+
+# ------------------------------------------------------------ pooling / masked gather
+def _brute_pooling(ids, g, ss, sl):
+    m, k = ids.shape
+    n = g.shape[2]
+    out = np.zeros((m, n), dtype=np.float32)
+    for i in range(m):
+        red = np.float32(0)
+        for j in range(k):
+            red = np.float32(red + np.float32(ids[i, j] > 0))
+        for p in range(n):
+            s = np.float32(0)
+            for j in range(k):
+                take = (ss[0] <= i < sl[0]) and (ss[1] <= j < sl[1]) and (ss[2] <= p < sl[2]) \
+                    and ids[i, j] > 0
+                s = np.float32(s + (g[i, j, p] if take else np.float32(0)))
+            out[i, p] = np.float32(0) if red == 0 else np.float32(s / red)
+    return out
+
+
+def test_pooling_matches_brute_force():
+    g = np.random.Generator(np.random.PCG64(5))
+    ids = g.integers(-3, 6, size=(6, 7)).astype(np.int64)
+    ids[2] = 0  # a row without positive ids pools to 0
+    gathered = g.standard_normal((6, 7, 5)).astype(np.float32)
+    for ss, sl in [((0, 0, 0), (6, 7, 5)), ((1, 2, 1), (5, 6, 4))]:
+        np.testing.assert_array_equal(ora.pooling(ids, gathered, ss, sl),
+                                      _brute_pooling(ids, gathered, ss, sl))
+
+
+def test_sparse_embedding2_mask_semantics():
+    table = np.arange(12, dtype=np.float32).reshape(4, 3) - 5.0
+    ids = np.array([0, 3, -1, 4, 2], dtype=np.int64)
+    out = ora.sparse_embedding2(table, ids, fallback=1)
+    np.testing.assert_array_equal(out[0], table[0])
+    np.testing.assert_array_equal(out[1], table[3])
+    # invalid ids multiply the fallback row by 0.0: signed zeros of that row
+    np.testing.assert_array_equal(out[2], table[1] * np.float32(0))
+    assert np.signbit(out[2]).tolist() == np.signbit(table[1] * np.float32(0)).tolist()
+    np.testing.assert_array_equal(out[4], table[2])
+
+
+# ------------------------------------------------------------ hash-bucket ops
+def test_embedding_with_hash_bucket_closed_form():
+    g = np.random.Generator(np.random.PCG64(2))
+    weight = g.standard_normal((50, 4)).astype(np.float32)
+    strs = [b"alpha", b"", b"1234567890123456789", b"x"]
+    out = ora.embedding_with_hash_bucket(strs, weight, 50)
+    for i, s in enumerate(strs):
+        want = np.zeros(4, np.float32) if not s else weight[ora.fingerprint64(s) % 50]
+        np.testing.assert_array_equal(out[i], want)
+
+
+def test_sparse_embedding_zero_bucket_quirk():
+    # find a non-empty string whose bucket is 0 for num_buckets = 3
+    zero = next(s for s in (str(i).encode() for i in range(1000))
+                if ora.fingerprint64(s) % 3 == 0)
+    nz = next(s for s in (str(i).encode() for i in range(1000))
+              if ora.fingerprint64(s) % 3 != 0)
+    idx, vals, empty, shape = ora.sparse_embedding([nz, b"", zero, nz], 3)
+    assert shape.tolist() == [4, 1]
+    assert idx.tolist() == [[0, 0], [1, 0], [2, 0], [3, 0]]
+    b = ora.fingerprint64(nz) % 3
+    assert vals.tolist() == [b, 0, b]  # the bucket-0 string adds no value
+    assert empty.tolist() == [False, True, False]
+
+
+# ------------------------------------------------------------ GEMM via OpenBLAS
+def test_openblas_is_0_3_29():
+    assert "0.3.29" in ora.blas_config()
+
+
+@pytest.mark.parametrize("m,n,k", [(512, 256, 256), (37, 45, 19), (1, 7, 300)])
+def test_gemm_oracle_against_float64(m, n, k):
+    g = np.random.Generator(np.random.PCG64(m * n))
+    a = g.standard_normal((m, k)).astype(np.float32)
+    b = g.standard_normal((k, n)).astype(np.float32)
+    e = g.standard_normal((m, n)).astype(np.float32)
+    ref = a.astype(np.float64) @ b.astype(np.float64)
+    bound = 1e-5 * (np.abs(a).astype(np.float64) @ np.abs(b).astype(np.float64)) + 1e-6
+    assert np.all(np.abs(ora.matmul(a, b) - ref) <= bound)
+    assert np.all(np.abs(ora.matmul_add(e, a, b) - (ref + e)) <= bound + 1e-6 * np.abs(e))
+    r = ora.matmul_add_relu(e, a, b)
+    assert np.all(r >= 0)
+    assert np.all(np.abs(r - np.maximum(ref + e, 0)) <= bound + 1e-6 * np.abs(e))
+
+
+def test_batch_matmul_oracle_is_loop():
+    g = np.random.Generator(np.random.PCG64(9))
+    a = g.standard_normal((3, 10, 8)).astype(np.float32)
+    b = g.standard_normal((3, 8, 12)).astype(np.float32)
+    out = ora.batch_matmul(a, b)
+    for i in range(3):
+        np.testing.assert_array_equal(out[i], ora.matmul(a[i], b[i]))
+
+
+def test_dense_layer_relu_and_sigmoid():
+    g = np.random.Generator(np.random.PCG64(4))
+    a = g.standard_normal((20, 16)).astype(np.float32)
+    w = g.standard_normal((16, 9)).astype(np.float32)
+    bias = g.standard_normal(9).astype(np.float32)
+    lin = ora.dense_layer(a, w, bias, 0)
+    np.testing.assert_allclose(lin, a.astype(np.float64) @ w + bias, rtol=1e-5, atol=1e-5)
+    np.testing.assert_array_equal(ora.dense_layer(a, w, bias, 1), np.where(lin < 0, 0, lin))
+    np.testing.assert_allclose(ora.dense_layer(a, w, bias, 2), 1 / (1 + np.exp(-lin.astype(np.float64))),
+                               rtol=1e-6, atol=1e-7)
