@@ -63,9 +63,10 @@ def graph_time_ms(make_fn, launches: int, replays: int):
     return e0.elapsed_time(e1) / (launches * replays)
 
 
-def read_traffic(kernel_tag: str):
-    """HBM bytes per launch from a committed rocprofv3 --pmc summary, if any."""
-    path = os.path.join(ROOT, "profiles", f"{kernel_tag}_pmc.md")
+def read_traffic(profile: str):
+    """HBM bytes per launch (calibrated FETCH_SIZE + WRITE_SIZE) from the
+    committed rocprofv3 --pmc summary profiles/<profile>.md, if present."""
+    path = os.path.join(ROOT, "profiles", f"{profile}.md")
     if not os.path.exists(path):
         return None
     m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", open(path).read())
@@ -118,7 +119,7 @@ def bench_tower(args, device):
         "peak": FP32_MFMA_PEAK_TFLOPS,
         "unit": "TFLOP/s",
         "frac": round(achieved / FP32_MFMA_PEAK_TFLOPS, 4),
-        "traffic": read_traffic("gemm_layer1"),
+        "traffic": read_traffic("gemm_layer1_4096x512x1024"),
         "avg_launch_us": round(k1_ms * 1e3, 3),
         "flops_per_launch": k1_flops,
     }
@@ -310,6 +311,68 @@ def cpu_baseline(inputs, bag_inputs):
     return out
 
 
+KERNELS = ("gemm_l1", "gemm_l2", "bag_sum", "bag_mean", "hashed", "copy")
+
+
+def profile_kernel(name: str, launches: int, device) -> dict:
+    """Launch one hot-path kernel `launches` times back to back, eagerly, for
+    rocprofv3 (--kernel-trace --stats, or --pmc FETCH_SIZE / WRITE_SIZE).
+
+    `copy` is the calibration kernel for the PMC byte counters: torch's copy
+    of a 256 MiB float32 buffer, which reads and writes exactly 256 MiB."""
+    import torch
+    from annc_amd import EPI_RELU, workloads
+    from annc_amd import device as dev
+
+    info: dict = {"kernel": name, "launches": launches}
+    if name in ("gemm_l1", "gemm_l2"):
+        w = workloads.config2(seed=0)
+        li = 0 if name == "gemm_l1" else 1
+        x = torch.from_numpy(w.x).to(device)
+        if li == 1:
+            x = torch.relu(x[:, :512]).contiguous()
+        wt = dev.pack_weight(torch.from_numpy(w.weights[li]).to(device))
+        bias = torch.from_numpy(w.biases[li]).to(device)
+        out = torch.empty((x.shape[0], wt.n), dtype=torch.float32, device=device)
+        fn = lambda: dev.gemm(x, wt, bias=bias, epilogue=EPI_RELU, out=out)  # noqa: E731
+        info.update(m=x.shape[0], n=wt.n, k=wt.k, flops_per_launch=2 * x.shape[0] * wt.n * wt.k)
+    elif name in ("bag_sum", "bag_mean"):
+        w = workloads.config3(seed=0)
+        table = torch.from_numpy(w.table).to(device)
+        ids = torch.from_numpy(w.ids).to(device)
+        offs = torch.from_numpy(w.offsets).to(device)
+        nnz, bags, dim = int(w.offsets[-1]), w.offsets.size - 1, w.table.shape[1]
+        out = torch.empty((bags, dim), dtype=torch.float32, device=device)
+        comb = 0 if name == "bag_sum" else 1
+        fn = lambda: dev.embedding_bag(table, ids, offs, comb, out=out)  # noqa: E731
+        info.update(algorithmic_bytes=8 * nnz + 8 * (bags + 1) + 4 * dim * nnz + 4 * dim * bags)
+    elif name == "hashed":
+        w = workloads.config4(seed=0)
+        tables = [torch.from_numpy(t).to(device) for t in w.tables]
+        ids = torch.from_numpy(w.ids).to(device)
+        offs = torch.from_numpy(w.offsets).to(device)
+        nf = len(tables)
+        out = torch.empty((w.batch, nf * w.dim), dtype=torch.float32, device=device)
+        nb = [w.num_buckets] * nf
+        fn = lambda: dev.hashed_embedding_bags(tables, nb, ids, offs, w.batch, 1,  # noqa: E731
+                                               out=out)
+        nnz = int(w.offsets[-1])
+        info.update(algorithmic_bytes=8 * nnz + 8 * (nf * w.batch + 1) + 4 * w.dim * nnz
+                    + 4 * w.batch * nf * w.dim)
+    elif name == "copy":
+        src = torch.ones(64 << 20, dtype=torch.float32, device=device)
+        dst = torch.empty_like(src)
+        fn = lambda: dst.copy_(src)  # noqa: E731
+        info.update(bytes_read=src.numel() * 4, bytes_written=dst.numel() * 4)
+    else:
+        raise ValueError(f"unknown kernel {name!r}; choose from {KERNELS}")
+    torch.cuda.synchronize()
+    for i in range(launches):
+        fn()
+    torch.cuda.synchronize()
+    return info
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -317,6 +380,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--no-components", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--kernel", choices=KERNELS, default=None,
+                    help="profiling mode: launch only this kernel --launches times")
+    ap.add_argument("--launches", type=int, default=20)
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build targets one GPU; --gpus must be 1 "
@@ -328,6 +394,9 @@ def main() -> int:
         return 1
     device = torch.device("cuda:0")
     torch.cuda.set_device(device)
+    if args.kernel:
+        print(json.dumps(profile_kernel(args.kernel, args.launches, device)), flush=True)
+        return 0
 
     tower = bench_tower(args, device)
     components = {}
