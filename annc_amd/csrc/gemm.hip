@@ -322,6 +322,250 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemmParams p) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Packed-B pipelined kernel (the __layout_matmul path, N % 32 == 0).
+//
+// Operand tiles stream global -> LDS through gfx950's 16-byte LDS-DMA loads
+// (global_load_lds_dwordx4: lane i of a wave writes bytes [16i, 16i+16) of a
+// 1 KiB LDS block), S stages deep, so no VGPRs stage the data and up to S-1
+// k-blocks are in flight while the MFMAs run on the oldest.  One barrier per
+// k-block: a wave waits for its own DMAs of stage kt (vmcnt), the barrier
+// publishes everyone's, and only then is the slot freed by stage kt-1
+// refilled.
+//   * A block = 8 full rows x 32 k (eight 128-byte lines per instruction);
+//     lane i loads row i/8, 16-byte chunk (i%8) ^ swz(row), so each MFMA
+//     fragment read (row = lane%32, chunk 4*(lane/32)+q) hits 64 distinct
+//     banks: swz(row) = (row & 7) ^ ((row >> 3) & 1).
+//   * B block = 1 KiB of the packed panel, already in MFMA-fragment order.
+//   * The DMAs are inline asm so the compiler neither tracks them nor adds
+//     its conservative vmcnt(0) before LDS reads; the kernel counts them
+//     itself (wait_vmcnt) and fences the barrier as asm as well.
+//   * Rows past M and panels past N are clamped for loading and never
+//     stored; a K tail (K % 32) is folded in after the loop from the
+//     packed format's row-major tail region with guarded loads.
+// ---------------------------------------------------------------------------
+namespace pipe {
+
+__device__ __forceinline__ uint32_t lds_offset(const void* p) {
+  return static_cast<uint32_t>(
+      reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) void*)p));
+}
+
+// 16 bytes per lane from `src` into LDS at `lds_base + 16*lane`; lds_base is
+// wave-uniform.
+__device__ __forceinline__ void dma16(const void* src, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+               :
+               : "v"(src), "s"(lds_base)
+               : "memory");
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+__device__ __forceinline__ void block_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+__device__ __forceinline__ int a_swizzle(int row) { return (row & 7) ^ ((row >> 3) & 1); }
+
+}  // namespace pipe
+
+template <int WM, int WN, int BLK_M, int BLK_N, int S>
+__global__ __launch_bounds__(64 * WM * WN) void gemm_packed_pipe_kernel(GemmParams p) {
+  constexpr int NW = WM * WN;
+  constexpr int BM = WM * BLK_M * 32, BN = WN * BLK_N * 32;
+  constexpr int NA = BM / 8, NB = BN / 8, NBLK = NA + NB;  // 1 KiB blocks per stage
+  static_assert(NBLK % NW == 0, "stage blocks split evenly over the waves");
+  static_assert(S >= 2 && S <= 4, "2..4 stages");
+  constexpr int LPW = NBLK / NW;                    // DMA instructions per wave per stage
+  constexpr uint32_t kStageBytes = NBLK * 1024;
+  __shared__ __attribute__((aligned(1024))) f32x4 lds[S][NBLK * 64];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / WN;
+  const int wn = wave % WN;
+  const int l32 = lane & 31;
+  const int half = lane >> 5;
+
+  int tile = blockIdx.x;
+  const int T = p.tiles_m * p.tiles_n;
+  if ((T & 7) == 0) tile = (tile & 7) * (T >> 3) + (tile >> 3);
+  const int m0 = (tile / p.tiles_n) * BM;
+  const int n0 = (tile % p.tiles_n) * BN;
+  const int64_t z = blockIdx.z;
+  const float* __restrict__ A = p.a + z * p.stride_a;
+  const float* __restrict__ B = p.b + z * p.stride_b;
+  const int M = p.m, N = p.n, K = p.k;
+  const int KT = K >> 5;          // full k-blocks
+  const int panels = N >> 5;      // N % 32 == 0 on this path
+
+  // bias of this lane's columns, fetched before the pipeline starts
+  float bias_v[BLK_N];
+#pragma unroll
+  for (int j = 0; j < BLK_N; ++j) {
+    const int col = n0 + wn * BLK_N * 32 + j * 32 + l32;
+    bias_v[j] = (p.bias && col < N) ? p.bias[col] : 0.0f;
+  }
+
+  // this wave's DMA sources (advanced by one k-block per stage) and LDS slots
+  const float* src[LPW];
+  int step[LPW];
+  uint32_t dst[LPW];
+#pragma unroll
+  for (int i = 0; i < LPW; ++i) {
+    const int b = wave + NW * i;
+    dst[i] = __builtin_amdgcn_readfirstlane(pipe::lds_offset(&lds[0][b * 64]));
+    if (b < NA) {
+      const int trow = b * 8 + (lane >> 3);
+      const int chunk = (lane & 7) ^ pipe::a_swizzle(trow);
+      const int row = min(m0 + trow, M - 1);
+      src[i] = A + (int64_t)row * p.lda + chunk * 4;
+      step[i] = 32;
+    } else {
+      const int bb = b - NA;
+      const int pn = min((n0 >> 5) + (bb >> 2), panels - 1);
+      src[i] = B + (int64_t)pn * KT * 1024 + (bb & 3) * 256 + lane * 4;
+      step[i] = 1024;
+    }
+  }
+  auto issue = [&](int slot, int kt) {
+#pragma unroll
+    for (int i = 0; i < LPW; ++i)
+      pipe::dma16(src[i] + (int64_t)kt * step[i], dst[i] + slot * kStageBytes);
+  };
+
+  // fragment addressing (f32x4 units inside a stage)
+  int a_off[BLK_M], a_swz[BLK_M];
+#pragma unroll
+  for (int i = 0; i < BLK_M; ++i) {
+    const int trow = (wm * BLK_M + i) * 32 + l32;
+    a_off[i] = (trow >> 3) * 64 + (trow & 7) * 8;
+    a_swz[i] = pipe::a_swizzle(trow);
+  }
+
+  f32x16 acc[BLK_M][BLK_N];
+#pragma unroll
+  for (int i = 0; i < BLK_M; ++i)
+#pragma unroll
+    for (int j = 0; j < BLK_N; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  auto compute = [&](int slot) {
+    const f32x4* cur = lds[slot];
+    f32x4 af[2][BLK_M], bf[2][BLK_N];
+    auto frag = [&](int q, int buf) {
+#pragma unroll
+      for (int i = 0; i < BLK_M; ++i) af[buf][i] = cur[a_off[i] + ((4 * half + q) ^ a_swz[i])];
+#pragma unroll
+      for (int j = 0; j < BLK_N; ++j) bf[buf][j] = cur[(NA + (wn * BLK_N + j) * 4 + q) * 64 + lane];
+    };
+    frag(0, 0);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      if (q < 3) frag(q + 1, (q + 1) & 1);
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+#pragma unroll
+        for (int i = 0; i < BLK_M; ++i)
+#pragma unroll
+          for (int j = 0; j < BLK_N; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[q & 1][i][e], bf[q & 1][j][e],
+                                                             acc[i][j], 0, 0, 0);
+      if (q < 3) {
+        // one fragment read between consecutive MFMAs, then the rest
+#pragma unroll
+        for (int r = 0; r < BLK_M + BLK_N; ++r) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, 4 * BLK_M * BLK_N - (BLK_M + BLK_N), 0);
+      }
+    }
+  };
+
+#pragma unroll
+  for (int s = 0; s < S - 1; ++s)
+    if (s < KT) issue(s, s);
+  for (int kt0 = 0; kt0 < KT; kt0 += S) {
+#pragma unroll
+    for (int u = 0; u < S; ++u) {
+      const int kt = kt0 + u;
+      if (kt < KT) {
+        // stages kt+1 .. kt+S-2 may stay in flight
+        const int after = min(KT - 1 - kt, S - 2);
+        if (after >= 2)
+          pipe::wait_vmcnt<2 * LPW>();
+        else if (after == 1)
+          pipe::wait_vmcnt<LPW>();
+        else
+          pipe::wait_vmcnt<0>();
+        pipe::block_barrier();
+        if (kt + S - 1 < KT) issue((u + S - 1) % S, kt + S - 1);
+        compute(u);
+      }
+    }
+  }
+
+  // K tail (K % 32 != 0): packed rows k >= 32*KT are row-major [K - 32*KT, N]
+  if (K & 31) {
+    const int kf = KT * 32;
+    const int64_t tail_base = (int64_t)N * kf;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      f32x4 af[BLK_M], bf[BLK_N];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int kk = 16 * half + 4 * q + e;
+        const bool kin = kf + kk < K;
+#pragma unroll
+        for (int i = 0; i < BLK_M; ++i) {
+          const int row = m0 + (wm * BLK_M + i) * 32 + l32;
+          af[i][e] = (kin && row < M) ? A[(int64_t)row * p.lda + kf + kk] : 0.0f;
+        }
+#pragma unroll
+        for (int j = 0; j < BLK_N; ++j) {
+          const int col = n0 + (wn * BLK_N + j) * 32 + l32;
+          bf[j][e] = (kin && col < N) ? B[tail_base + (int64_t)kk * N + col] : 0.0f;
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+#pragma unroll
+        for (int i = 0; i < BLK_M; ++i)
+#pragma unroll
+          for (int j = 0; j < BLK_N; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i][e], bf[j][e], acc[i][j], 0, 0, 0);
+    }
+  }
+
+  // fused epilogue
+  const float* __restrict__ E = p.e ? p.e + z * p.stride_e : nullptr;
+  float* __restrict__ C = p.c + z * p.stride_c;
+#pragma unroll
+  for (int i = 0; i < BLK_M; ++i) {
+#pragma unroll
+    for (int j = 0; j < BLK_N; ++j) {
+      const int col = n0 + wn * BLK_N * 32 + j * 32 + l32;
+      if (col >= N) continue;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = m0 + wm * BLK_M * 32 + i * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+        if (row >= M) continue;
+        float v = acc[i][j][r];
+        if (E) v += E[(int64_t)row * p.lde + col];
+        if (p.bias) v += bias_v[j];
+        C[(int64_t)row * p.ldc + col] = apply_epilogue(v, p.epilogue);
+      }
+    }
+  }
+}
+
 __global__ void pack_rhs_kernel(const float* __restrict__ src, float* __restrict__ dst, int64_t K,
                                 int64_t N) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -341,6 +585,31 @@ int launch_tile(const GemmParams& p0, int64_t batch, hipStream_t stream) {
                      stream, p);
   ANNC_HIP_TRY(hipGetLastError());
   return ANNC_OK;
+}
+
+template <int WM, int WN, int BMB, int BNB, int S>
+int launch_pipe(const GemmParams& p0, int64_t batch, hipStream_t stream) {
+  constexpr int BM = WM * BMB * 32, BN = WN * BNB * 32;
+  GemmParams p = p0;
+  p.tiles_m = (p.m + BM - 1) / BM;
+  p.tiles_n = (p.n + BN - 1) / BN;
+  dim3 grid(p.tiles_m * p.tiles_n, 1, (unsigned)batch);
+  hipLaunchKernelGGL((gemm_packed_pipe_kernel<WM, WN, BMB, BNB, S>), grid, dim3(64 * WM * WN), 0,
+                     stream, p);
+  ANNC_HIP_TRY(hipGetLastError());
+  return ANNC_OK;
+}
+
+// Packed B with N % 32 == 0 and 16-byte aligned A rows: the LDS-DMA pipeline.
+// Largest tile that still gives every CU (256 on MI355X) a workgroup.
+int launch_packed_pipe(const GemmParams& p, int64_t batch, hipStream_t stream) {
+  const int64_t cus = 256;
+  auto tiles = [&](int bm, int bn) {
+    return ((int64_t)(p.m + bm - 1) / bm) * ((p.n + bn - 1) / bn) * batch;
+  };
+  if (tiles(128, 128) >= cus) return launch_pipe<4, 2, 1, 2, 3>(p, batch, stream);
+  if (tiles(128, 64) >= cus) return launch_pipe<4, 2, 1, 1, 4>(p, batch, stream);
+  return launch_pipe<2, 2, 1, 1, 4>(p, batch, stream);
 }
 
 template <bool PACKED>
@@ -407,6 +676,7 @@ int annc_hip_gemm(void* stream, int64_t batch, int64_t m, int64_t n, int64_t k, 
   }
   if (b_packed) {
     ANNC_REQUIRE(aligned16(b) && stride_b % 4 == 0, "packed B must be 16-byte aligned");
+    if (n % 32 == 0 && p.a_vec) return launch_packed_pipe(p, batch, s);
     return launch_gemm<true>(p, batch, s);
   }
   return launch_gemm<false>(p, batch, s);

@@ -76,6 +76,47 @@ def test_layout_matmul_packed(m, n, k):
     assert_gemm_close(to_host(got), ref, gemm_bound(a, w))
 
 
+# Packed B with N % 32 == 0 and 16-byte aligned A rows runs the LDS-DMA
+# pipelined kernel: each of its three tile configurations (128x128, 128x64,
+# 64x64, chosen by how many tiles the shape yields), partial M and N tiles,
+# a K tail with and without full k-blocks, padded lda, addend and sigmoid.
+PIPE_CASES = [
+    (4096, 1024, 864, 864, "128x128 tiles"),
+    (4096, 512, 1024, 1024, "128x64 tiles"),
+    (4096, 256, 512, 516, "64x64 tiles, padded lda"),
+    (1000, 96, 845, 848, "partial M tile, partial N tile, K tail after 26 k-blocks"),
+    (65, 32, 31, 32, "K < 32: tail only"),
+    (33, 160, 64, 64, "2 k-blocks"),
+    (130, 64, 96, 100, "3 k-blocks (one full pipeline round), lda not a multiple of 32"),
+    (7, 64, 300, 300, "tiny M"),
+]
+
+
+@pytest.mark.parametrize("m,n,k,lda,what", PIPE_CASES)
+def test_layout_matmul_pipeline_edges(m, n, k, lda, what):
+    note(f"packed pipeline {m}x{n}x{k} lda={lda}: {what}")
+    g = workloads.rng(m + 3 * n + 7 * k)
+    buf = g.standard_normal((m, lda)).astype(np.float32)
+    a = np.ascontiguousarray(buf[:, :k])
+    w = (g.standard_normal((k, n)) * 0.05).astype(np.float32)
+    bias = g.standard_normal(n).astype(np.float32)
+    e = g.standard_normal((m, n)).astype(np.float32)
+    pw = dev.pack_weight(to_dev(w))
+    da = to_dev(buf)[:, :k]
+    ref = ora.dense_layer(a, w, bias, 1)
+    got = to_host(dev.gemm(da, pw, bias=to_dev(bias), epilogue=EPI_RELU))
+    assert_gemm_close(got, ref, gemm_bound(a, w, np.broadcast_to(bias, (m, n))))
+    # addend instead of bias, sigmoid epilogue
+    got = to_host(dev.gemm(da, pw, addend=to_dev(e), epilogue=EPI_SIGMOID))
+    lin = ora.matmul_add(e, a, w)
+    np.testing.assert_allclose(got, 1.0 / (1.0 + np.exp(-lin.astype(np.float64))), rtol=1e-4,
+                               atol=1e-5)
+    # the same numbers through the XLA custom call with host buffers
+    out = np.empty((m, n), np.float32)
+    xla.layout_matmul(a, dev.pack_weight_host(w), k, n, out)
+    assert_gemm_close(out, ora.matmul(a, w), gemm_bound(a, w))
+
+
 @pytest.mark.parametrize("batch,m,n,k", [(3, 40, 50, 60), (8, 64, 64, 64), (2, 8, 8, 8),
                                          (5, 100, 13, 200)])
 def test_batch_matmul(batch, m, n, k):
