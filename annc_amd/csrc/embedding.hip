@@ -14,12 +14,13 @@
 // consecutive floats of the row, so a row is one contiguous G*16-byte
 // (up to 1 KiB) read and one wave covers 64/G bags.  Every lane adds its
 // rows in index order, which reproduces the reference's summation order
-// exactly: the sum is bit-identical.  Eight row loads are issued before
-// the first add to keep them in flight together.
+// exactly: the sum is bit-identical.  The ids and rows of up to kGroupRound
+// positions are loaded before the first add, so they are in flight together.
 #include <hip/hip_runtime.h>
 #include <hipcub/hipcub.hpp>
 
 #include <algorithm>
+#include <utility>
 
 #include "common.h"
 #include "embedding_impl.h"
@@ -28,13 +29,24 @@ namespace annc {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kUnroll = 8;
+constexpr int kGroupRound = 32;  // bag positions whose loads are in flight together
+constexpr int kHalf = kGroupRound / 2;
+constexpr uint32_t kNoRow = 0xffffffffu;  // row number of a masked bag position
+
+// What masked bag positions read: zeros, so they add nothing.
+// (a plain __device__ array, so that it shares the global address space
+// with the table and selecting between the two keeps global loads).
+__device__ __align__(16) float g_zero_vec[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 
 template <int VEC>
 struct VecT;
 template <>
 struct VecT<4> {
   typedef float type __attribute__((ext_vector_type(4)));
+};
+template <>
+struct VecT<2> {
+  typedef float type __attribute__((ext_vector_type(2)));
 };
 template <>
 struct VecT<1> {
@@ -51,13 +63,31 @@ __device__ __forceinline__ void store_row(float* p, typename VecT<VEC>::type v) 
   *reinterpret_cast<typename VecT<VEC>::type*>(p) = v;
 }
 
-template <typename IdxT>
-__device__ __forceinline__ int64_t fetch_id(const IdxT* __restrict__ ids,
-                                            const int32_t* __restrict__ perm, int64_t j) {
-  return perm ? static_cast<int64_t>(ids[perm[j]]) : static_cast<int64_t>(ids[j]);
+template <typename F, int... U>
+__device__ __forceinline__ void static_for(F&& f, std::integer_sequence<int, U...>) {
+  (f(std::integral_constant<int, U>{}), ...);
 }
 
-template <typename IdxT, int G, int VEC, bool MEAN>
+// The value `v` holds in lane U of this lane's aligned group of G lanes.
+// For G = 16 the group is a DPP row and row_newbcast is one VALU move;
+// other widths go through the LDS permute network (ds_bpermute).
+template <int G, int U>
+__device__ __forceinline__ uint32_t group_bcast(uint32_t v) {
+  if constexpr (G == 16)
+    return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(v), 0x150 + U, 0xF, 0xF, false));
+  else
+    return static_cast<uint32_t>(__shfl(static_cast<int>(v), U, G));
+}
+
+
+// One bag per group of G lanes (64/G bags share a wave).  The bag is walked
+// in rounds of kGroupRound positions: the round's ids are fetched (clamped
+// into the bag, so every load is valid and no per-position exec mask is
+// needed; lanes fetch distinct ids and broadcast them inside the group),
+// then all of the round's row chunks, and only then are the first
+// `cnt` rows added in index order.  A bag of n ids costs ceil(n/32) id->row
+// round trips.
+template <typename IdxT, int G, int VEC, bool MEAN, bool PERM>
 __global__ __launch_bounds__(kThreads) void bag_kernel(
     const float* __restrict__ table, int64_t rows, int64_t dim, const IdxT* __restrict__ ids,
     const int32_t* __restrict__ perm, const int64_t* __restrict__ offsets, int64_t num_bags,
@@ -69,37 +99,60 @@ __global__ __launch_bounds__(kThreads) void bag_kernel(
   const int64_t beg = offsets[bag];
   const int64_t end = offsets[bag + 1];
   bool bad = false;
-  for (int64_t c = (int64_t)g * VEC; c < dim; c += (int64_t)G * VEC) {
+  // Every lane of the group runs the same chunk and round loops (the row
+  // broadcasts read all G lanes); lanes past `dim` read the zero vector.
+  const uint32_t row_bytes = static_cast<uint32_t>(dim * sizeof(float));
+  for (int64_t c0 = 0; c0 < dim; c0 += (int64_t)G * VEC) {
+    const int64_t c = c0 + (int64_t)g * VEC;
+    const bool active = c < dim;
+    const char* base = reinterpret_cast<const char*>(table + (active ? c : 0));
+    const char* zero = reinterpret_cast<const char*>(g_zero_vec);
     V acc = V(0.0f);
-    int64_t j = beg;
-    for (; j + kUnroll <= end; j += kUnroll) {
-      int64_t r[kUnroll];
+    for (int64_t j0 = beg; j0 < end; j0 += kGroupRound) {
+      const int cnt = static_cast<int>(end - j0 < kGroupRound ? end - j0 : kGroupRound);
+      // the second half of the round is loaded only if a bag of this wave needs it
+      const bool more = __ballot(cnt > kHalf) != 0;
+      // Lane g of the group fetches positions g, g+G, ... of the round (one
+      // coalesced load per slot) and turns each into a 32-bit row number, or
+      // kNoRow for positions past the bag and ids outside the table.
+      constexpr int kPer = (kGroupRound + G - 1) / G;
+      uint32_t mine[kPer];
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u) r[u] = fetch_id(ids, perm, j + u);
-      V v[kUnroll];
-#pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
-        const bool ok = static_cast<uint64_t>(r[u]) < static_cast<uint64_t>(rows);
-        bad |= !ok;
-        v[u] = ok ? load_row<VEC>(table + r[u] * dim + c) : V(0.0f);
+      for (int t = 0; t < kPer; ++t) {
+        const int pos = g + G * t;
+        const int64_t at = j0 + min(pos, cnt - 1);
+        const int64_t id = PERM ? static_cast<int64_t>(ids[perm[at]]) : static_cast<int64_t>(ids[at]);
+        const bool ok = static_cast<uint64_t>(id) < static_cast<uint64_t>(rows);
+        bad |= pos < cnt && !ok;
+        mine[t] = (pos < cnt && ok) ? static_cast<uint32_t>(id) : kNoRow;
       }
+      // position u comes from lane u % G, slot u / G; kNoRow reads zeros, so
+      // the adds below need no mask (x + 0.0f == x for the +0-seeded sums)
+      V v[kGroupRound];
+      auto gather = [&](auto first) {
+        static_for([&](auto uc) {
+          constexpr int u = decltype(first)::value + decltype(uc)::value;
+          const uint32_t row = group_bcast<G, u % G>(mine[u / G]);
+          const bool take = row != kNoRow && active;
+          const uint64_t off = static_cast<uint64_t>(take ? row : 0u) * row_bytes;
+          const char* src = (take ? base : zero) + off;
+          v[u] = load_row<VEC>(reinterpret_cast<const float*>(src));
+        }, std::make_integer_sequence<int, kHalf>{});
+      };
+      gather(std::integral_constant<int, 0>{});
+      if (more) gather(std::integral_constant<int, kHalf>{});
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u) acc += v[u];
-    }
-    for (; j < end; ++j) {
-      const int64_t r = fetch_id(ids, perm, j);
-      const bool ok = static_cast<uint64_t>(r) < static_cast<uint64_t>(rows);
-      bad |= !ok;
-      if (ok) acc += load_row<VEC>(table + r * dim + c);
+      for (int u = 0; u < kHalf; ++u) acc += v[u];
+      if (more) {
+#pragma unroll
+        for (int u = kHalf; u < kGroupRound; ++u) acc += v[u];
+      }
     }
     if (MEAN) {
-      const int32_t cnt = static_cast<int32_t>(end - beg);
-      if (cnt > 0) {
-        const float inv = 1.0f / static_cast<float>(cnt);
-        acc *= inv;
-      }
+      const int32_t n = static_cast<int32_t>(end - beg);
+      if (n > 0) acc *= 1.0f / static_cast<float>(n);
     }
-    store_row<VEC>(out + bag * ldo + c, acc);
+    if (active) store_row<VEC>(out + bag * ldo + c, acc);
   }
   if (bad) atomicOr(status, 1);
 }
@@ -109,12 +162,11 @@ int launch_bag_g(const BagArgs& a, hipStream_t s) {
   const int64_t threads = a.num_bags * G;
   dim3 grid((unsigned)ceil_div(threads, kThreads));
   const IdxT* ids = static_cast<const IdxT*>(a.ids);
-  if (a.combiner == ANNC_COMBINER_MEAN)
-    hipLaunchKernelGGL((bag_kernel<IdxT, G, VEC, true>), grid, dim3(kThreads), 0, s, a.table,
-                       a.rows, a.dim, ids, a.perm, a.offsets, a.num_bags, a.out, a.ldo, a.status);
-  else
-    hipLaunchKernelGGL((bag_kernel<IdxT, G, VEC, false>), grid, dim3(kThreads), 0, s, a.table,
-                       a.rows, a.dim, ids, a.perm, a.offsets, a.num_bags, a.out, a.ldo, a.status);
+  const bool mean = a.combiner == ANNC_COMBINER_MEAN;
+  auto kernel = a.perm ? (mean ? bag_kernel<IdxT, G, VEC, true, true> : bag_kernel<IdxT, G, VEC, false, true>)
+                       : (mean ? bag_kernel<IdxT, G, VEC, true, false> : bag_kernel<IdxT, G, VEC, false, false>);
+  hipLaunchKernelGGL(kernel, grid, dim3(kThreads), 0, s, a.table, a.rows, a.dim, ids, a.perm,
+                     a.offsets, a.num_bags, a.out, a.ldo, a.status);
   ANNC_HIP_TRY(hipGetLastError());
   return ANNC_OK;
 }
@@ -131,9 +183,13 @@ int launch_bag_vec(const BagArgs& a, hipStream_t s) {
 
 template <typename IdxT>
 int launch_bag_idx(const BagArgs& a, hipStream_t s) {
-  auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
-  const bool vec = a.dim % 4 == 0 && a.ldo % 4 == 0 && al16(a.table) && al16(a.out);
-  return vec ? launch_bag_vec<IdxT, 4>(a, s) : launch_bag_vec<IdxT, 1>(a, s);
+  auto aligned = [](const void* p, int bytes) {
+    return (reinterpret_cast<uintptr_t>(p) & (bytes - 1)) == 0;
+  };
+  auto vec_ok = [&](int v) {
+    return a.dim % v == 0 && a.ldo % v == 0 && aligned(a.table, 4 * v) && aligned(a.out, 4 * v);
+  };
+  return vec_ok(4) ? launch_bag_vec<IdxT, 4>(a, s) : launch_bag_vec<IdxT, 1>(a, s);
 }
 
 // ---------------------------------------------------------------------------
@@ -236,6 +292,8 @@ __global__ __launch_bounds__(kThreads) void pooling_kernel(
 }  // namespace
 
 int launch_bag(const BagArgs& a, hipStream_t s) {
+  ANNC_REQUIRE(a.rows < static_cast<int64_t>(kNoRow), "tables of 2^32-1 rows or more are not supported");
+  ANNC_REQUIRE(a.dim < (int64_t(1) << 29), "embedding dim must be below 2^29");
   return a.ids_is_64 ? launch_bag_idx<int64_t>(a, s) : launch_bag_idx<int32_t>(a, s);
 }
 
