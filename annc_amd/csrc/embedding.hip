@@ -63,6 +63,32 @@ __device__ __forceinline__ void store_row(float* p, typename VecT<VEC>::type v) 
   *reinterpret_cast<typename VecT<VEC>::type*>(p) = v;
 }
 
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// Raw buffer load of VEC floats at byte offset `off` of `rsrc`; offsets at or
+// past the descriptor's byte count read zeros (hardware range check).
+template <int VEC>
+__device__ __forceinline__ typename VecT<VEC>::type buffer_row(__amdgpu_buffer_rsrc_t rsrc,
+                                                               uint32_t off) {
+  typedef typename VecT<VEC>::type V;
+  if constexpr (VEC == 4) {
+    const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rsrc, static_cast<int>(off), 0, 0);
+    return __builtin_bit_cast(V, v);
+  } else if constexpr (VEC == 2) {
+    const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(rsrc, static_cast<int>(off), 0, 0);
+    return __builtin_bit_cast(V, v);
+  } else {
+    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rsrc, static_cast<int>(off), 0, 0));
+  }
+}
+
+// dword3 of a raw (untyped, stride 0) buffer descriptor on gfx950.
+constexpr int kRawBufferFlags = 0x00020000;
+// Byte offset that a masked bag position carries: the buffer path is used
+// only for tables below 2 GiB, so it is always past the range check.
+constexpr uint32_t kMaskedOff = 0x80000000u;
+
 template <typename F, int... U>
 __device__ __forceinline__ void static_for(F&& f, std::integer_sequence<int, U...>) {
   (f(std::integral_constant<int, U>{}), ...);
@@ -87,7 +113,7 @@ __device__ __forceinline__ uint32_t group_bcast(uint32_t v) {
 // then all of the round's row chunks, and only then are the first
 // `cnt` rows added in index order.  A bag of n ids costs ceil(n/32) id->row
 // round trips.
-template <typename IdxT, int G, int VEC, bool MEAN, bool PERM>
+template <typename IdxT, int G, int VEC, bool MEAN, bool PERM, bool BUF>
 __global__ __launch_bounds__(kThreads) void bag_kernel(
     const float* __restrict__ table, int64_t rows, int64_t dim, const IdxT* __restrict__ ids,
     const int32_t* __restrict__ perm, const int64_t* __restrict__ offsets, int64_t num_bags,
@@ -102,11 +128,17 @@ __global__ __launch_bounds__(kThreads) void bag_kernel(
   // Every lane of the group runs the same chunk and round loops (the row
   // broadcasts read all G lanes); lanes past `dim` read the zero vector.
   const uint32_t row_bytes = static_cast<uint32_t>(dim * sizeof(float));
+  // BUF: the table is below 2 GiB, reached through a raw buffer descriptor
+  const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float*>(table), 0, static_cast<int>(BUF ? rows * row_bytes : 0), kRawBufferFlags);
   for (int64_t c0 = 0; c0 < dim; c0 += (int64_t)G * VEC) {
     const int64_t c = c0 + (int64_t)g * VEC;
     const bool active = c < dim;
     const char* base = reinterpret_cast<const char*>(table + (active ? c : 0));
     const char* zero = reinterpret_cast<const char*>(g_zero_vec);
+    // buffer path: byte offset of this lane's chunk; inactive lanes push every
+    // offset past the range check
+    const uint32_t c_off = active ? static_cast<uint32_t>(c * sizeof(float)) : kMaskedOff;
     V acc = V(0.0f);
     for (int64_t j0 = beg; j0 < end; j0 += kGroupRound) {
       const int cnt = static_cast<int>(end - j0 < kGroupRound ? end - j0 : kGroupRound);
@@ -124,7 +156,10 @@ __global__ __launch_bounds__(kThreads) void bag_kernel(
         const int64_t id = PERM ? static_cast<int64_t>(ids[perm[at]]) : static_cast<int64_t>(ids[at]);
         const bool ok = static_cast<uint64_t>(id) < static_cast<uint64_t>(rows);
         bad |= pos < cnt && !ok;
-        mine[t] = (pos < cnt && ok) ? static_cast<uint32_t>(id) : kNoRow;
+        if constexpr (BUF)
+          mine[t] = (pos < cnt && ok) ? static_cast<uint32_t>(id) * row_bytes : kMaskedOff;
+        else
+          mine[t] = (pos < cnt && ok) ? static_cast<uint32_t>(id) : kNoRow;
       }
       // position u comes from lane u % G, slot u / G; kNoRow reads zeros, so
       // the adds below need no mask (x + 0.0f == x for the +0-seeded sums)
@@ -132,11 +167,15 @@ __global__ __launch_bounds__(kThreads) void bag_kernel(
       auto gather = [&](auto first) {
         static_for([&](auto uc) {
           constexpr int u = decltype(first)::value + decltype(uc)::value;
-          const uint32_t row = group_bcast<G, u % G>(mine[u / G]);
-          const bool take = row != kNoRow && active;
-          const uint64_t off = static_cast<uint64_t>(take ? row : 0u) * row_bytes;
-          const char* src = (take ? base : zero) + off;
-          v[u] = load_row<VEC>(reinterpret_cast<const float*>(src));
+          if constexpr (BUF) {
+            v[u] = buffer_row<VEC>(rsrc, group_bcast<G, u % G>(mine[u / G]) + c_off);
+          } else {
+            const uint32_t row = group_bcast<G, u % G>(mine[u / G]);
+            const bool take = row != kNoRow && active;
+            const uint64_t off = static_cast<uint64_t>(take ? row : 0u) * row_bytes;
+            const char* src = (take ? base : zero) + off;
+            v[u] = load_row<VEC>(reinterpret_cast<const float*>(src));
+          }
         }, std::make_integer_sequence<int, kHalf>{});
       };
       gather(std::integral_constant<int, 0>{});
@@ -163,8 +202,15 @@ int launch_bag_g(const BagArgs& a, hipStream_t s) {
   dim3 grid((unsigned)ceil_div(threads, kThreads));
   const IdxT* ids = static_cast<const IdxT*>(a.ids);
   const bool mean = a.combiner == ANNC_COMBINER_MEAN;
-  auto kernel = a.perm ? (mean ? bag_kernel<IdxT, G, VEC, true, true> : bag_kernel<IdxT, G, VEC, false, true>)
-                       : (mean ? bag_kernel<IdxT, G, VEC, true, false> : bag_kernel<IdxT, G, VEC, false, false>);
+  // tables below 2 GiB go through the buffer path (masked positions read the
+  // range check's zeros)
+  const bool buf = a.rows * a.dim * static_cast<int64_t>(sizeof(float)) < (int64_t(1) << 31);
+  auto pick = [&](auto buf_tag) {
+    constexpr bool B = decltype(buf_tag)::value;
+    return a.perm ? (mean ? bag_kernel<IdxT, G, VEC, true, true, B> : bag_kernel<IdxT, G, VEC, false, true, B>)
+                  : (mean ? bag_kernel<IdxT, G, VEC, true, false, B> : bag_kernel<IdxT, G, VEC, false, false, B>);
+  };
+  auto kernel = buf ? pick(std::true_type{}) : pick(std::false_type{});
   hipLaunchKernelGGL(kernel, grid, dim3(kThreads), 0, s, a.table, a.rows, a.dim, ids, a.perm,
                      a.offsets, a.num_bags, a.out, a.ldo, a.status);
   ANNC_HIP_TRY(hipGetLastError());
