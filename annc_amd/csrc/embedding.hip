@@ -30,7 +30,7 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kGroupRound = 32;  // bag positions whose loads are in flight together
-constexpr int kHalf = kGroupRound / 2;
+constexpr int kQuarter = 8;  // granularity at which a round's row loads are skipped
 constexpr uint32_t kNoRow = 0xffffffffu;  // row number of a masked bag position
 
 // What masked bag positions read: zeros, so they add nothing.
@@ -142,50 +142,75 @@ __global__ __launch_bounds__(kThreads) void bag_kernel(
     V acc = V(0.0f);
     for (int64_t j0 = beg; j0 < end; j0 += kGroupRound) {
       const int cnt = static_cast<int>(end - j0 < kGroupRound ? end - j0 : kGroupRound);
-      // the second half of the round is loaded only if a bag of this wave needs it
-      const bool more = __ballot(cnt > kHalf) != 0;
-      // Lane g of the group fetches positions g, g+G, ... of the round (one
-      // coalesced load per slot) and turns each into a 32-bit row number, or
-      // kNoRow for positions past the bag and ids outside the table.
+      // Only the parts of the round that some bag of this wave reaches are
+      // loaded: id slot t if a bag has more than G*t positions left, row
+      // quarter q (positions 8q..8q+7) if one has more than 8q.
       constexpr int kPer = (kGroupRound + G - 1) / G;
+      constexpr int kQuarters = kGroupRound / kQuarter;
+      constexpr uint32_t kMasked = BUF ? kMaskedOff : kNoRow;
+      // Lane g of the group fetches positions g, g+G, ... of the round (one
+      // coalesced load per slot) and turns each into a byte offset (BUF) or a
+      // 32-bit row number, or the masked value for positions past the bag,
+      // ids outside the table and slots no bag of the wave reaches.
+      // (all of the round's id loads are issued before any is used, so the
+      // conversion below waits for them once)
+      int64_t idv[kPer];
+      bool loaded[kPer];
+      int64_t at[kPer];
+#pragma unroll
+      for (int t = 0; t < kPer; ++t) {
+        loaded[t] = t == 0 || __ballot(cnt > G * t) != 0;
+        at[t] = j0 + min(g + G * t, cnt - 1);
+      }
+      if constexpr (PERM) {
+        // every slot (clamped positions are valid): permuted positions first,
+        // then the ids they name, so each level is waited for once
+#pragma unroll
+        for (int t = 0; t < kPer; ++t) at[t] = perm[at[t]];
+#pragma unroll
+        for (int t = 0; t < kPer; ++t) idv[t] = static_cast<int64_t>(ids[at[t]]);
+      } else {
+#pragma unroll
+        for (int t = 0; t < kPer; ++t) idv[t] = loaded[t] ? static_cast<int64_t>(ids[at[t]]) : 0;
+      }
       uint32_t mine[kPer];
 #pragma unroll
       for (int t = 0; t < kPer; ++t) {
-        const int pos = g + G * t;
-        const int64_t at = j0 + min(pos, cnt - 1);
-        const int64_t id = PERM ? static_cast<int64_t>(ids[perm[at]]) : static_cast<int64_t>(ids[at]);
-        const bool ok = static_cast<uint64_t>(id) < static_cast<uint64_t>(rows);
-        bad |= pos < cnt && !ok;
-        if constexpr (BUF)
-          mine[t] = (pos < cnt && ok) ? static_cast<uint32_t>(id) * row_bytes : kMaskedOff;
-        else
-          mine[t] = (pos < cnt && ok) ? static_cast<uint32_t>(id) : kNoRow;
+        const bool in_bag = loaded[t] && g + G * t < cnt;
+        const bool ok = static_cast<uint64_t>(idv[t]) < static_cast<uint64_t>(rows);
+        bad |= in_bag && !ok;
+        const uint32_t row = static_cast<uint32_t>(idv[t]);
+        mine[t] = (in_bag && ok) ? (BUF ? row * row_bytes : row) : kMasked;
       }
-      // position u comes from lane u % G, slot u / G; kNoRow reads zeros, so
-      // the adds below need no mask (x + 0.0f == x for the +0-seeded sums)
+      // position u comes from lane u % G, slot u / G; masked positions read
+      // zeros, so the adds need no mask (x + 0.0f == x for the +0-seeded sums)
       V v[kGroupRound];
-      auto gather = [&](auto first) {
-        static_for([&](auto uc) {
-          constexpr int u = decltype(first)::value + decltype(uc)::value;
-          if constexpr (BUF) {
-            v[u] = buffer_row<VEC>(rsrc, group_bcast<G, u % G>(mine[u / G]) + c_off);
-          } else {
-            const uint32_t row = group_bcast<G, u % G>(mine[u / G]);
-            const bool take = row != kNoRow && active;
-            const uint64_t off = static_cast<uint64_t>(take ? row : 0u) * row_bytes;
-            const char* src = (take ? base : zero) + off;
-            v[u] = load_row<VEC>(reinterpret_cast<const float*>(src));
-          }
-        }, std::make_integer_sequence<int, kHalf>{});
-      };
-      gather(std::integral_constant<int, 0>{});
-      if (more) gather(std::integral_constant<int, kHalf>{});
+      bool need[kQuarters];
+      static_for([&](auto qc) {
+        constexpr int q = decltype(qc)::value;
+        need[q] = q == 0 || __ballot(cnt > kQuarter * q) != 0;
+        if (need[q]) {
+          static_for([&](auto uc) {
+            constexpr int u = kQuarter * q + decltype(uc)::value;
+            if constexpr (BUF) {
+              v[u] = buffer_row<VEC>(rsrc, group_bcast<G, u % G>(mine[u / G]) + c_off);
+            } else {
+              const uint32_t row = group_bcast<G, u % G>(mine[u / G]);
+              const bool take = row != kNoRow && active;
+              const uint64_t off = static_cast<uint64_t>(take ? row : 0u) * row_bytes;
+              const char* src = (take ? base : zero) + off;
+              v[u] = load_row<VEC>(reinterpret_cast<const float*>(src));
+            }
+          }, std::make_integer_sequence<int, kQuarter>{});
+        }
+      }, std::make_integer_sequence<int, kQuarters>{});
+      static_for([&](auto qc) {
+        constexpr int q = decltype(qc)::value;
+        if (need[q]) {
 #pragma unroll
-      for (int u = 0; u < kHalf; ++u) acc += v[u];
-      if (more) {
-#pragma unroll
-        for (int u = kHalf; u < kGroupRound; ++u) acc += v[u];
-      }
+          for (int u = kQuarter * q; u < kQuarter * (q + 1); ++u) acc += v[u];
+        }
+      }, std::make_integer_sequence<int, kQuarters>{});
     }
     if (MEAN) {
       const int32_t n = static_cast<int32_t>(end - beg);

@@ -179,17 +179,31 @@ struct Text24 {
   uint32_t len;
 };
 
-// x < 10^width rendered as `width` ASCII digits, first digit in byte 0.
-template <int WIDTH>
-__device__ __forceinline__ uint64_t ascii_digits(uint32_t x) {
-  uint64_t r = 0;
-#pragma unroll
-  for (int i = WIDTH - 1; i >= 0; --i) {
-    const uint32_t q = x / 10u;
-    r |= static_cast<uint64_t>(0x30u + (x - q * 10u)) << (8 * i);
-    x = q;
-  }
-  return r;
+// Two ASCII digits of p < 100, tens in the low byte: p / 10 as (p * 103) >> 10
+// (exact below 179) on the full-rate 24-bit multiplier.
+__device__ __forceinline__ uint32_t ascii_pair(uint32_t p) {
+  const uint32_t t = __umul24(p, 103u) >> 10;
+  return 0x3030u + t + ((p - __umul24(t, 10u)) << 8);
+}
+
+// x < 10^8 rendered as 8 ASCII digits, first digit in byte 0: one
+// multiply-high splits off the upper four digits, the rest are 24-bit
+// multiplies (x / 100 as (x * 5243) >> 19, exact below 43699).
+__device__ __forceinline__ uint64_t ascii8(uint32_t x) {
+  const uint32_t a = x / 10000u;
+  const uint32_t b = x - __umul24(a, 10000u);
+  const uint32_t a1 = __umul24(a, 5243u) >> 19, b1 = __umul24(b, 5243u) >> 19;
+  const uint32_t a2 = a - __umul24(a1, 100u), b2 = b - __umul24(b1, 100u);
+  const uint32_t lo = ascii_pair(a1) | (ascii_pair(a2) << 16);
+  const uint32_t hi = ascii_pair(b1) | (ascii_pair(b2) << 16);
+  return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+
+// x < 1000 rendered as 3 ASCII digits (x / 100 as (x * 41) >> 12, exact
+// below 1000).
+__device__ __forceinline__ uint64_t ascii3(uint32_t x) {
+  const uint32_t h = __umul24(x, 41u) >> 12;
+  return (0x30u + h) | (ascii_pair(x - __umul24(h, 100u)) << 8);
 }
 
 __device__ __forceinline__ uint32_t count_digits8(uint32_t x) {
@@ -200,11 +214,12 @@ __device__ __forceinline__ uint32_t count_digits8(uint32_t x) {
 __device__ __forceinline__ Text24 int64_text(int64_t v) {
   const bool neg = v < 0;
   const uint64_t u = neg ? (0ull - static_cast<uint64_t>(v)) : static_cast<uint64_t>(v);
+  // u = hi * 10^16 + mid * 10^8 + lo; 10^8 = 390625 * 2^8, so the second
+  // division runs on q1 >> 8 < 2^29 in 32 bits
   const uint64_t q1 = u / 100000000ull;
-  const uint32_t lo = static_cast<uint32_t>(u - q1 * 100000000ull);
-  const uint64_t q2 = q1 / 100000000ull;
-  const uint32_t mid = static_cast<uint32_t>(q1 - q2 * 100000000ull);
-  const uint32_t hi = static_cast<uint32_t>(q2);  // <= 922
+  const uint32_t lo = static_cast<uint32_t>(u) - static_cast<uint32_t>(q1) * 100000000u;
+  const uint32_t hi = static_cast<uint32_t>(q1 >> 8) / 390625u;  // <= 922
+  const uint32_t mid = static_cast<uint32_t>(q1) - (__umul24(hi, 390625u) << 8);
   uint32_t nd;
   if (hi)
     nd = 16u + 1u + (hi >= 10u) + (hi >= 100u);
@@ -213,9 +228,9 @@ __device__ __forceinline__ Text24 int64_text(int64_t v) {
   else
     nd = count_digits8(lo);
   // 19 zero-padded characters: hi(3) mid(8) lo(8).
-  const uint64_t d3 = ascii_digits<3>(hi);
-  const uint64_t m8 = ascii_digits<8>(mid);
-  const uint64_t l8 = ascii_digits<8>(lo);
+  const uint64_t d3 = ascii3(hi);
+  const uint64_t m8 = ascii8(mid);
+  const uint64_t l8 = ascii8(lo);
   const uint64_t p0 = d3 | (m8 << 24);
   const uint64_t p1 = (m8 >> 40) | (l8 << 24);
   const uint64_t p2 = l8 >> 40;
@@ -336,8 +351,106 @@ __global__ __launch_bounds__(kThreads) void gather_rows_kernel(const float* __re
 
 struct FieldSet {
   const float* table[kMaxFields];
+  int64_t rows[kMaxFields];
   U64Divisor div[kMaxFields];
 };
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+constexpr int kRawBufferFlags = 0x00020000;  // dword3 of a raw buffer descriptor (gfx950)
+constexpr uint32_t kMaskedOff = 0x80000000u;  // past the range check of any table < 2 GiB
+
+// Fused multi-field hash -> bucket -> gather -> pool, one run of consecutive
+// bags of one field per wave (G lanes per bag, 64/G bags).  The wave's bags
+// occupy a contiguous range of positions, so lane l loads and hashes
+// position wbeg + 64k + l -- every lane hashes one id per 64 positions, the
+// id loads are coalesced -- and turns the bucket into the byte offset of its
+// row.  Each bag group then walks its positions eight at a time, fetching
+// the offset from the lane that hashed it (ds_bpermute) and the row chunk
+// through a raw buffer load; positions past the bag carry an offset past
+// the buffer's range check and read zeros, which leave the +0-seeded,
+// index-ordered sums unchanged.
+template <int G, bool MEAN>
+__global__ __launch_bounds__(kThreads) void hashed_bags_wave_kernel(
+    FieldSet fs, int64_t field0, int64_t nfields, int64_t batch, int64_t dim,
+    int64_t waves_per_field, const int64_t* __restrict__ ids, const int64_t* __restrict__ offsets,
+    float* __restrict__ out, int64_t ldo, int64_t* __restrict__ buckets_out) {
+  typedef float f32x4 __attribute__((ext_vector_type(4)));
+  constexpr int NB = 64 / G;
+  const int lane = threadIdx.x & 63;
+  const int64_t w =
+      (int64_t)blockIdx.x * (kThreads / 64) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  if (w >= nfields * waves_per_field) return;
+  const int fl = static_cast<int>(w / waves_per_field);
+  const int64_t b0 = (w - (int64_t)fl * waves_per_field) * NB;
+  const int64_t f = field0 + fl;
+  const int64_t nbag = batch - b0 < NB ? batch - b0 : NB;  // bags of this wave
+  const int64_t wbeg = offsets[f * batch + b0];
+  const int64_t wend = offsets[f * batch + b0 + nbag];
+  const int grp = lane / G;
+  const int g = lane & (G - 1);
+  const bool bag_ok = grp < nbag;
+  const int64_t b = b0 + (bag_ok ? grp : 0);
+  const int64_t beg = bag_ok ? offsets[f * batch + b] : wend;
+  const int64_t end = bag_ok ? offsets[f * batch + b + 1] : wend;
+  const U64Divisor dv = fs.div[fl];
+  const uint32_t row_bytes = static_cast<uint32_t>(dim * sizeof(float));
+  const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float*>(fs.table[fl]), 0, static_cast<int>(fs.rows[fl] * row_bytes),
+      kRawBufferFlags);
+  float* __restrict__ dst = out + b * ldo + f * dim;
+  for (int64_t c0 = 0; c0 < dim; c0 += (int64_t)G * 4) {
+    const int64_t c = c0 + (int64_t)g * 4;
+    const bool active = c < dim;
+    const uint32_t c_off = active ? static_cast<uint32_t>(c * sizeof(float)) : kMaskedOff;
+    f32x4 acc = f32x4(0.0f);
+    for (int64_t k0 = wbeg; k0 < wend; k0 += 64) {
+      const int64_t p = k0 + lane;
+      const bool pv = p < wend;
+      const int64_t id = ids[pv ? p : wend - 1];
+      const uint64_t bucket = mod_invariant(fp64_text(int64_text(id)), dv);
+      if (buckets_out && pv && c0 == 0) buckets_out[p] = static_cast<int64_t>(bucket);
+      const uint32_t my_off = pv ? static_cast<uint32_t>(bucket) * row_bytes : kMaskedOff;
+      // this bag's positions inside the chunk: [lo, lo + cnt) relative to k0
+      const int64_t lo64 = beg > k0 ? beg : k0;
+      const int64_t hi64 = end < k0 + 64 ? end : k0 + 64;
+      const int cnt = hi64 > lo64 ? static_cast<int>(hi64 - lo64) : 0;
+      const int lo = static_cast<int>(lo64 - k0);
+      for (int u0 = 0; __ballot(cnt > u0) != 0; u0 += 8) {
+        f32x4 v[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const int u = u0 + i;
+          const uint32_t off = static_cast<uint32_t>(
+              __builtin_amdgcn_ds_bpermute(((lo + u) & 63) << 2, static_cast<int>(my_off)));
+          const u32x4 raw = __builtin_amdgcn_raw_buffer_load_b128(
+              rsrc, static_cast<int>((u < cnt ? off : kMaskedOff) + c_off), 0, 0);
+          v[i] = __builtin_bit_cast(f32x4, raw);
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc += v[i];
+      }
+    }
+    if (MEAN) {
+      const int32_t n = static_cast<int32_t>(end - beg);
+      if (n > 0) acc *= 1.0f / static_cast<float>(n);
+    }
+    if (active && bag_ok) *reinterpret_cast<f32x4*>(dst + c) = acc;
+  }
+}
+
+template <int G>
+void launch_hashed_wave_g(const FieldSet& fs, int64_t f0, int64_t nf, int64_t batch, int64_t dim,
+                          const int64_t* ids, const int64_t* offsets, int combiner, float* out,
+                          int64_t ldo, int64_t* buckets_out, hipStream_t s) {
+  const int64_t wpf = (batch + 64 / G - 1) / (64 / G);
+  dim3 grid((unsigned)ceil_div(nf * wpf, kThreads / 64));
+  if (combiner == ANNC_COMBINER_MEAN)
+    hipLaunchKernelGGL((hashed_bags_wave_kernel<G, true>), grid, dim3(kThreads), 0, s, fs, f0, nf,
+                       batch, dim, wpf, ids, offsets, out, ldo, buckets_out);
+  else
+    hipLaunchKernelGGL((hashed_bags_wave_kernel<G, false>), grid, dim3(kThreads), 0, s, fs, f0,
+                       nf, batch, dim, wpf, ids, offsets, out, ldo, buckets_out);
+}
 
 // Fused multi-field hash -> bucket -> gather -> pool.  A bag is owned by a
 // group of G lanes (4 floats of the row each).  The group hashes up to G
@@ -546,9 +659,26 @@ int annc_hip_hashed_embedding_bags(void* stream, int64_t num_fields, int64_t bat
   for (int64_t f0 = 0; f0 < num_fields; f0 += kMaxFields) {
     const int64_t nf = std::min<int64_t>(kMaxFields, num_fields - f0);
     FieldSet fs{};
+    bool small_tables = true;  // every table below 2 GiB: the buffer-load kernel
     for (int64_t i = 0; i < nf; ++i) {
       fs.table[i] = tables[f0 + i];
+      fs.rows[i] = table_rows[f0 + i];
       fs.div[i] = make_divisor(static_cast<uint64_t>(num_buckets[f0 + i]));
+      small_tables = small_tables && table_rows[f0 + i] * dim * 4 < (int64_t(1) << 31);
+    }
+    if (small_tables) {
+      if (lanes <= 4)
+        launch_hashed_wave_g<4>(fs, f0, nf, batch, dim, ids, offsets, combiner, out, ldo, buckets_out, s);
+      else if (lanes <= 8)
+        launch_hashed_wave_g<8>(fs, f0, nf, batch, dim, ids, offsets, combiner, out, ldo, buckets_out, s);
+      else if (lanes <= 16)
+        launch_hashed_wave_g<16>(fs, f0, nf, batch, dim, ids, offsets, combiner, out, ldo, buckets_out, s);
+      else if (lanes <= 32)
+        launch_hashed_wave_g<32>(fs, f0, nf, batch, dim, ids, offsets, combiner, out, ldo, buckets_out, s);
+      else
+        launch_hashed_wave_g<64>(fs, f0, nf, batch, dim, ids, offsets, combiner, out, ldo, buckets_out, s);
+      ANNC_HIP_TRY(hipGetLastError());
+      continue;
     }
     if (lanes <= 4)
       launch_hashed_g<4>(fs, f0, nf, batch, dim, ids, offsets, combiner, out, ldo, buckets_out, s);

@@ -52,6 +52,9 @@ EDGE_IDS = [0, 1, -1, 9, 10, 11, 99, 100, 101, -9, -10, 999_999, 1_000_000, 1234
             99_999_999, 100_000_000, 100_000_001, 10**15, 10**16 - 1, 10**16, 10**16 + 1,
             10**17, 10**18, 2**63 - 1, -2**63, -2**63 + 1, -(10**18), 4_294_967_295,
             4_294_967_296, -4_294_967_296]
+# every decimal length 1..19 at both ends, both signs
+EDGE_IDS += sorted({s * v for k in range(19) for v in (10**k - 1, 10**k, 10**k + 1, 2 * 10**k)
+                    for s in (1, -1) if -2**63 <= s * v < 2**63})
 
 
 @pytest.mark.parametrize("num_buckets", [1, 2, 7, 10, 100_000, 2**31 - 1, 2**32 + 15,
