@@ -90,6 +90,10 @@ _PROTOTYPES = {
     "annc_hip_hashed_embedding_bags": (_i32, [_c_void_p, _i64, _i64, _i64, _c_void_p, _c_void_p,
                                               _c_void_p, _c_void_p, _c_void_p, _i32, _c_void_p,
                                               _i64, _c_void_p]),
+    "annc_hip_unique_gather": (_i32, [_c_void_p, _c_void_p, _i64, _i64, _c_void_p, _i64, _i64,
+                                      _c_void_p, _c_void_p, _c_void_p, _c_void_p]),
+    "annc_kp_fused_gather": (_i32, [_c_void_p, _i32, _c_void_p, _c_void_p, _i32, _c_void_p,
+                                    _c_void_p, _i64, _c_void_p, _c_void_p, _c_void_p, _c_void_p]),
     "annc_kp_fused_sparse_segment_reduce": (_i32, [_c_void_p, _i32, _c_void_p, _c_void_p, _i32,
                                                    _i64, _c_void_p, _i32, _c_void_p, _c_void_p,
                                                    _i64, _c_void_p, _i64, _i32, _c_void_p,

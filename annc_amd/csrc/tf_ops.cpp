@@ -15,6 +15,9 @@ int launch_bucket_strings(hipStream_t s, const char* bytes, const int64_t* offse
                           int64_t num_buckets, int nul, int64_t empty_value, int64_t* out);
 int launch_gather_rows(hipStream_t s, const float* table, int64_t rows, int64_t dim,
                        const int64_t* bucket, int64_t n, float* out);
+int unique_gather(hipStream_t s, const float* table, int64_t rows, int64_t dim,
+                  const int64_t* keys, int64_t stride, int64_t n, int64_t* num_unique,
+                  int64_t* unique, int32_t* indices, float* out);
 int run_sparse_embedding(hipStream_t s, const int64_t* offsets, const int64_t* bucket, int64_t n,
                          int32_t* keep, int32_t* pos, int64_t* indices, int64_t* values,
                          uint8_t* empty, int64_t* num_values);
@@ -220,6 +223,61 @@ int annc_kp_fused_sparse_embedding(const char* bytes, const int64_t* offsets, in
   if (rc != ANNC_OK) return rc;
   rc = st.finish();
   return rc == ANNC_OK ? set_error(ANNC_OK, "") : rc;
+}
+
+int annc_kp_fused_gather(const float* data, int data_rank, const int64_t* data_dims,
+                         const int64_t* slice_input, int slice_rank, const int64_t* slice_dims,
+                         const int32_t* begin, int64_t begin_elems, int64_t* num_unique,
+                         int64_t* out_unique, int32_t* out_indices, float* out_data) {
+  using namespace annc;
+  // Compute() checks, same order and text (embedding_fused_gather.cc:34-42);
+  // the reference reports them as errors::Internal.
+  if (slice_rank != 2) return set_error(ANNC_INTERNAL, "Input key must be 2D");
+  if (data_rank != 2) return set_error(ANNC_INTERNAL, "Embedding table shape must be 2D");
+  if (begin_elems != 2) return set_error(ANNC_INTERNAL, "begin must be same as keys rank");
+  ANNC_REQUIRE(data_dims && slice_dims && begin && num_unique, "null operand");
+  int32_t b[2];
+  int rc = read_i32(begin, 2, b);
+  if (rc != ANNC_OK) return rc;
+  const int32_t col = b[1];
+  if (col < 0 || col >= slice_dims[1])
+    return set_error(ANNC_INTERNAL, "slice cols out of keys range");
+  const int64_t rows = data_dims[0], dim = data_dims[1], n = slice_dims[0];
+  ANNC_REQUIRE(rows >= 0 && dim >= 0 && n >= 0, "bad dimensions");
+  ANNC_REQUIRE(n < (int64_t(1) << 31) - 1, "too many keys");
+  if (n == 0) {
+    *num_unique = 0;
+    return set_error(ANNC_OK, "");
+  }
+  ANNC_REQUIRE(slice_input && (data || rows * dim == 0), "null operand");
+  hipStream_t s = lib_stream();
+  if (!s) return set_error(ANNC_INTERNAL, "no HIP stream");
+  (void)annc_hip_stream_status(s);  // start from a clear status word
+  Staging st(s);
+  const float* d_data =
+      static_cast<const float*>(st.in(data, sizeof(float) * (size_t)(rows * dim > 0 ? rows * dim : 1)));
+  const int64_t* d_keys =
+      static_cast<const int64_t*>(st.in(slice_input, sizeof(int64_t) * (size_t)(n * slice_dims[1])));
+  int64_t* d_nu = static_cast<int64_t*>(st.scratch(sizeof(int64_t)));
+  int64_t* d_uniq = static_cast<int64_t*>(st.scratch(sizeof(int64_t) * (size_t)n));
+  int32_t* d_idx = static_cast<int32_t*>(st.scratch(sizeof(int32_t) * (size_t)n));
+  float* d_out = static_cast<float*>(st.scratch(sizeof(float) * (size_t)(n * (dim > 0 ? dim : 1))));
+  if (st.status() != ANNC_OK) return st.status();
+  rc = unique_gather(s, d_data, rows, dim, d_keys + col, slice_dims[1], n, d_nu, d_uniq, d_idx,
+                     d_out);
+  if (rc != ANNC_OK) return rc;
+  if (annc_hip_stream_status(s) != ANNC_OK)  // synchronises
+    return set_error(ANNC_INTERNAL, "idx out of table range");
+  int64_t u = 0;
+  ANNC_HIP_TRY(hipMemcpy(&u, d_nu, sizeof(u), hipMemcpyDeviceToHost));
+  *num_unique = u;
+  if (out_unique)
+    ANNC_HIP_TRY(hipMemcpy(out_unique, d_uniq, sizeof(int64_t) * (size_t)u, hipMemcpyDefault));
+  if (out_indices)
+    ANNC_HIP_TRY(hipMemcpy(out_indices, d_idx, sizeof(int32_t) * (size_t)n, hipMemcpyDefault));
+  if (out_data && u * dim > 0)
+    ANNC_HIP_TRY(hipMemcpy(out_data, d_out, sizeof(float) * (size_t)(u * dim), hipMemcpyDefault));
+  return set_error(ANNC_OK, "");
 }
 
 }  // extern "C"

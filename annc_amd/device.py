@@ -156,6 +156,31 @@ def segment_reduce(data: torch.Tensor, indices: torch.Tensor, segment_ids: torch
     return out
 
 
+def unique_gather(table: torch.Tensor, keys: torch.Tensor, col: int = 0, stream=None):
+    """KPFusedGather engine on device tensors: keys [N, C] (or [N]) int64,
+    column `col`.  Returns (unique int64[U], indices int32[N], rows [U, dim])
+    -- U is read back, which synchronises the stream."""
+    _require_cuda(table, keys)
+    if keys.dtype != torch.int64:
+        raise ValueError("keys must be int64")
+    k2 = keys if keys.dim() == 2 else keys.reshape(-1, 1)
+    if k2.stride(-1) != 1:
+        k2 = k2.contiguous()
+    if not 0 <= col < k2.shape[1]:
+        raise ValueError("col outside the key columns")
+    rows, dim = table.shape
+    n = k2.shape[0]
+    nu = torch.zeros(1, dtype=torch.int64, device=table.device)
+    uniq = torch.empty(max(n, 1), dtype=torch.int64, device=table.device)
+    idx = torch.empty(n, dtype=torch.int32, device=table.device)
+    out = torch.empty((max(n, 1), dim), dtype=torch.float32, device=table.device)
+    check(_lib.lib().annc_hip_unique_gather(stream_ptr(stream), ptr(table.contiguous()), rows, dim,
+                                            ptr(k2) + 8 * col if n else None, k2.stride(0), n,
+                                            ptr(nu), ptr(uniq), ptr(idx), ptr(out)))
+    u = int(nu.item())
+    return uniq[:u], idx, out[:u]
+
+
 def sparse_embedding2(table: torch.Tensor, ids: torch.Tensor, fallback_row: int = 0,
                       stream=None) -> torch.Tensor:
     _require_cuda(table, ids)

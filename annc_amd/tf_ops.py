@@ -20,6 +20,7 @@ __all__ = [
     "kp_fused_dnn_embedding_with_hash_bucket",
     "kp_fused_linear_embedding_with_hash_bucket",
     "kp_fused_sparse_embedding",
+    "kp_fused_gather",
     "InvalidArgumentError",
 ]
 
@@ -83,6 +84,34 @@ def kp_fused_sparse_segment_reduce(data, indices, slice_input, begin, begin_1, c
     slice_out = np.zeros(1, dtype=np.int32)
     check(lib.annc_kp_fused_sparse_segment_reduce(*args, ptr(out), ptr(slice_out)))
     return out, np.int32(slice_out[0])
+
+
+def kp_fused_gather(data, slice_input, begin):
+    """KPFusedGather (annc/tensorflow/ops/embedding_fused_ops.cc:114-121,
+    annc/tensorflow/kernels/embedding_fused_gather.cc:26-85).
+
+    Returns (out_shape int64[U]: the distinct keys of column begin[1] in order
+    of first occurrence, out_indices int32[N], out_data float32[U, D]).
+    Errors raise AnncError (code 13, errors::Internal) with the reference text.
+    """
+    lib = _lib.lib()
+    data = _contig(data)
+    slice_input = _contig(slice_input)
+    begin_h = _as_host_i32(begin).reshape(-1)
+    ddims = _dims(data)
+    sdims = _dims(slice_input)
+    nu = np.zeros(1, dtype=np.int64)
+    args = (ptr(data), len(data.shape), ptr(ddims), ptr(slice_input), len(slice_input.shape),
+            ptr(sdims), ptr(begin_h), begin_h.size, ptr(nu))
+    n = int(sdims[0]) if sdims.size else 0
+    dim = int(ddims[1]) if ddims.size == 2 else 0
+    # outputs sized for every key being distinct, trimmed to U afterwards
+    uniq = np.empty(max(n, 1), dtype=np.int64)
+    idx = _empty_like_kind(data, (n,), np.int32)
+    out = _empty_like_kind(data, (max(n, 1), dim), np.float32)
+    check(lib.annc_kp_fused_gather(*args, ptr(uniq), ptr(idx), ptr(out)))
+    u = int(nu[0])
+    return uniq[:u].copy(), idx, out[:u]
 
 
 def _pack_strings(strings: Sequence[bytes | str]):

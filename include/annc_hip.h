@@ -162,6 +162,17 @@ int annc_hip_pooling(void* stream, const int64_t* ids, const float* gathered, in
                      int64_t k, int64_t n, const int64_t* slice_starts3,
                      const int64_t* slice_limits3, float* out);
 
+/* Unique + gather, the engine of KPFusedGather: keys[i * key_stride] for
+ * i < n are de-duplicated in order of first occurrence; unique[r] is the
+ * r-th distinct key, indices[i] the rank of keys[i], out[r, :] =
+ * table[unique[r], :] (a zero row, and the stream's status word set, for a
+ * key outside [0, rows)).  unique and out must hold n keys / n rows; the
+ * count U is written to the device int64 *num_unique.  All device pointers,
+ * asynchronous on `stream`. */
+int annc_hip_unique_gather(void* stream, const float* table, int64_t rows, int64_t dim,
+                           const int64_t* keys, int64_t key_stride, int64_t n,
+                           int64_t* num_unique, int64_t* unique, int32_t* indices, float* out);
+
 /* ------------------------------------------------------------------------ */
 /* Hashing: FarmHash Fingerprint64 (farmhashna::Hash64, google/farmhash as  */
 /* pinned by TensorFlow 2.15) and StringToHashBucketFast semantics          */
@@ -213,6 +224,20 @@ int annc_kp_fused_sparse_segment_reduce(const float* data, int data_rank, const 
                                         const int32_t* begin_1, int64_t begin_1_elems,
                                         int combiner, int64_t* out_rows, float* output,
                                         int32_t* slice_output);
+
+/* KPFusedGather (annc/tensorflow/ops/embedding_fused_ops.cc:114-121,
+ * kernels/embedding_fused_gather.cc:26-85).  Inputs: data f32 (data_rank,
+ * data_dims), slice_input int64 (slice_rank, slice_dims), begin int32
+ * [begin_elems]; the key column is begin[1].  Outputs: out_unique int64[U]
+ * (the op's "out_shape": distinct keys in order of first occurrence),
+ * out_indices int32[N], out_data f32[U, data_dims[1]].  *num_unique = U.
+ * Output pointers may be NULL (e.g. a first call that only sizes them).
+ * Errors: the reference messages verbatim, with ANNC_INTERNAL as the
+ * reference's errors::Internal. */
+int annc_kp_fused_gather(const float* data, int data_rank, const int64_t* data_dims,
+                         const int64_t* slice_input, int slice_rank, const int64_t* slice_dims,
+                         const int32_t* begin, int64_t begin_elems, int64_t* num_unique,
+                         int64_t* out_unique, int32_t* out_indices, float* out_data);
 
 /* KPFusedEmbeddingWithHashBucket
  * (python/tensorflow/kernels/fused_embedding_with_hash_bucket.cc:15-83):

@@ -19,6 +19,9 @@
  *   ora_embedding_bag      same order as ora_segment_reduce (CSR form);
  *                          checked equal to it in tests/.
  *   ora_pooling            brute force on tiny inputs in tests/.
+ *   ora_fused_gather       reference gtest golden vector
+ *                          (embedding_fused_gather_test.cc:111-128) and
+ *                          numpy.unique(return_index, return_inverse) in tests/.
  *   ora_sgemm & wrappers   OpenBLAS 0.3.29 sgemm (the reference's pinned
  *                          math library, third_party/repo.bzl:7) loaded
  *                          from numpy's bundled scipy_openblas64_; checked
@@ -292,6 +295,42 @@ void ora_pooling(const int64_t* ids, const float* gathered, int64_t m, int64_t k
 /* sparse_embedding2 (graph_opt.cc:8-41; bounds from
  * bisheng-cpu/embedding_simplify.cc:62-81):
  * out[i,:] = table[valid ? id : fallback, :] * (float)valid. */
+/* KPFusedGather (annc/tensorflow/kernels/embedding_fused_gather.cc:48-84):
+ * walk the key column in row order with a map key -> first-occurrence index
+ * (open addressing here, unordered_map there); a new key gets the next index
+ * and joins `unique`; every row records its key's index.  Then the table
+ * rows of the unique keys are copied.  Returns the unique count, or -1 if a
+ * unique key lies outside [0, rows) ("idx out of table range"). */
+int64_t ora_fused_gather(const float* table, int64_t rows, int64_t dim, const int64_t* keys,
+                         int64_t stride, int64_t n, int64_t* unique, int32_t* indices,
+                         float* out) {
+  int64_t cap = 16;
+  while (cap < 2 * n) cap <<= 1;
+  int64_t* slot_key = (int64_t*)malloc(sizeof(int64_t) * (size_t)cap);
+  int32_t* slot_idx = (int32_t*)malloc(sizeof(int32_t) * (size_t)cap);
+  for (int64_t i = 0; i < cap; ++i) slot_idx[i] = -1;
+  int64_t u = 0;
+  for (int64_t i = 0; i < n; ++i) {
+    const int64_t key = keys[i * stride];
+    uint64_t h = (uint64_t)key * 0x9e3779b97f4a7c15ULL;
+    int64_t at = (int64_t)(h >> 17) & (cap - 1);
+    while (slot_idx[at] >= 0 && slot_key[at] != key) at = (at + 1) & (cap - 1);
+    if (slot_idx[at] < 0) {
+      slot_key[at] = key;
+      slot_idx[at] = (int32_t)u;
+      unique[u++] = key;
+    }
+    indices[i] = slot_idx[at];
+  }
+  free(slot_key);
+  free(slot_idx);
+  for (int64_t r = 0; r < u; ++r) {
+    if (unique[r] < 0 || unique[r] >= rows) return -1;
+    memcpy(out + r * dim, table + unique[r] * dim, sizeof(float) * (size_t)dim);
+  }
+  return u;
+}
+
 void ora_sparse_embedding2(const float* table, int64_t rows, int64_t dim, const void* ids,
                            int idx64, int64_t n, int64_t fallback, float* out) {
   for (int64_t i = 0; i < n; ++i) {

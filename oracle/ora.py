@@ -33,6 +33,7 @@ _PROTO = {
     "ora_embedding_bag": (None, [_v, _i64, _i64, _v, _i32, _v, _i64, _i32, _v, _i64, _i32]),
     "ora_pooling": (None, [_v, _v, _i64, _i64, _i64, _v, _v, _v]),
     "ora_sparse_embedding2": (None, [_v, _i64, _i64, _v, _i32, _i64, _i64, _v]),
+    "ora_fused_gather": (_i64, [_v, _i64, _i64, _v, _i64, _i64, _v, _v, _v]),
     "ora_embedding_with_hash_bucket": (None, [_v, _v, _i64, _v, _i64, _i64, _v]),
     "ora_dnn_embedding_with_hash_bucket": (None, [_v, _v, _i64, _v, _i64, _i64, _i64, _v]),
     "ora_sparse_embedding": (None, [_v, _v, _i64, _i64, _v, _v, _v, _v, _v]),
@@ -173,6 +174,22 @@ def pooling(ids, gathered, ss, sl) -> np.ndarray:
     out = np.empty((m, n), dtype=np.float32)
     lib().ora_pooling(_p(ids), _p(gathered), m, k, n, _p(ss), _p(sl), _p(out))
     return out
+
+
+def fused_gather(table, keys2d, col):
+    """KPFusedGather: (unique int64[U], indices int32[N], rows [U, D]); raises
+    IndexError for a unique key outside the table."""
+    table = _c(table, np.float32)
+    keys2d = _c(keys2d, np.int64)
+    n, c = keys2d.shape
+    uniq = np.empty(max(n, 1), np.int64)
+    idx = np.empty(n, np.int32)
+    out = np.empty((max(n, 1), table.shape[1]), np.float32)
+    u = lib().ora_fused_gather(_p(table), table.shape[0], table.shape[1],
+                               keys2d.ctypes.data + 8 * col, c, n, _p(uniq), _p(idx), _p(out))
+    if u < 0:
+        raise IndexError("idx out of table range")
+    return uniq[:u].copy(), idx, out[:u].copy()
 
 
 def sparse_embedding2(table, ids, fallback=0) -> np.ndarray:

@@ -10,6 +10,7 @@ import numpy as np
 import pytest
 
 from annc_amd import _lib, flags, tf_ops, xla
+from annc_amd._lib import AnncError
 from annc_amd import device as dev
 from oracle import ora
 
@@ -177,3 +178,17 @@ def test_shape_info_encoding():
     # hlo_util.h:14-21 -- dims then minor_to_major; row-major [512,256] -> {512,256,1,0}
     assert xla.shape_info((512, 256)).tolist() == [512, 256, 1, 0]
     assert xla.shape_info((2, 3, 4)).tolist() == [2, 3, 4, 2, 1, 0]
+
+
+@pytest.mark.parametrize("case", [c for c in json.load(open(os.path.join(
+    os.path.dirname(__file__), "golden", "fused_gather_reference_gtest.json")))["error_cases"]
+    if not c.get("needs_gpu")], ids=lambda c: c["name"])
+def test_fused_gather_error_messages(case):
+    """The shape checks of KPFusedGather run on the host, before any GPU work."""
+    from annc_amd import tf_ops
+    data = np.ones(case["data_shape"], np.float32)
+    keys = np.asarray(case["slice_input"], np.int64).reshape(case["slice_shape"])
+    with pytest.raises(AnncError) as e:
+        tf_ops.kp_fused_gather(data, keys, np.asarray(case["begin"], np.int32))
+    assert case["message"] in e.value.message
+    assert e.value.code == 13  # errors::Internal

@@ -243,3 +243,43 @@ def test_dense_layer_relu_and_sigmoid():
     np.testing.assert_array_equal(ora.dense_layer(a, w, bias, 1), np.where(lin < 0, 0, lin))
     np.testing.assert_allclose(ora.dense_layer(a, w, bias, 2), 1 / (1 + np.exp(-lin.astype(np.float64))),
                                rtol=1e-6, atol=1e-7)
+
+
+# ---------------------------------------------------------------- KPFusedGather
+GATHER_GOLD = json.load(open(os.path.join(os.path.dirname(__file__), "golden",
+                                          "fused_gather_reference_gtest.json")))
+
+
+def test_fused_gather_reference_golden():
+    c = GATHER_GOLD["cases"][0]
+    data = np.asarray(c["data"], np.float32).reshape(c["data_shape"])
+    keys = np.asarray(c["slice_input"], np.int64).reshape(c["slice_shape"])
+    u, idx, rows = ora.fused_gather(data, keys, c["begin"][1])
+    assert u.tolist() == c["expected_unique"]
+    assert idx.tolist() == c["expected_indices"]
+    assert rows.reshape(-1).tolist() == c["expected_data"]
+
+
+@pytest.mark.parametrize("n,span", [(1, 1), (50, 5), (5000, 300), (20000, 10**9)])
+def test_fused_gather_against_numpy_unique(n, span):
+    """First-occurrence order: numpy.unique gives sorted keys with the index
+    of each key's first occurrence; ordering the keys by that index is the
+    reference's order, and the inverse map renumbered the same way is the
+    per-row index."""
+    g = np.random.default_rng(n)
+    keys = g.integers(-span, span, size=(n, 3))
+    table = g.standard_normal((4, 5)).astype(np.float32)
+    keys[:, 1] = np.abs(keys[:, 1]) % 4
+    u, idx, rows = ora.fused_gather(table, keys, 1)
+    srt, first, inv = np.unique(keys[:, 1], return_index=True, return_inverse=True)
+    order = np.argsort(first, kind="stable")
+    rank = np.empty_like(order)
+    rank[order] = np.arange(order.size)
+    np.testing.assert_array_equal(u, srt[order])
+    np.testing.assert_array_equal(idx, rank[inv.reshape(-1)])
+    np.testing.assert_array_equal(rows, table[u])
+
+
+def test_fused_gather_out_of_range_is_reported():
+    with pytest.raises(IndexError):
+        ora.fused_gather(np.zeros((2, 3), np.float32), np.array([[0], [2]], np.int64), 0)
