@@ -94,6 +94,9 @@ _PROTOTYPES = {
                                       _c_void_p, _c_void_p, _c_void_p, _c_void_p]),
     "annc_kp_fused_gather": (_i32, [_c_void_p, _i32, _c_void_p, _c_void_p, _i32, _c_void_p,
                                     _c_void_p, _i64, _c_void_p, _c_void_p, _c_void_p, _c_void_p]),
+    "annc_kp_fused_batch_matmul_add_sigmoid": (_i32, [_c_void_p, _i32, _c_void_p, _c_void_p,
+                                                      _i32, _c_void_p, _c_void_p, _i32,
+                                                      _c_void_p, _c_void_p]),
     "annc_kp_fused_sparse_segment_reduce": (_i32, [_c_void_p, _i32, _c_void_p, _c_void_p, _i32,
                                                    _i64, _c_void_p, _i32, _c_void_p, _c_void_p,
                                                    _i64, _c_void_p, _i64, _i32, _c_void_p,

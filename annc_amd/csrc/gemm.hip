@@ -566,6 +566,17 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_packed_pipe_kernel(GemmPara
   }
 }
 
+// dst[z, i, j] = src[z*s0 + i*s1 + j*s2] over [nz, m, n] (a broadcast bias
+// materialised as a GEMM addend; strides of broadcast dims are 0).
+__global__ void broadcast3_kernel(const float* __restrict__ src, int64_t s0, int64_t s1,
+                                  int64_t s2, int64_t nz, int64_t m, int64_t n,
+                                  float* __restrict__ dst) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= nz * m * n) return;
+  const int64_t j = t % n, i = (t / n) % m, z = t / (m * n);
+  dst[t] = src[z * s0 + i * s1 + j * s2];
+}
+
 __global__ void pack_rhs_kernel(const float* __restrict__ src, float* __restrict__ dst, int64_t K,
                                 int64_t N) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -625,6 +636,17 @@ int launch_gemm(const GemmParams& p, int64_t batch, hipStream_t stream) {
 }
 
 }  // namespace
+
+int launch_broadcast3(hipStream_t s, const float* src, int64_t s0, int64_t s1, int64_t s2,
+                      int64_t nz, int64_t m, int64_t n, float* dst) {
+  const int64_t total = nz * m * n;
+  if (total == 0) return ANNC_OK;
+  hipLaunchKernelGGL(broadcast3_kernel, dim3((unsigned)ceil_div(total, 256)), dim3(256), 0, s,
+                     src, s0, s1, s2, nz, m, n, dst);
+  ANNC_HIP_TRY(hipGetLastError());
+  return ANNC_OK;
+}
+
 }  // namespace annc
 
 extern "C" {

@@ -18,6 +18,8 @@ int launch_gather_rows(hipStream_t s, const float* table, int64_t rows, int64_t 
 int unique_gather(hipStream_t s, const float* table, int64_t rows, int64_t dim,
                   const int64_t* keys, int64_t stride, int64_t n, int64_t* num_unique,
                   int64_t* unique, int32_t* indices, float* out);
+int launch_broadcast3(hipStream_t s, const float* src, int64_t s0, int64_t s1, int64_t s2,
+                      int64_t nz, int64_t m, int64_t n, float* dst);
 int run_sparse_embedding(hipStream_t s, const int64_t* offsets, const int64_t* bucket, int64_t n,
                          int32_t* keep, int32_t* pos, int64_t* indices, int64_t* values,
                          uint8_t* empty, int64_t* num_values);
@@ -278,6 +280,54 @@ int annc_kp_fused_gather(const float* data, int data_rank, const int64_t* data_d
   if (out_data && u * dim > 0)
     ANNC_HIP_TRY(hipMemcpy(out_data, d_out, sizeof(float) * (size_t)(u * dim), hipMemcpyDefault));
   return set_error(ANNC_OK, "");
+}
+
+int annc_kp_fused_batch_matmul_add_sigmoid(const float* lhs, int lhs_rank,
+                                           const int64_t* lhs_dims, const float* rhs, int rhs_rank,
+                                           const int64_t* rhs_dims, const float* bias,
+                                           int bias_rank, const int64_t* bias_dims,
+                                           float* output) {
+  using namespace annc;
+  // Compute() checks, same order and text (fused_batchmatmul_add_sigmoid.cc:
+  // Compute and BuildBiasInfo).
+  ANNC_REQUIRE(lhs_rank == 3, "lhs must be rank 3");
+  ANNC_REQUIRE(rhs_rank == 2 || rhs_rank == 3, "rhs must be rank 2 or 3");
+  ANNC_REQUIRE(bias_rank >= 0 && bias_rank <= 3, "bias rank must be <= 3");
+  ANNC_REQUIRE(lhs_dims && rhs_dims && (bias_rank == 0 || bias_dims), "null shape operand");
+  const int64_t batch = lhs_dims[0], m = lhs_dims[1], k = lhs_dims[2];
+  const bool rhs_batched = rhs_rank == 3;
+  ANNC_REQUIRE(!rhs_batched || rhs_dims[0] == batch, "lhs/rhs batch mismatch");
+  ANNC_REQUIRE(rhs_dims[rhs_batched ? 1 : 0] == k, "lhs/rhs contracting dim mismatch");
+  const int64_t n = rhs_dims[rhs_batched ? 2 : 1];
+  int64_t bd[3] = {1, 1, 1};
+  for (int i = 0; i < bias_rank; ++i) bd[3 - bias_rank + i] = bias_dims[i];
+  ANNC_REQUIRE((bd[0] == 1 || bd[0] == batch) && (bd[1] == 1 || bd[1] == m) &&
+                   (bd[2] == 1 || bd[2] == n),
+               "bias shape is not broadcast-compatible");
+  if (batch == 0 || m == 0 || n == 0) return set_error(ANNC_OK, "");
+  ANNC_REQUIRE(lhs && rhs && bias && output, "null operand");
+  const int64_t s2 = bd[2] == 1 ? 0 : 1;
+  const int64_t s1 = bd[1] == 1 ? 0 : bd[2];
+  const int64_t s0 = bd[0] == 1 ? 0 : bd[1] * bd[2];
+  const int64_t nz = bd[0];  // 1 or batch: the materialised addend's batch
+  hipStream_t s = lib_stream();
+  if (!s) return set_error(ANNC_INTERNAL, "no HIP stream");
+  Staging st(s);
+  const size_t f = sizeof(float);
+  const float* d_lhs = static_cast<const float*>(st.in(lhs, f * (size_t)(batch * m * k)));
+  const float* d_rhs = static_cast<const float*>(
+      st.in(rhs, f * (size_t)((rhs_batched ? batch : 1) * k * n)));
+  const float* d_bias = static_cast<const float*>(st.in(bias, f * (size_t)(bd[0] * bd[1] * bd[2])));
+  float* d_out = static_cast<float*>(st.out(output, f * (size_t)(batch * m * n)));
+  float* addend = static_cast<float*>(st.scratch(f * (size_t)(nz * m * n)));
+  if (st.status() != ANNC_OK) return st.status();
+  int rc = launch_broadcast3(s, d_bias, s0, s1, s2, nz, m, n, addend);
+  if (rc == ANNC_OK)
+    rc = annc_hip_gemm(s, batch, m, n, k, d_lhs, k, m * k, d_rhs, n, rhs_batched ? k * n : 0, 0,
+                       addend, n, nz > 1 ? m * n : 0, nullptr, ANNC_EPI_SIGMOID, d_out, n, m * n);
+  if (rc != ANNC_OK) return rc;
+  rc = st.finish();
+  return rc == ANNC_OK ? set_error(ANNC_OK, "") : rc;
 }
 
 }  // extern "C"

@@ -21,6 +21,7 @@ __all__ = [
     "kp_fused_linear_embedding_with_hash_bucket",
     "kp_fused_sparse_embedding",
     "kp_fused_gather",
+    "kp_fused_batch_matmul_add_sigmoid",
     "InvalidArgumentError",
 ]
 
@@ -112,6 +113,25 @@ def kp_fused_gather(data, slice_input, begin):
     check(lib.annc_kp_fused_gather(*args, ptr(uniq), ptr(idx), ptr(out)))
     u = int(nu[0])
     return uniq[:u].copy(), idx, out[:u]
+
+
+def kp_fused_batch_matmul_add_sigmoid(lhs, rhs, bias):
+    """KPFusedBatchMatMulAddSigmoid (annc/tensorflow/ops/embedding_fused_ops.cc:134-139,
+    annc/tensorflow/kernels/fused_batchmatmul_add_sigmoid.cc):
+    sigmoid(bias + lhs @ rhs) -> float32 [batch, m, n]."""
+    lib = _lib.lib()
+    lhs, rhs, bias = _contig(lhs), _contig(rhs), _contig(bias)
+    ld, rd, bd = _dims(lhs), _dims(rhs), _dims(bias)
+    if len(lhs.shape) == 3 and len(rhs.shape) in (2, 3):
+        n = int(rd[-1])
+        shape = (int(ld[0]), int(ld[1]), n)
+    else:
+        shape = (0,)
+    out = _empty_like_kind(lhs, shape, np.float32)
+    check(lib.annc_kp_fused_batch_matmul_add_sigmoid(
+        ptr(lhs), len(lhs.shape), ptr(ld), ptr(rhs), len(rhs.shape), ptr(rd), ptr(bias),
+        len(bias.shape), ptr(bd) if bd.size else None, ptr(out)))
+    return out
 
 
 def _pack_strings(strings: Sequence[bytes | str]):

@@ -239,6 +239,18 @@ int annc_kp_fused_gather(const float* data, int data_rank, const int64_t* data_d
                          const int32_t* begin, int64_t begin_elems, int64_t* num_unique,
                          int64_t* out_unique, int32_t* out_indices, float* out_data);
 
+/* KPFusedBatchMatMulAddSigmoid (annc/tensorflow/ops/embedding_fused_ops.cc:134-139,
+ * kernels/fused_batchmatmul_add_sigmoid.cc): output[b,i,j] =
+ * sigmoid(bias[b,i,j] + sum_k lhs[b,i,k] * rhs[(b,)k,j]) with lhs [batch,m,k],
+ * rhs [k,n] or [batch,k,n], bias of rank <= 3 broadcast from the right.
+ * "any" pointers, synchronous; errors are the reference messages
+ * (ANNC_INVALID_ARGUMENT). */
+int annc_kp_fused_batch_matmul_add_sigmoid(const float* lhs, int lhs_rank,
+                                           const int64_t* lhs_dims, const float* rhs, int rhs_rank,
+                                           const int64_t* rhs_dims, const float* bias,
+                                           int bias_rank, const int64_t* bias_dims,
+                                           float* output);
+
 /* KPFusedEmbeddingWithHashBucket
  * (python/tensorflow/kernels/fused_embedding_with_hash_bucket.cc:15-83):
  * out[i,:] = weight[Fingerprint64(s_i) % num_buckets, :] for non-empty s_i,

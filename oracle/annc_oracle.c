@@ -19,6 +19,10 @@
  *   ora_embedding_bag      same order as ora_segment_reduce (CSR form);
  *                          checked equal to it in tests/.
  *   ora_pooling            brute force on tiny inputs in tests/.
+ *   ora_batch_matmul_add_sigmoid
+ *                          float64 closed form (numpy matmul + broadcast) on
+ *                          the reference test's shapes and inputs
+ *                          (fused_batchmatmul_add_sigmoid_test.cc:140-204).
  *   ora_fused_gather       reference gtest golden vector
  *                          (embedding_fused_gather_test.cc:111-128) and
  *                          numpy.unique(return_index, return_inverse) in tests/.
@@ -329,6 +333,30 @@ int64_t ora_fused_gather(const float* table, int64_t rows, int64_t dim, const in
     memcpy(out + r * dim, table + unique[r] * dim, sizeof(float) * (size_t)dim);
   }
   return u;
+}
+
+/* KPFusedBatchMatMulAddSigmoid, the generic path
+ * (annc/tensorflow/kernels/fused_batchmatmul_add_sigmoid.cc ComputeGeneric,
+ * with the bias broadcast of BuildBiasInfo): acc = bias, acc += lhs * rhs in
+ * k order, out = 1 / (1 + exp(-acc)) (the reference test's Sigmoid).
+ * bias_dims holds the right-aligned [3] dims, each 1 or full. */
+void ora_batch_matmul_add_sigmoid(const float* lhs, const float* rhs, int rhs_batched,
+                                  const float* bias, const int64_t* bias_dims, int64_t batch,
+                                  int64_t m, int64_t k, int64_t n, float* out) {
+  const int64_t s2 = bias_dims[2] == 1 ? 0 : 1;
+  const int64_t s1 = bias_dims[1] == 1 ? 0 : bias_dims[2];
+  const int64_t s0 = bias_dims[0] == 1 ? 0 : bias_dims[1] * bias_dims[2];
+  for (int64_t b = 0; b < batch; ++b) {
+    const float* lb = lhs + b * m * k;
+    const float* rb = rhs + (rhs_batched ? b * k * n : 0);
+    for (int64_t i = 0; i < m; ++i) {
+      for (int64_t j = 0; j < n; ++j) {
+        float acc = bias[b * s0 + i * s1 + j * s2];
+        for (int64_t kk = 0; kk < k; ++kk) acc += lb[i * k + kk] * rb[kk * n + j];
+        out[(b * m + i) * n + j] = 1.0f / (1.0f + expf(-acc));
+      }
+    }
+  }
 }
 
 void ora_sparse_embedding2(const float* table, int64_t rows, int64_t dim, const void* ids,

@@ -34,6 +34,7 @@ _PROTO = {
     "ora_pooling": (None, [_v, _v, _i64, _i64, _i64, _v, _v, _v]),
     "ora_sparse_embedding2": (None, [_v, _i64, _i64, _v, _i32, _i64, _i64, _v]),
     "ora_fused_gather": (_i64, [_v, _i64, _i64, _v, _i64, _i64, _v, _v, _v]),
+    "ora_batch_matmul_add_sigmoid": (None, [_v, _v, _i32, _v, _v, _i64, _i64, _i64, _i64, _v]),
     "ora_embedding_with_hash_bucket": (None, [_v, _v, _i64, _v, _i64, _i64, _v]),
     "ora_dnn_embedding_with_hash_bucket": (None, [_v, _v, _i64, _v, _i64, _i64, _i64, _v]),
     "ora_sparse_embedding": (None, [_v, _v, _i64, _i64, _v, _v, _v, _v, _v]),
@@ -190,6 +191,21 @@ def fused_gather(table, keys2d, col):
     if u < 0:
         raise IndexError("idx out of table range")
     return uniq[:u].copy(), idx, out[:u].copy()
+
+
+def batch_matmul_add_sigmoid(lhs, rhs, bias) -> np.ndarray:
+    lhs = _c(lhs, np.float32)
+    rhs = _c(rhs, np.float32)
+    bias = _c(bias, np.float32)
+    b, m, k = lhs.shape
+    n = rhs.shape[-1]
+    bd = np.ones(3, np.int64)
+    if bias.ndim:
+        bd[3 - bias.ndim:] = bias.shape
+    out = np.empty((b, m, n), np.float32)
+    lib().ora_batch_matmul_add_sigmoid(_p(lhs), _p(rhs), int(rhs.ndim == 3), _p(bias), _p(bd),
+                                       b, m, k, n, _p(out))
+    return out
 
 
 def sparse_embedding2(table, ids, fallback=0) -> np.ndarray:

@@ -199,3 +199,38 @@ def test_config5_wide_deep_graph():
     concat = to_host(graph.concat_buffer(h.batch))[:, :x.shape[1]]
     np.testing.assert_array_equal(concat, x)  # embeddings bit-exact, dense copied
     np.testing.assert_allclose(y, ora.mlp_tower(x, w.weights, w.biases), rtol=1e-3, atol=1e-5)
+
+
+# ---------------------------------------------------------------- KPFusedBatchMatMulAddSigmoid
+import json  # noqa: E402
+import os  # noqa: E402
+
+from annc_amd import tf_ops  # noqa: E402
+from tests.test_oracle import BMS_GOLD, bms_inputs  # noqa: E402
+
+
+@pytest.mark.parametrize("case", BMS_GOLD["cases"], ids=lambda c: c["name"])
+@pytest.mark.parametrize("where", ["host", "device"])
+def test_batch_matmul_add_sigmoid_reference_cases(case, where):
+    note(f"KPFusedBatchMatMulAddSigmoid {case['name']} ({where})")
+    lhs, rhs, bias = bms_inputs(case)
+    ref = ora.batch_matmul_add_sigmoid(lhs, rhs, bias)
+    args = (lhs, rhs, bias) if where == "host" else tuple(to_dev(x) for x in (lhs, rhs, bias))
+    got = tf_ops.kp_fused_batch_matmul_add_sigmoid(*args)
+    got = got if where == "host" else to_host(got)
+    np.testing.assert_allclose(got, ref, rtol=0, atol=BMS_GOLD["tolerance"])
+
+
+@pytest.mark.parametrize("bias_shape", [(64,), (1, 64), (300, 64), (7, 1, 64), (7, 300, 64),
+                                        (7, 300, 1), (1,), ()])
+@pytest.mark.parametrize("rhs_batched", [False, True])
+def test_batch_matmul_add_sigmoid_broadcasts(bias_shape, rhs_batched):
+    note(f"KPFusedBatchMatMulAddSigmoid bias {bias_shape} rhs_batched={rhs_batched}")
+    g = workloads.rng(len(bias_shape) * 2 + rhs_batched)
+    b, m, k, n = 7, 300, 96, 64
+    lhs = (g.standard_normal((b, m, k)) * 0.1).astype(np.float32)
+    rhs = (g.standard_normal((b, k, n) if rhs_batched else (k, n)) * 0.1).astype(np.float32)
+    bias = g.standard_normal(bias_shape).astype(np.float32)
+    ref = ora.batch_matmul_add_sigmoid(lhs, rhs, bias)
+    got = tf_ops.kp_fused_batch_matmul_add_sigmoid(lhs, rhs, bias)
+    np.testing.assert_allclose(got, ref, rtol=0, atol=1e-5)

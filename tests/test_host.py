@@ -192,3 +192,15 @@ def test_fused_gather_error_messages(case):
         tf_ops.kp_fused_gather(data, keys, np.asarray(case["begin"], np.int32))
     assert case["message"] in e.value.message
     assert e.value.code == 13  # errors::Internal
+
+
+@pytest.mark.parametrize("case", json.load(open(os.path.join(
+    os.path.dirname(__file__), "golden", "batch_matmul_add_sigmoid_reference_gtest.json")))["error_cases"],
+    ids=lambda c: c["name"])
+def test_batch_matmul_add_sigmoid_error_messages(case):
+    """Shape checks run on the host before any GPU work."""
+    mk = lambda s: np.zeros(s, np.float32)  # noqa: E731
+    with pytest.raises(_lib.InvalidArgumentError) as e:
+        tf_ops.kp_fused_batch_matmul_add_sigmoid(mk(case["lhs_shape"]), mk(case["rhs_shape"]),
+                                                 mk(case["bias_shape"]))
+    assert case["message"] in e.value.message

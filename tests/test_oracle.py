@@ -283,3 +283,32 @@ def test_fused_gather_against_numpy_unique(n, span):
 def test_fused_gather_out_of_range_is_reported():
     with pytest.raises(IndexError):
         ora.fused_gather(np.zeros((2, 3), np.float32), np.array([[0], [2]], np.int64), 0)
+
+
+# ---------------------------------------------------------------- KPFusedBatchMatMulAddSigmoid
+BMS_GOLD = json.load(open(os.path.join(os.path.dirname(__file__), "golden",
+                                       "batch_matmul_add_sigmoid_reference_gtest.json")))
+
+
+def make_range(shape, start_step):
+    """MakeRange (fused_batchmatmul_add_sigmoid_test.cc:30-36): start + step*i in float32."""
+    start, step = (np.float32(v) for v in start_step)
+    size = int(np.prod(shape))
+    return (start + step * np.arange(size, dtype=np.float32)).astype(np.float32).reshape(shape)
+
+
+def bms_inputs(c):
+    return (make_range(c["lhs_shape"], c["lhs_range"]), make_range(c["rhs_shape"], c["rhs_range"]),
+            make_range(c["bias_shape"], c["bias_range"]))
+
+
+@pytest.mark.parametrize("case", BMS_GOLD["cases"], ids=lambda c: c["name"])
+def test_batch_matmul_add_sigmoid_oracle_closed_form(case):
+    """Against float64 numpy (matmul, broadcasting, exp) at the reference
+    test's own tolerance."""
+    lhs, rhs, bias = bms_inputs(case)
+    lin = np.matmul(lhs.astype(np.float64), rhs.astype(np.float64)) + bias.astype(np.float64)
+    want = 1.0 / (1.0 + np.exp(-lin))
+    got = ora.batch_matmul_add_sigmoid(lhs, rhs, bias)
+    assert got.shape == want.shape
+    np.testing.assert_allclose(got, want, rtol=0, atol=BMS_GOLD["tolerance"])
