@@ -23,6 +23,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cmath>
+#include <type_traits>
 
 #include "common.h"
 #include "layout_pack.h"
@@ -50,6 +51,7 @@ struct GemmParams {
   int epilogue;
   int a_vec;  // A rows can be read as aligned float4
   int b_vec;  // row-major B rows can be read as aligned float4
+  int b_dense;  // B is a dense row-major [K, N] block (ldb == N), 16-byte aligned
 };
 
 __device__ __forceinline__ float apply_epilogue(float v, int epilogue) {
@@ -273,52 +275,85 @@ __global__ __launch_bounds__(kThreads) void gemm_mfma_kernel(GemmParams p) {
   }
 }
 
-// Skinny-N path (N <= 4): one wave per output row, lanes stride over k.
-// For N < 32 the packed layout is row-major (region 3), so both forms share it.
-__global__ __launch_bounds__(kThreads) void gemv_kernel(GemmParams p) {
-  const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+// Skinny-N path, N <= 4 (a tower's scoring layer); for N < 32 the packed
+// layout is row-major, so packed and plain B share it.  16 lanes per row,
+// 4 rows per wave.  Lane
+// t of a row multiplies A[row, 64i + 4t .. 64i + 4t + 3] (one float4 per
+// chunk i) with the matching B rows, and the 16 partial sums are combined with
+// DPP row rotations, after which every lane of the row holds its sums.  Rows
+// past M are clamped to M - 1 so every lane takes part in the DPP; only the
+// store is predicated.
+template <int CTRL>
+__device__ __forceinline__ float dpp_add(float v) {
+  return v + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+template <int N>
+__global__ __launch_bounds__(kThreads) void gemv_rows_kernel(GemmParams p) {
+  constexpr int kRowLanes = 16;
+  const int t = threadIdx.x & (kRowLanes - 1);
+  const int64_t row = ((int64_t)blockIdx.x * kThreads + threadIdx.x) / kRowLanes;
   const int64_t z = blockIdx.z;
-  if (row >= p.m) return;
-  const float* __restrict__ A = p.a + z * p.stride_a + row * p.lda;
+  const int64_t r = row < p.m ? row : (int64_t)p.m - 1;
+  const float* __restrict__ A = p.a + z * p.stride_a + r * p.lda;
   const float* __restrict__ B = p.b + z * p.stride_b;
-  float part[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-  const int N = p.n, K = p.k;
-  int kk = lane * 4;
-  if (p.a_vec) {
-    for (; kk + 3 < K; kk += 256) {
-      const f32x4 av = *reinterpret_cast<const f32x4*>(A + kk);
+  const int K = p.k;
+  float part[N];
+#pragma unroll
+  for (int j = 0; j < N; ++j) part[j] = 0.0f;
+  int kk = 4 * t;
+  if (p.a_vec && p.b_dense) {
+    // B rows kk .. kk+3 are the 4N floats at B + kk*N: element (e, j) is e*N + j
+    auto chunk = [&](const f32x4& av, const f32x4* bv) {
 #pragma unroll
       for (int e = 0; e < 4; ++e)
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-          if (j < N) part[j] += av[e] * B[(int64_t)(kk + e) * p.ldb + j];
+        for (int j = 0; j < N; ++j) part[j] += av[e] * bv[(e * N + j) >> 2][(e * N + j) & 3];
+    };
+    for (; kk + 195 < K; kk += 256) {  // four chunks in flight per lane
+      f32x4 av[4], bv[4][N];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        av[u] = *reinterpret_cast<const f32x4*>(A + kk + 64 * u);
+#pragma unroll
+        for (int c = 0; c < N; ++c)
+          bv[u][c] = *reinterpret_cast<const f32x4*>(B + (int64_t)(kk + 64 * u) * N + 4 * c);
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) chunk(av[u], bv[u]);
+    }
+    for (; kk + 3 < K; kk += 64) {
+      f32x4 bv[N];
+      const f32x4 av = *reinterpret_cast<const f32x4*>(A + kk);
+#pragma unroll
+      for (int c = 0; c < N; ++c) bv[c] = *reinterpret_cast<const f32x4*>(B + (int64_t)kk * N + 4 * c);
+      chunk(av, bv);
     }
   }
-  for (; kk < K; kk += 256) {
+  for (; kk < K; kk += 64) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       if (kk + e < K) {
         const float av = A[kk + e];
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-          if (j < N) part[j] += av * B[(int64_t)(kk + e) * p.ldb + j];
+        for (int j = 0; j < N; ++j) part[j] += av * B[(int64_t)(kk + e) * p.ldb + j];
       }
     }
   }
+  float v = 0.0f;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) part[j] += __shfl_xor(part[j], off, 64);
+  for (int j = 0; j < N; ++j) {
+    float s = part[j];
+    s = dpp_add<0x128>(s);  // row_ror:8
+    s = dpp_add<0x124>(s);  // row_ror:4
+    s = dpp_add<0x04E>(s);  // quad_perm [2,3,0,1]
+    s = dpp_add<0x0B1>(s);  // quad_perm [1,0,3,2]
+    if (t == j) v = s;
   }
-  if (lane < N) {
-    float v = part[0];
-#pragma unroll
-    for (int j = 1; j < 4; ++j)
-      if (lane == j) v = part[j];
-    if (p.e) v += p.e[z * p.stride_e + row * p.lde + lane];
-    if (p.bias) v += p.bias[lane];
-    p.c[z * p.stride_c + row * p.ldc + lane] = apply_epilogue(v, p.epilogue);
+  if (row < p.m && t < N) {
+    if (p.e) v += p.e[z * p.stride_e + row * p.lde + t];
+    if (p.bias) v += p.bias[t];
+    p.c[z * p.stride_c + row * p.ldc + t] = apply_epilogue(v, p.epilogue);
   }
 }
 
@@ -373,13 +408,18 @@ __device__ __forceinline__ int a_swizzle(int row) { return (row & 7) ^ ((row >> 
 
 }  // namespace pipe
 
-template <int WM, int WN, int BLK_M, int BLK_N, int S>
-__global__ __launch_bounds__(64 * WM * WN) void gemm_packed_pipe_kernel(GemmParams p) {
-  constexpr int NW = WM * WN;
+template <int WM, int WN, int BLK_M, int BLK_N, int S, int NACC, int KS>
+__global__ __launch_bounds__(64 * WM * WN * KS) void gemm_packed_pipe_kernel(GemmParams p) {
+  static_assert(NACC == 1 || NACC == 2, "one or two accumulator chains");
+  static_assert(KS == 1 || KS == 2, "one or two k groups");
+  constexpr int NT = WM * WN;                      // waves per k group
+  constexpr int NW = NT * KS;
+  constexpr int NQ = 4 / KS;                       // 8-k quads per wave per k-block
   constexpr int BM = WM * BLK_M * 32, BN = WN * BLK_N * 32;
   constexpr int NA = BM / 8, NB = BN / 8, NBLK = NA + NB;  // 1 KiB blocks per stage
   static_assert(NBLK % NW == 0, "stage blocks split evenly over the waves");
   static_assert(S >= 2 && S <= 4, "2..4 stages");
+  static_assert(KS == 1 || NT * 2 * BLK_M * BLK_N * 2 <= S * NBLK, "exchange fits in LDS");
   constexpr int LPW = NBLK / NW;                    // DMA instructions per wave per stage
   constexpr uint32_t kStageBytes = NBLK * 1024;
   __shared__ __attribute__((aligned(1024))) f32x4 lds[S][NBLK * 64];
@@ -387,8 +427,10 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_packed_pipe_kernel(GemmPara
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave / WN;
-  const int wn = wave % WN;
+  const int kg = wave / NT;                         // k group: quads kg*NQ .. kg*NQ+NQ-1
+  const int wt = wave % NT;
+  const int wm = wt / WN;
+  const int wn = wt % WN;
   const int l32 = lane & 31;
   const int half = lane >> 5;
 
@@ -440,6 +482,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_packed_pipe_kernel(GemmPara
   };
 
   // fragment addressing (f32x4 units inside a stage)
+  const int q0 = kg * NQ;
   int a_off[BLK_M], a_swz[BLK_M];
 #pragma unroll
   for (int i = 0; i < BLK_M; ++i) {
@@ -448,18 +491,23 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_packed_pipe_kernel(GemmPara
     a_swz[i] = pipe::a_swizzle(trow);
   }
 
-  f32x16 acc[BLK_M][BLK_N];
+  // NACC = 2: even and odd k-steps accumulate into separate chains, so a wave
+  // always has an independent MFMA to issue; the chains are added at the end
+  f32x16 acc[NACC][BLK_M][BLK_N];
 #pragma unroll
-  for (int i = 0; i < BLK_M; ++i)
+  for (int c = 0; c < NACC; ++c)
 #pragma unroll
-    for (int j = 0; j < BLK_N; ++j)
+    for (int i = 0; i < BLK_M; ++i)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+      for (int j = 0; j < BLK_N; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[c][i][j][r] = 0.0f;
 
   auto compute = [&](int slot) {
     const f32x4* cur = lds[slot];
     f32x4 af[2][BLK_M], bf[2][BLK_N];
-    auto frag = [&](int q, int buf) {
+    auto frag = [&](int qi, int buf) {
+      const int q = q0 + qi;
 #pragma unroll
       for (int i = 0; i < BLK_M; ++i) af[buf][i] = cur[a_off[i] + ((4 * half + q) ^ a_swz[i])];
 #pragma unroll
@@ -467,17 +515,17 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_packed_pipe_kernel(GemmPara
     };
     frag(0, 0);
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      if (q < 3) frag(q + 1, (q + 1) & 1);
+    for (int qi = 0; qi < NQ; ++qi) {
+      if (qi < NQ - 1) frag(qi + 1, (qi + 1) & 1);
 #pragma unroll
       for (int e = 0; e < 4; ++e)
 #pragma unroll
         for (int i = 0; i < BLK_M; ++i)
 #pragma unroll
           for (int j = 0; j < BLK_N; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[q & 1][i][e], bf[q & 1][j][e],
-                                                             acc[i][j], 0, 0, 0);
-      if (q < 3) {
+            acc[e % NACC][i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(
+                af[qi & 1][i][e], bf[qi & 1][j][e], acc[e % NACC][i][j], 0, 0, 0);
+      if (qi < NQ - 1) {
         // one fragment read between consecutive MFMAs, then the rest
 #pragma unroll
         for (int r = 0; r < BLK_M + BLK_N; ++r) {
@@ -517,7 +565,8 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_packed_pipe_kernel(GemmPara
     const int kf = KT * 32;
     const int64_t tail_base = (int64_t)N * kf;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
+    for (int qi = 0; qi < NQ; ++qi) {
+      const int q = q0 + qi;
       f32x4 af[BLK_M], bf[BLK_N];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
@@ -540,28 +589,92 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_packed_pipe_kernel(GemmPara
         for (int i = 0; i < BLK_M; ++i)
 #pragma unroll
           for (int j = 0; j < BLK_N; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i][e], bf[j][e], acc[i][j], 0, 0, 0);
+            acc[e % NACC][i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(
+                af[i][e], bf[j][e], acc[e % NACC][i][j], 0, 0, 0);
     }
   }
+  if constexpr (NACC == 2) {
+#pragma unroll
+    for (int i = 0; i < BLK_M; ++i)
+#pragma unroll
+      for (int j = 0; j < BLK_N; ++j) acc[0][i][j] += acc[1][i][j];
+  }
 
-  // fused epilogue
+  // fused epilogue over accumulator registers [R0, R1)
   const float* __restrict__ E = p.e ? p.e + z * p.stride_e : nullptr;
   float* __restrict__ C = p.c + z * p.stride_c;
+  auto epilogue = [&](auto r0_c, auto r1_c) {
+    constexpr int R0 = decltype(r0_c)::value, R1 = decltype(r1_c)::value;
 #pragma unroll
-  for (int i = 0; i < BLK_M; ++i) {
+    for (int i = 0; i < BLK_M; ++i) {
 #pragma unroll
-    for (int j = 0; j < BLK_N; ++j) {
-      const int col = n0 + wn * BLK_N * 32 + j * 32 + l32;
-      if (col >= N) continue;
+      for (int j = 0; j < BLK_N; ++j) {
+        const int col = n0 + wn * BLK_N * 32 + j * 32 + l32;
+        if (col >= N) continue;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = m0 + wm * BLK_M * 32 + i * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-        if (row >= M) continue;
-        float v = acc[i][j][r];
-        if (E) v += E[(int64_t)row * p.lde + col];
-        if (p.bias) v += bias_v[j];
-        C[(int64_t)row * p.ldc + col] = apply_epilogue(v, p.epilogue);
+        for (int r = R0; r < R1; ++r) {
+          const int row = m0 + wm * BLK_M * 32 + i * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+          if (row >= M) continue;
+          float v = acc[0][i][j][r];
+          if (E) v += E[(int64_t)row * p.lde + col];
+          if (p.bias) v += bias_v[j];
+          C[(int64_t)row * p.ldc + col] = apply_epilogue(v, p.epilogue);
+        }
       }
+    }
+  };
+  using I0 = std::integral_constant<int, 0>;
+  using I8 = std::integral_constant<int, 8>;
+  using I16 = std::integral_constant<int, 16>;
+  if constexpr (KS == 1) {
+    epilogue(I0{}, I16{});
+  } else {
+    // The two k groups hold partial sums of the same outputs.  Group g keeps
+    // registers [8g, 8g+8) and hands the other eight to its partner through
+    // LDS; each output is then partial(0) + partial(1) whichever wave adds.
+    f32x4* xch = &lds[0][0];
+    auto slot = [&](int owner, int blk, int u) {
+      return ((wt * 2 + owner) * BLK_M * BLK_N + blk) * 2 * 64 + u * 64 + lane;
+    };
+    auto send = [&](auto g_c) {
+      constexpr int G = 1 - decltype(g_c)::value;  // receiver; its registers [8G, 8G+8)
+#pragma unroll
+      for (int i = 0; i < BLK_M; ++i)
+#pragma unroll
+        for (int j = 0; j < BLK_N; ++j)
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            f32x4 v;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) v[c] = acc[0][i][j][8 * G + 4 * u + c];
+            xch[slot(G, i * BLK_N + j, u)] = v;
+          }
+    };
+    auto receive = [&](auto g_c) {
+      constexpr int G = decltype(g_c)::value;
+#pragma unroll
+      for (int i = 0; i < BLK_M; ++i)
+#pragma unroll
+        for (int j = 0; j < BLK_N; ++j)
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            const f32x4 v = xch[slot(G, i * BLK_N + j, u)];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) acc[0][i][j][8 * G + 4 * u + c] += v[c];
+          }
+    };
+    pipe::block_barrier();  // every wave is done with the pipeline stages
+    if (kg == 0)
+      send(I0{});
+    else
+      send(std::integral_constant<int, 1>{});
+    pipe::block_barrier();
+    if (kg == 0) {
+      receive(I0{});
+      epilogue(I0{}, I8{});
+    } else {
+      receive(std::integral_constant<int, 1>{});
+      epilogue(I8{}, I16{});
     }
   }
 }
@@ -598,15 +711,15 @@ int launch_tile(const GemmParams& p0, int64_t batch, hipStream_t stream) {
   return ANNC_OK;
 }
 
-template <int WM, int WN, int BMB, int BNB, int S>
+template <int WM, int WN, int BMB, int BNB, int S, int NACC, int KS>
 int launch_pipe(const GemmParams& p0, int64_t batch, hipStream_t stream) {
   constexpr int BM = WM * BMB * 32, BN = WN * BNB * 32;
   GemmParams p = p0;
   p.tiles_m = (p.m + BM - 1) / BM;
   p.tiles_n = (p.n + BN - 1) / BN;
   dim3 grid(p.tiles_m * p.tiles_n, 1, (unsigned)batch);
-  hipLaunchKernelGGL((gemm_packed_pipe_kernel<WM, WN, BMB, BNB, S>), grid, dim3(64 * WM * WN), 0,
-                     stream, p);
+  hipLaunchKernelGGL((gemm_packed_pipe_kernel<WM, WN, BMB, BNB, S, NACC, KS>), grid,
+                     dim3(64 * WM * WN * KS), 0, stream, p);
   ANNC_HIP_TRY(hipGetLastError());
   return ANNC_OK;
 }
@@ -618,9 +731,11 @@ int launch_packed_pipe(const GemmParams& p, int64_t batch, hipStream_t stream) {
   auto tiles = [&](int bm, int bn) {
     return ((int64_t)(p.m + bm - 1) / bm) * ((p.n + bn - 1) / bn) * batch;
   };
-  if (tiles(128, 128) >= cus) return launch_pipe<4, 2, 1, 2, 3>(p, batch, stream);
-  if (tiles(128, 64) >= cus) return launch_pipe<4, 2, 1, 1, 4>(p, batch, stream);
-  return launch_pipe<2, 2, 1, 1, 4>(p, batch, stream);
+  if (tiles(128, 128) >= cus) return launch_pipe<4, 2, 1, 2, 3, 1, 1>(p, batch, stream);
+  if (tiles(128, 64) >= cus) return launch_pipe<4, 2, 1, 1, 3, 2, 1>(p, batch, stream);
+  // 64x64 tiles leave one wave per SIMD; split each k-block over two wave
+  // groups so every SIMD runs two
+  return launch_pipe<2, 2, 1, 1, 2, 1, 2>(p, batch, stream);
 }
 
 template <bool PACKED>
@@ -689,10 +804,16 @@ int annc_hip_gemm(void* stream, int64_t batch, int64_t m, int64_t n, int64_t k, 
   auto aligned16 = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
   p.a_vec = (lda % 4 == 0) && (stride_a % 4 == 0) && aligned16(a);
   p.b_vec = (ldb % 4 == 0) && (stride_b % 4 == 0) && aligned16(b);
+  p.b_dense = (p.ldb == n) && (stride_b % 4 == 0) && aligned16(b);
 
   if (n <= 4) {
-    dim3 grid((unsigned)ceil_div(m, kThreads / 64), 1, (unsigned)batch);
-    hipLaunchKernelGGL(gemv_kernel, grid, dim3(kThreads), 0, s, p);
+    dim3 grid((unsigned)ceil_div(m, kThreads / 16), 1, (unsigned)batch);
+    switch (n) {
+      case 1: hipLaunchKernelGGL(gemv_rows_kernel<1>, grid, dim3(kThreads), 0, s, p); break;
+      case 2: hipLaunchKernelGGL(gemv_rows_kernel<2>, grid, dim3(kThreads), 0, s, p); break;
+      case 3: hipLaunchKernelGGL(gemv_rows_kernel<3>, grid, dim3(kThreads), 0, s, p); break;
+      default: hipLaunchKernelGGL(gemv_rows_kernel<4>, grid, dim3(kThreads), 0, s, p); break;
+    }
     ANNC_HIP_TRY(hipGetLastError());
     return set_error(ANNC_OK, "");
   }

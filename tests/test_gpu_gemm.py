@@ -131,6 +131,53 @@ def test_batch_matmul(batch, m, n, k):
         assert_gemm_close(out[i], ref[i], gemm_bound(a[i], b[i]))
 
 
+# N <= 4 runs the 16-lanes-per-row kernel: float4 loads of A and of the dense
+# [K, N] B block when both are aligned (four chunks at a time while k + 195 < K,
+# then single chunks), scalar loads otherwise; rows past M are clamped.
+SKINNY_CASES = [
+    (1, 4096, 1, 256, "tower scoring layer"),
+    (1, 257, 4, 1000, "K with unrolled, single and tail chunks"),
+    (1, 5, 4, 196, "K at the unrolled-loop boundary"),
+    (1, 1000, 3, 130, "lda % 4 != 0: scalar path"),
+    (1, 33, 2, 7, "tiny K"),
+    (1, 64, 1, 1, "K = 1"),
+    (3, 100, 2, 300, "batched A and B"),
+]
+
+
+@pytest.mark.parametrize("batch,m,n,k,what", SKINNY_CASES)
+@pytest.mark.parametrize("layout", ["dense", "ldb>n", "a offset"])
+def test_skinny_n(batch, m, n, k, what, layout):
+    note(f"skinny-N gemm {batch}x{m}x{n}x{k} {layout}: {what}")
+    g = workloads.rng(batch * m + 11 * n + k)
+    a = g.standard_normal((batch, m, k)).astype(np.float32)
+    b = (g.standard_normal((batch, k, n)) * 0.1).astype(np.float32)
+    e = g.standard_normal((batch, m, n)).astype(np.float32)
+    bias = g.standard_normal(n).astype(np.float32)
+    if layout == "ldb>n":  # B as the first n columns of a wider matrix
+        wide = to_dev(np.concatenate([b, np.ones((batch, k, 3), np.float32)], axis=2))
+        db = wide[:, :, :n]
+    else:
+        db = to_dev(b)
+    if layout == "a offset":  # A rows start 4 bytes past an aligned address
+        flat = torch.zeros(batch * m * k + 1, dtype=torch.float32, device=device())
+        flat[1:] = to_dev(a).reshape(-1)
+        da = flat[1:].view(batch, m, k)
+    else:
+        da = to_dev(a)
+    if batch == 1:
+        da, db = da[0], db[0]
+    got = to_host(dev.gemm(da, db, bias=to_dev(bias), epilogue=EPI_RELU)).reshape(batch, m, n)
+    for z in range(batch):
+        ref = ora.dense_layer(a[z], b[z], bias, 1)
+        assert_gemm_close(got[z], ref, gemm_bound(a[z], b[z], np.broadcast_to(bias, (m, n))))
+    de = to_dev(e) if batch > 1 else to_dev(e[0])
+    got = to_host(dev.gemm(da, db, addend=de, epilogue=EPI_SIGMOID)).reshape(batch, m, n)
+    for z in range(batch):
+        lin = ora.matmul_add(e[z], a[z], b[z]).astype(np.float64)
+        np.testing.assert_allclose(got[z], 1.0 / (1.0 + np.exp(-lin)), rtol=1e-4, atol=1e-5)
+
+
 @pytest.mark.parametrize("epi", [EPI_NONE, EPI_RELU, EPI_SIGMOID])
 @pytest.mark.parametrize("packed", [False, True])
 def test_bias_epilogues_and_padded_lda(epi, packed):
