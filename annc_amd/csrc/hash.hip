@@ -452,6 +452,149 @@ void launch_hashed_wave_g(const FieldSet& fs, int64_t f0, int64_t nf, int64_t ba
                        nf, batch, dim, wpf, ids, offsets, out, ldo, buckets_out);
 }
 
+// Fused multi-field hash -> bucket -> gather -> pool with the row offsets
+// staged in LDS.  A wave owns a run of BW = (64/G)*R consecutive bags of one
+// field.  Phase 1 hashes the run's positions 64 at a time -- every lane busy
+// except in the last chunk -- into the wave's LDS window as row byte offsets
+// (positions past the run carry an offset past the buffer's range check).
+// Phase 2: the 64/G lane groups take R bags each (bag r*(64/G) + group), G
+// lanes per bag with 4 floats per lane, and walk the bags in index order,
+// reading offsets from LDS and rows through raw buffer loads, all R bags'
+// loads in flight together.  A run longer than the window is processed in
+// windows, the sums carried across them in position order.  Requires
+// dim <= 4G (one column pass).
+template <int G, int R, bool MEAN>
+__global__ __launch_bounds__(kThreads) void hashed_bags_lds_kernel(
+    FieldSet fs, int64_t field0, int64_t nfields, int64_t batch, int64_t dim,
+    int64_t waves_per_field, const int64_t* __restrict__ ids, const int64_t* __restrict__ offsets,
+    float* __restrict__ out, int64_t ldo, int64_t* __restrict__ buckets_out) {
+  typedef float f32x4 __attribute__((ext_vector_type(4)));
+  constexpr int NB = 64 / G;   // lane groups
+  constexpr int BW = NB * R;   // bags per wave
+  static_assert(BW <= 64, "one bag start per lane");
+  constexpr int kChunks = 4;   // 64-position chunks per window
+  constexpr int kWin = 64 * kChunks;
+  constexpr int U = 4;         // positions per bag per round
+  __shared__ uint32_t win_off[kThreads / 64][kWin];
+  const int lane = threadIdx.x & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t w = (int64_t)blockIdx.x * (kThreads / 64) + wid;
+  if (w >= nfields * waves_per_field) return;
+  const int fl = static_cast<int>(w / waves_per_field);
+  const int64_t b0 = (w - (int64_t)fl * waves_per_field) * BW;
+  const int64_t f = field0 + fl;
+  const int nbag = static_cast<int>(batch - b0 < BW ? batch - b0 : BW);
+  const int64_t* __restrict__ run = offsets + f * batch + b0;
+  const int64_t wbeg = run[0];
+  const int64_t wend = run[nbag];
+  // lane i < nbag holds the start of bag i; the others hold the run's end
+  const int64_t start = run[lane < nbag ? lane : nbag];
+  const int grp = lane / G;
+  const int g = lane & (G - 1);
+  int64_t beg[R], end[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int j = r * NB + grp;
+    beg[r] = __shfl(start, j, 64);
+    const int64_t nx = __shfl(start, (j + 1) & 63, 64);
+    end[r] = j + 1 < 64 ? nx : wend;
+  }
+  const U64Divisor dv = fs.div[fl];
+  const uint32_t row_bytes = static_cast<uint32_t>(dim * sizeof(float));
+  const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float*>(fs.table[fl]), 0, static_cast<int>(fs.rows[fl] * row_bytes),
+      kRawBufferFlags);
+  const int c = g * 4;
+  const bool active = c < dim;
+  const uint32_t c_off = active ? static_cast<uint32_t>(c * sizeof(float)) : kMaskedOff;
+  uint32_t* __restrict__ win = win_off[wid];
+  f32x4 acc[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) acc[r] = f32x4(0.0f);
+
+  for (int64_t w0 = wbeg; w0 < wend; w0 += kWin) {
+    const int64_t wlen64 = wend - w0 < kWin ? wend - w0 : kWin;
+    const int wlen = static_cast<int>(wlen64);
+    // ids of the window, all loads issued before any hashing
+    int64_t idv[kChunks];
+#pragma unroll
+    for (int ch = 0; ch < kChunks; ++ch) {
+      const int q = 64 * ch + lane;
+      idv[ch] = ids[w0 + (q < wlen ? q : wlen - 1)];
+    }
+#pragma unroll
+    for (int ch = 0; ch < kChunks; ++ch) {
+      if (64 * ch < wlen) {
+        const int q = 64 * ch + lane;
+        const uint64_t bucket = mod_invariant(fp64_text(int64_text(idv[ch])), dv);
+        win[q] = q < wlen ? static_cast<uint32_t>(bucket) * row_bytes : kMaskedOff;
+        if (buckets_out && q < wlen) buckets_out[w0 + q] = static_cast<int64_t>(bucket);
+      }
+    }
+    // LDS writes of this wave are visible to its own later reads
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    int lo[R], cnt[R];
+    bool more = false;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int64_t l = beg[r] > w0 ? beg[r] : w0;
+      const int64_t h = end[r] < w0 + wlen ? end[r] : w0 + wlen;
+      lo[r] = static_cast<int>(l - w0);
+      cnt[r] = h > l ? static_cast<int>(h - l) : 0;
+      more = more || cnt[r] > 0;
+    }
+    for (int u0 = 0; __ballot(more) != 0; u0 += U) {
+      f32x4 v[R][U];
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int i = 0; i < U; ++i) {
+          const int u = u0 + i;
+          const uint32_t off = win[(lo[r] + u) & (kWin - 1)];
+          const u32x4 raw = __builtin_amdgcn_raw_buffer_load_b128(
+              rsrc, static_cast<int>((u < cnt[r] ? off : kMaskedOff) + c_off), 0, 0);
+          v[r][i] = __builtin_bit_cast(f32x4, raw);
+        }
+      more = false;
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+#pragma unroll
+        for (int i = 0; i < U; ++i) acc[r] += v[r][i];
+        more = more || cnt[r] > u0 + U;
+      }
+    }
+    // the next window's LDS writes must not pass this window's reads
+    __builtin_amdgcn_wave_barrier();
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int j = r * NB + grp;
+    if (MEAN) {
+      const int32_t n = static_cast<int32_t>(end[r] - beg[r]);
+      if (n > 0) acc[r] *= 1.0f / static_cast<float>(n);
+    }
+    if (active && j < nbag)
+      *reinterpret_cast<f32x4*>(out + (b0 + j) * ldo + f * dim + c) = acc[r];
+  }
+}
+
+template <int G, int R>
+void launch_hashed_lds_g(const FieldSet& fs, int64_t f0, int64_t nf, int64_t batch, int64_t dim,
+                         const int64_t* ids, const int64_t* offsets, int combiner, float* out,
+                         int64_t ldo, int64_t* buckets_out, hipStream_t s) {
+  constexpr int BW = (64 / G) * R;
+  const int64_t wpf = (batch + BW - 1) / BW;
+  dim3 grid((unsigned)ceil_div(nf * wpf, kThreads / 64));
+  if (combiner == ANNC_COMBINER_MEAN)
+    hipLaunchKernelGGL((hashed_bags_lds_kernel<G, R, true>), grid, dim3(kThreads), 0, s, fs, f0,
+                       nf, batch, dim, wpf, ids, offsets, out, ldo, buckets_out);
+  else
+    hipLaunchKernelGGL((hashed_bags_lds_kernel<G, R, false>), grid, dim3(kThreads), 0, s, fs, f0,
+                       nf, batch, dim, wpf, ids, offsets, out, ldo, buckets_out);
+}
+
 // Fused multi-field hash -> bucket -> gather -> pool.  A bag is owned by a
 // group of G lanes (4 floats of the row each).  The group hashes up to G
 // ids at once (one per lane), then every lane walks the bag in index order,
@@ -669,10 +812,10 @@ int annc_hip_hashed_embedding_bags(void* stream, int64_t num_fields, int64_t bat
     if (small_tables) {
       if (lanes <= 4)
         launch_hashed_wave_g<4>(fs, f0, nf, batch, dim, ids, offsets, combiner, out, ldo, buckets_out, s);
-      else if (lanes <= 8)
-        launch_hashed_wave_g<8>(fs, f0, nf, batch, dim, ids, offsets, combiner, out, ldo, buckets_out, s);
+      else if (lanes <= 8)  // two bags per lane group: more positions hashed per wave
+        launch_hashed_lds_g<8, 2>(fs, f0, nf, batch, dim, ids, offsets, combiner, out, ldo, buckets_out, s);
       else if (lanes <= 16)
-        launch_hashed_wave_g<16>(fs, f0, nf, batch, dim, ids, offsets, combiner, out, ldo, buckets_out, s);
+        launch_hashed_lds_g<16, 2>(fs, f0, nf, batch, dim, ids, offsets, combiner, out, ldo, buckets_out, s);
       else if (lanes <= 32)
         launch_hashed_wave_g<32>(fs, f0, nf, batch, dim, ids, offsets, combiner, out, ldo, buckets_out, s);
       else

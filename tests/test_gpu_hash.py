@@ -106,6 +106,24 @@ def test_hashed_bags_dims_sum(dim):
     np.testing.assert_array_equal(to_host(out), ref)
 
 
+@pytest.mark.parametrize("dim", [16, 32, 64])
+def test_hashed_bags_long_bags_mean(dim):
+    """Bags of 40-130 ids: a wave's run of bags spans several windows of
+    staged row offsets, and single bags straddle window edges."""
+    note(f"hashed bags long bags dim={dim}")
+    g = workloads.rng(dim + 2)
+    nf, batch, rows = 2, 67, 5000
+    ids, offsets = workloads.hashed_structure(g, nf, batch, lo=40, hi=130)
+    tables = [g.standard_normal((rows, dim)).astype(np.float32) for _ in range(nf)]
+    ref, ref_buckets = ora.hashed_embedding_bags(tables, rows, ids, offsets, batch, 1,
+                                                 with_buckets=True)
+    buckets = to_dev(np.full(ids.size, -7, dtype=np.int64))
+    out = dev.hashed_embedding_bags([to_dev(t) for t in tables], [rows] * nf, to_dev(ids),
+                                    to_dev(offsets), batch, 1, buckets_out=buckets)
+    np.testing.assert_array_equal(to_host(buckets), ref_buckets)
+    np.testing.assert_array_equal(to_host(out), ref)
+
+
 def test_tf_embedding_with_hash_bucket_ops():
     note("tf hash bucket ops")
     g = workloads.rng(5)
