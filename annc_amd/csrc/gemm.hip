@@ -357,6 +357,128 @@ __global__ __launch_bounds__(kThreads) void gemv_rows_kernel(GemmParams p) {
   }
 }
 
+// Small row-major GEMMs (few output tiles, e.g. the 512x256x256 custom call):
+// one 32x32 output block per workgroup and the K dimension split over its W
+// waves (wave w takes k-blocks w, w+W, ...), so a 512x256 output still runs
+// 128 workgroups x W waves.  Each wave loads its MFMA operands straight from
+// global memory -- A as one float4 per lane per 4 k (row l32, k chunk
+// 16*half + 4q), B as one float per lane per k (row k, column l32) -- one
+// k-block ahead of the MFMAs, with two accumulator chains.  Full k-blocks
+// load unguarded (rows and columns past the edge are clamped, computed and
+// never stored), so the loads carry no branches; the K % 32 tail is one
+// guarded block afterwards.  The W partial blocks meet in LDS and wave v
+// adds registers 4v..4v+3 over w = 0..W-1 in that order before the fused
+// epilogue.
+template <int W, bool AVEC>
+__global__ __launch_bounds__(64 * W) void gemm_small_kernel(GemmParams p) {
+  static_assert(W == 4 || W == 8, "4 or 8 waves");
+  __shared__ float red[W][16][64];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int l32 = lane & 31;
+  const int half = lane >> 5;
+  const int m0 = (blockIdx.x / p.tiles_n) * 32;
+  const int n0 = (blockIdx.x % p.tiles_n) * 32;
+  const int64_t z = blockIdx.z;
+  const int M = p.m, N = p.n, K = p.k;
+  const int KF = K >> 5;  // full k-blocks
+  const int col = n0 + l32;
+  const bool col_ok = col < N;
+  const float* __restrict__ arow = p.a + z * p.stride_a + (int64_t)min(m0 + l32, M - 1) * p.lda;
+  const float* __restrict__ bcol = p.b + z * p.stride_b + min(col, N - 1);
+  const int64_t ldb = p.ldb;
+  // the addend of the four output registers this wave finishes (wave & 3),
+  // fetched before the k-loop; without an addend the loads re-read C and are
+  // ignored, so no wave branches around them
+  const float* __restrict__ E = p.e ? p.e + z * p.stride_e : nullptr;
+  float* __restrict__ C = p.c + z * p.stride_c;
+  const float* __restrict__ esrc = E ? E : C;
+  const int64_t lde = E ? p.lde : p.ldc;
+  float e_pre[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int orow = min(m0 + 8 * (wave & 3) + 4 * half + i, M - 1);
+    e_pre[i] = esrc[(int64_t)orow * lde + min(col, N - 1)];
+  }
+
+  f32x4 af[2][4];
+  float bf[2][16];
+  auto load = [&](int kt, int buf) {
+    const int kb = kt * 32 + 16 * half;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      if constexpr (AVEC) {
+        af[buf][q] = *reinterpret_cast<const f32x4*>(arow + kb + 4 * q);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) af[buf][q][e] = arow[kb + 4 * q + e];
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) bf[buf][4 * q + e] = bcol[(int64_t)(kb + 4 * q + e) * ldb];
+    }
+  };
+  f32x16 acc[2];
+#pragma unroll
+  for (int c = 0; c < 2; ++c)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[c][r] = 0.0f;
+  auto mma = [&](int buf) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        acc[e & 1] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[buf][q][e], bf[buf][4 * q + e],
+                                                          acc[e & 1], 0, 0, 0);
+  };
+  if (wave < KF) {
+    // blocks wave, wave+W, ...; the prefetch of a block past the end
+    // re-reads the current one instead of branching
+    // sched_barrier keeps each prefetch issued ahead of the MFMAs it overlaps
+    load(wave, 0);
+    for (int kt = wave; kt < KF; kt += 2 * W) {
+      load(kt + W < KF ? kt + W : kt, 1);
+      __builtin_amdgcn_sched_barrier(0);
+      mma(0);
+      __builtin_amdgcn_sched_barrier(0);
+      if (kt + W >= KF) break;
+      load(kt + 2 * W < KF ? kt + 2 * W : kt + W, 0);
+      __builtin_amdgcn_sched_barrier(0);
+      mma(1);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  if ((K & 31) && wave == KF % W) {
+    const int kb = KF * 32 + 16 * half;
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int k = kb + 4 * q + e;
+        af[0][q][e] = k < K ? arow[k] : 0.0f;
+        bf[0][4 * q + e] = k < K ? bcol[(int64_t)k * ldb] : 0.0f;
+      }
+    mma(0);
+  }
+  acc[0] += acc[1];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) red[wave][r][lane] = acc[0][r];
+  __syncthreads();
+  if (wave >= 4) return;
+  const float bias = (p.bias && col_ok) ? p.bias[col] : 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = 4 * wave + i;
+    float v = red[0][r][lane];
+#pragma unroll
+    for (int w = 1; w < W; ++w) v += red[w][r][lane];
+    const int orow = m0 + 8 * wave + 4 * half + i;  // 8*(r>>2) + 4*half + (r&3)
+    if (orow >= M || !col_ok) continue;
+    if (E) v += e_pre[i];
+    if (p.bias) v += bias;
+    C[(int64_t)orow * p.ldc + col] = apply_epilogue(v, p.epilogue);
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Packed-B pipelined kernel (the __layout_matmul path, N % 32 == 0).
 //
@@ -738,6 +860,20 @@ int launch_packed_pipe(const GemmParams& p, int64_t batch, hipStream_t stream) {
   return launch_pipe<2, 2, 1, 1, 2, 1, 2>(p, batch, stream);
 }
 
+template <int W>
+int launch_small(const GemmParams& p0, int64_t batch, hipStream_t stream) {
+  GemmParams p = p0;
+  p.tiles_m = (p.m + 31) / 32;
+  p.tiles_n = (p.n + 31) / 32;
+  dim3 grid(p.tiles_m * p.tiles_n, 1, (unsigned)batch);
+  if (p.a_vec)
+    hipLaunchKernelGGL((gemm_small_kernel<W, true>), grid, dim3(64 * W), 0, stream, p);
+  else
+    hipLaunchKernelGGL((gemm_small_kernel<W, false>), grid, dim3(64 * W), 0, stream, p);
+  ANNC_HIP_TRY(hipGetLastError());
+  return ANNC_OK;
+}
+
 template <bool PACKED>
 int launch_gemm(const GemmParams& p, int64_t batch, hipStream_t stream) {
   // Largest tile that still gives every CU a workgroup (256 CUs on MI355X).
@@ -745,6 +881,9 @@ int launch_gemm(const GemmParams& p, int64_t batch, hipStream_t stream) {
   auto tiles = [&](int bm, int bn) {
     return ((int64_t)(p.m + bm - 1) / bm) * ((p.n + bn - 1) / bn) * batch;
   };
+  // Too few 64x64 tiles to occupy the chip: 32x32 blocks with K split over
+  // four waves (eight measured slower at every K)
+  if (!PACKED && tiles(64, 64) < cus / 2) return launch_small<4>(p, batch, stream);
   if (tiles(128, 128) >= cus) return launch_tile<2, 2, 2, 2, PACKED>(p, batch, stream);
   if (tiles(64, 128) >= cus) return launch_tile<2, 2, 1, 2, PACKED>(p, batch, stream);
   return launch_tile<2, 2, 1, 1, PACKED>(p, batch, stream);
