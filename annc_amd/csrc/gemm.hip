@@ -485,10 +485,15 @@ __global__ __launch_bounds__(64 * W) void gemm_small_kernel(GemmParams p) {
 // Operand tiles stream global -> LDS through gfx950's 16-byte LDS-DMA loads
 // (global_load_lds_dwordx4: lane i of a wave writes bytes [16i, 16i+16) of a
 // 1 KiB LDS block), S stages deep, so no VGPRs stage the data and up to S-1
-// k-blocks are in flight while the MFMAs run on the oldest.  One barrier per
-// k-block: a wave waits for its own DMAs of stage kt (vmcnt), the barrier
-// publishes everyone's, and only then is the slot freed by stage kt-1
-// refilled.
+// stages are in flight while the MFMAs run on the oldest.  A stage holds
+// KSUB consecutive 32-k blocks.  One barrier per stage: a wave waits for its
+// own DMAs of the stage (vmcnt), the barrier publishes everyone's, and only
+// then is the slot freed by the previous stage refilled.
+//   * WM x WN waves own BLK_M x BLK_N 32x32 accumulator blocks each; with
+//     KS = 2 a second group of WM x WN waves takes the other half of every
+//     k-block (quads 2-3) and the two partial tiles are added through LDS
+//     before the epilogue.  NACC = 2 alternates two accumulator chains per
+//     block so a wave always has an independent MFMA to issue.
 //   * A block = 8 full rows x 32 k (eight 128-byte lines per instruction);
 //     lane i loads row i/8, 16-byte chunk (i%8) ^ swz(row), so each MFMA
 //     fragment read (row = lane%32, chunk 4*(lane/32)+q) hits 64 distinct
@@ -530,10 +535,11 @@ __device__ __forceinline__ int a_swizzle(int row) { return (row & 7) ^ ((row >> 
 
 }  // namespace pipe
 
-template <int WM, int WN, int BLK_M, int BLK_N, int S, int NACC, int KS>
+template <int WM, int WN, int BLK_M, int BLK_N, int S, int NACC, int KS, int KSUB>
 __global__ __launch_bounds__(64 * WM * WN * KS) void gemm_packed_pipe_kernel(GemmParams p) {
   static_assert(NACC == 1 || NACC == 2, "one or two accumulator chains");
   static_assert(KS == 1 || KS == 2, "one or two k groups");
+  static_assert(KSUB == 1 || KSUB == 2, "one or two 32-k blocks per stage");
   constexpr int NT = WM * WN;                      // waves per k group
   constexpr int NW = NT * KS;
   constexpr int NQ = 4 / KS;                       // 8-k quads per wave per k-block
@@ -541,10 +547,11 @@ __global__ __launch_bounds__(64 * WM * WN * KS) void gemm_packed_pipe_kernel(Gem
   constexpr int NA = BM / 8, NB = BN / 8, NBLK = NA + NB;  // 1 KiB blocks per stage
   static_assert(NBLK % NW == 0, "stage blocks split evenly over the waves");
   static_assert(S >= 2 && S <= 4, "2..4 stages");
-  static_assert(KS == 1 || NT * 2 * BLK_M * BLK_N * 2 <= S * NBLK, "exchange fits in LDS");
-  constexpr int LPW = NBLK / NW;                    // DMA instructions per wave per stage
-  constexpr uint32_t kStageBytes = NBLK * 1024;
-  __shared__ __attribute__((aligned(1024))) f32x4 lds[S][NBLK * 64];
+  static_assert(KS == 1 || NT * 2 * BLK_M * BLK_N * 2 <= S * KSUB * NBLK, "exchange fits in LDS");
+  constexpr int LPW = NBLK / NW;                    // DMA instructions per wave per k-block
+  constexpr uint32_t kSubBytes = NBLK * 1024;
+  constexpr uint32_t kStageBytes = KSUB * kSubBytes;
+  __shared__ __attribute__((aligned(1024))) f32x4 lds[S][KSUB * NBLK * 64];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -566,6 +573,7 @@ __global__ __launch_bounds__(64 * WM * WN * KS) void gemm_packed_pipe_kernel(Gem
   const float* __restrict__ B = p.b + z * p.stride_b;
   const int M = p.m, N = p.n, K = p.k;
   const int KT = K >> 5;          // full k-blocks
+  const int KB = KT / KSUB;       // stages (KT % KSUB == 0 on this path)
   const int panels = N >> 5;      // N % 32 == 0 on this path
 
   // bias of this lane's columns, fetched before the pipeline starts
@@ -597,10 +605,13 @@ __global__ __launch_bounds__(64 * WM * WN * KS) void gemm_packed_pipe_kernel(Gem
       step[i] = 1024;
     }
   }
-  auto issue = [&](int slot, int kt) {
+  auto issue = [&](int slot, int kb) {
 #pragma unroll
-    for (int i = 0; i < LPW; ++i)
-      pipe::dma16(src[i] + (int64_t)kt * step[i], dst[i] + slot * kStageBytes);
+    for (int sub = 0; sub < KSUB; ++sub)
+#pragma unroll
+      for (int i = 0; i < LPW; ++i)
+        pipe::dma16(src[i] + (int64_t)(kb * KSUB + sub) * step[i],
+                    dst[i] + slot * kStageBytes + sub * kSubBytes);
   };
 
   // fragment addressing (f32x4 units inside a stage)
@@ -625,8 +636,7 @@ __global__ __launch_bounds__(64 * WM * WN * KS) void gemm_packed_pipe_kernel(Gem
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[c][i][j][r] = 0.0f;
 
-  auto compute = [&](int slot) {
-    const f32x4* cur = lds[slot];
+  auto compute_sub = [&](const f32x4* cur) {
     f32x4 af[2][BLK_M], bf[2][BLK_N];
     auto frag = [&](int qi, int buf) {
       const int q = q0 + qi;
@@ -658,25 +668,29 @@ __global__ __launch_bounds__(64 * WM * WN * KS) void gemm_packed_pipe_kernel(Gem
       }
     }
   };
+  auto compute = [&](int slot) {
+#pragma unroll
+    for (int sub = 0; sub < KSUB; ++sub) compute_sub(&lds[slot][sub * NBLK * 64]);
+  };
 
 #pragma unroll
   for (int s = 0; s < S - 1; ++s)
-    if (s < KT) issue(s, s);
-  for (int kt0 = 0; kt0 < KT; kt0 += S) {
+    if (s < KB) issue(s, s);
+  for (int kb0 = 0; kb0 < KB; kb0 += S) {
 #pragma unroll
     for (int u = 0; u < S; ++u) {
-      const int kt = kt0 + u;
-      if (kt < KT) {
-        // stages kt+1 .. kt+S-2 may stay in flight
-        const int after = min(KT - 1 - kt, S - 2);
+      const int kb = kb0 + u;
+      if (kb < KB) {
+        // stages kb+1 .. kb+S-2 may stay in flight
+        const int after = min(KB - 1 - kb, S - 2);
         if (after >= 2)
-          pipe::wait_vmcnt<2 * LPW>();
+          pipe::wait_vmcnt<2 * KSUB * LPW>();
         else if (after == 1)
-          pipe::wait_vmcnt<LPW>();
+          pipe::wait_vmcnt<KSUB * LPW>();
         else
           pipe::wait_vmcnt<0>();
         pipe::block_barrier();
-        if (kt + S - 1 < KT) issue((u + S - 1) % S, kt + S - 1);
+        if (kb + S - 1 < KB) issue((u + S - 1) % S, kb + S - 1);
         compute(u);
       }
     }
@@ -833,14 +847,14 @@ int launch_tile(const GemmParams& p0, int64_t batch, hipStream_t stream) {
   return ANNC_OK;
 }
 
-template <int WM, int WN, int BMB, int BNB, int S, int NACC, int KS>
+template <int WM, int WN, int BMB, int BNB, int S, int NACC, int KS, int KSUB = 1>
 int launch_pipe(const GemmParams& p0, int64_t batch, hipStream_t stream) {
   constexpr int BM = WM * BMB * 32, BN = WN * BNB * 32;
   GemmParams p = p0;
   p.tiles_m = (p.m + BM - 1) / BM;
   p.tiles_n = (p.n + BN - 1) / BN;
   dim3 grid(p.tiles_m * p.tiles_n, 1, (unsigned)batch);
-  hipLaunchKernelGGL((gemm_packed_pipe_kernel<WM, WN, BMB, BNB, S, NACC, KS>), grid,
+  hipLaunchKernelGGL((gemm_packed_pipe_kernel<WM, WN, BMB, BNB, S, NACC, KS, KSUB>), grid,
                      dim3(64 * WM * WN * KS), 0, stream, p);
   ANNC_HIP_TRY(hipGetLastError());
   return ANNC_OK;
@@ -853,11 +867,19 @@ int launch_packed_pipe(const GemmParams& p, int64_t batch, hipStream_t stream) {
   auto tiles = [&](int bm, int bn) {
     return ((int64_t)(p.m + bm - 1) / bm) * ((p.n + bn - 1) / bn) * batch;
   };
-  if (tiles(128, 128) >= cus) return launch_pipe<4, 2, 1, 2, 3, 1, 1>(p, batch, stream);
-  if (tiles(128, 64) >= cus) return launch_pipe<4, 2, 1, 1, 3, 2, 1>(p, batch, stream);
+  // An even number of full k-blocks streams 64 k per stage (half the
+  // barriers); an odd one 32.
+  const bool k64 = ((p.k >> 5) & 1) == 0;
+  if (tiles(128, 128) >= cus)
+    return k64 ? launch_pipe<4, 2, 1, 2, 2, 1, 1, 2>(p, batch, stream)
+               : launch_pipe<4, 2, 1, 2, 3, 1, 1, 1>(p, batch, stream);
+  if (tiles(128, 64) >= cus)
+    return k64 ? launch_pipe<4, 2, 1, 1, 2, 2, 1, 2>(p, batch, stream)
+               : launch_pipe<4, 2, 1, 1, 3, 2, 1, 1>(p, batch, stream);
   // 64x64 tiles leave one wave per SIMD; split each k-block over two wave
   // groups so every SIMD runs two
-  return launch_pipe<2, 2, 1, 1, 2, 1, 2>(p, batch, stream);
+  return k64 ? launch_pipe<2, 2, 1, 1, 2, 2, 2, 2>(p, batch, stream)
+             : launch_pipe<2, 2, 1, 1, 2, 1, 2, 1>(p, batch, stream);
 }
 
 template <int W>
