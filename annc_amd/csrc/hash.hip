@@ -172,13 +172,8 @@ __device__ uint64_t fp64_bytes(const unsigned char* s, uint64_t len) {
 }
 
 // ---------------------------------------------------------------------------
-// Decimal text of an int64 held in registers.
+// Fingerprint64 of the decimal text of an int64, built in registers.
 // ---------------------------------------------------------------------------
-struct Text24 {
-  uint64_t w0, w1, w2;  // little-endian bytes: w0 holds characters 0..7
-  uint32_t len;
-};
-
 // Two ASCII digits of p < 100, tens in the low byte: p / 10 as (p * 103) >> 10
 // (exact below 179) on the full-rate 24-bit multiplier.
 __device__ __forceinline__ uint32_t ascii_pair(uint32_t p) {
@@ -206,91 +201,83 @@ __device__ __forceinline__ uint64_t ascii3(uint32_t x) {
   return (0x30u + h) | (ascii_pair(x - __umul24(h, 100u)) << 8);
 }
 
-__device__ __forceinline__ uint32_t count_digits8(uint32_t x) {
-  return 1u + (x >= 10u) + (x >= 100u) + (x >= 1000u) + (x >= 10000u) + (x >= 100000u) +
-         (x >= 1000000u) + (x >= 10000000u);
+constexpr uint64_t kAsciiZeros = 0x3030303030303030ull;
+
+// Eight bytes starting at bit s (a multiple of 8, possibly 0) of the 128-bit
+// little-endian value hi_w:lo_w.
+__device__ __forceinline__ uint64_t window64(uint64_t lo_w, uint64_t hi_w, uint32_t s) {
+  return (lo_w >> s) | ((hi_w << 1) << (63u - s));
 }
 
-__device__ __forceinline__ Text24 int64_text(int64_t v) {
+// Leading '0' characters of an 8-digit ASCII group (digit 0 in byte 0); bit
+// 63 caps the count at 7 for an all-zero group.
+__device__ __forceinline__ uint32_t leading_zero_digits(uint64_t text8) {
+  return static_cast<uint32_t>(__builtin_ctzll((text8 ^ kAsciiZeros) | (1ull << 63))) >> 3;
+}
+
+// farmhashna::Hash64 of the decimal text of v (TensorFlow's AsString of an
+// int64: optional '-', no leading zeros; at most 20 bytes, so only the
+// 0-16 and 17-32 byte branches exist).
+// The 19 zero-padded digits of |v| sit right-aligned in a 24-byte string P
+// held in q0, q1, q2: P[2,5) digits 0-2, P[5,13) digits 3-10, P[13,21)
+// digits 11-18.  A text of len bytes is P[21-len, 21), the sign replacing
+// the byte before the first digit.  Reads at a fixed distance from the end
+// of the text are then fixed registers (the last 8 bytes are digits 11-18,
+// the 8 before them digits 3-10); only reads from the start shift by
+// 21 - len.
+__device__ __forceinline__ uint64_t fp64_decimal(int64_t v) {
   const bool neg = v < 0;
-  const uint64_t u = neg ? (0ull - static_cast<uint64_t>(v)) : static_cast<uint64_t>(v);
+  const uint64_t u = neg ? 0ull - static_cast<uint64_t>(v) : static_cast<uint64_t>(v);
   // u = hi * 10^16 + mid * 10^8 + lo; 10^8 = 390625 * 2^8, so the second
   // division runs on q1 >> 8 < 2^29 in 32 bits
   const uint64_t q1 = u / 100000000ull;
   const uint32_t lo = static_cast<uint32_t>(u) - static_cast<uint32_t>(q1) * 100000000u;
   const uint32_t hi = static_cast<uint32_t>(q1 >> 8) / 390625u;  // <= 922
   const uint32_t mid = static_cast<uint32_t>(q1) - (__umul24(hi, 390625u) << 8);
-  uint32_t nd;
-  if (hi)
-    nd = 16u + 1u + (hi >= 10u) + (hi >= 100u);
-  else if (mid)
-    nd = 8u + count_digits8(mid);
-  else
-    nd = count_digits8(lo);
-  // 19 zero-padded characters: hi(3) mid(8) lo(8).
   const uint64_t d3 = ascii3(hi);
   const uint64_t m8 = ascii8(mid);
   const uint64_t l8 = ascii8(lo);
-  const uint64_t p0 = d3 | (m8 << 24);
-  const uint64_t p1 = (m8 >> 40) | (l8 << 24);
-  const uint64_t p2 = l8 >> 40;
-  // Drop the 19 - nd leading zeros: 192-bit right shift by 8*(19-nd) bits.
-  const uint32_t bits = 8u * (19u - nd);
-  const uint32_t q = bits >> 6, r = bits & 63u;
-  const uint64_t x0 = q == 0 ? p0 : (q == 1 ? p1 : p2);
-  const uint64_t x1 = q == 0 ? p1 : (q == 1 ? p2 : 0ull);
-  const uint64_t x2 = q == 0 ? p2 : 0ull;
-  Text24 t;
-  t.w0 = r ? (x0 >> r) | (x1 << (64 - r)) : x0;
-  t.w1 = r ? (x1 >> r) | (x2 << (64 - r)) : x1;
-  t.w2 = x2 >> r;
-  t.len = nd;
-  if (neg) {
-    t.w2 = (t.w2 << 8) | (t.w1 >> 56);
-    t.w1 = (t.w1 << 8) | (t.w0 >> 56);
-    t.w0 = (t.w0 << 8) | 0x2Dull;  // '-'
-    t.len = nd + 1;
+  const uint32_t nd = hi    ? 17u + (hi >= 10u) + (hi >= 100u)
+                      : mid ? 16u - leading_zero_digits(m8)
+                            : 8u - leading_zero_digits(l8);
+  const uint32_t len = nd + (neg ? 1u : 0u);  // 1..20
+  const uint64_t p0 = (d3 << 16) | (m8 << 40);
+  const uint64_t p1 = (m8 >> 24) | (l8 << 40);
+  const uint64_t p2 = l8 >> 24;
+  const uint32_t start = 21u - len;
+  const uint64_t mul = kC2 + 2ull * len;
+  if (len > 16) {  // HashLen17to32; start = 1..4
+    const uint32_t s = 8u * start;
+    uint64_t a = (p0 >> s) | (p1 << (64u - s));
+    const uint64_t b = (p1 >> s) | (p2 << (64u - s));
+    if (neg) a = (a & ~0xffull) | 0x2Dull;
+    a *= kC1;
+    const uint64_t c = l8 * mul;
+    const uint64_t d = m8 * kC2;
+    return mix16(rotr(a + b, 43) + rotr(c, 30) + d, a + rotr(b + kC2, 18) + c, mul);
   }
-  return t;
-}
-
-// Eight bytes of the text starting at byte offset o (0 <= o <= 16); bytes
-// past the text read as zero.
-__device__ __forceinline__ uint64_t text_fetch64(const Text24& t, uint32_t o) {
-  const uint32_t q = o >> 3, r = (o & 7u) * 8u;
-  const uint64_t a = q == 0 ? t.w0 : (q == 1 ? t.w1 : t.w2);
-  const uint64_t b = q == 0 ? t.w1 : (q == 1 ? t.w2 : 0ull);
-  return r ? (a >> r) | (b << (64 - r)) : a;
-}
-
-__device__ __forceinline__ uint64_t fp64_text(const Text24& t) {
-  const uint64_t len = t.len;  // 1..20
-  if (len <= 16) {
-    if (len >= 8) {
-      const uint64_t mul = kC2 + len * 2;
-      const uint64_t a = text_fetch64(t, 0) + kC2;
-      const uint64_t b = text_fetch64(t, (uint32_t)len - 8);
-      return mix16(rotr(b, 37) * mul + a, (rotr(a, 25) + b) * mul, mul);
-    }
-    if (len >= 4) {
-      const uint64_t mul = kC2 + len * 2;
-      const uint64_t a = t.w0 & 0xffffffffull;
-      const uint64_t b = text_fetch64(t, (uint32_t)len - 4) & 0xffffffffull;
-      return mix16(len + (a << 3), b, mul);
-    }
-    const uint32_t c0 = static_cast<uint32_t>(t.w0 & 0xff);
-    const uint32_t cm = static_cast<uint32_t>((t.w0 >> (8 * (len >> 1))) & 0xff);
-    const uint32_t cl = static_cast<uint32_t>((t.w0 >> (8 * (len - 1))) & 0xff);
-    const uint32_t y = c0 + (cm << 8);
-    const uint32_t z = static_cast<uint32_t>(len) + (cl << 2);
-    return smix(y * kC2 ^ z * kC0) * kC2;
+  // first eight bytes of the text (start = 5..20)
+  const uint32_t w = start >> 3;
+  const uint64_t lo_w = w == 0 ? p0 : (w == 1 ? p1 : p2);
+  const uint64_t hi_w = w == 0 ? p1 : (w == 1 ? p2 : 0ull);
+  uint64_t a = window64(lo_w, hi_w, 8u * (start & 7u));
+  if (neg) a = (a & ~0xffull) | 0x2Dull;
+  if (len >= 8) {  // HashLen0to16, 8..16 bytes; the last 8 are digits 11-18
+    const uint64_t b = len == 8 ? a : l8;
+    const uint64_t a2 = a + kC2;
+    return mix16(rotr(b, 37) * mul + a2, (rotr(a2, 25) + b) * mul, mul);
   }
-  const uint64_t mul = kC2 + len * 2;
-  const uint64_t a = t.w0 * kC1;
-  const uint64_t b = t.w1;
-  const uint64_t c = text_fetch64(t, (uint32_t)len - 8) * mul;
-  const uint64_t d = text_fetch64(t, (uint32_t)len - 16) * kC2;
-  return mix16(rotr(a + b, 43) + rotr(c, 30) + d, a + rotr(b + kC2, 18) + c, mul);
+  if (len >= 4) {  // 4..7 bytes; the last 4 are digits 15-18
+    const uint64_t x = a & 0xffffffffull;
+    const uint64_t y = len == 4 ? x : (l8 >> 32);
+    return mix16(len + (x << 3), y, mul);
+  }
+  const uint32_t c0 = static_cast<uint32_t>(a & 0xff);  // 1..3 bytes
+  const uint32_t cm = static_cast<uint32_t>((a >> (8u * (len >> 1))) & 0xff);
+  const uint32_t cl = static_cast<uint32_t>((a >> (8u * (len - 1u))) & 0xff);
+  const uint32_t y = c0 + (cm << 8);
+  const uint32_t z = len + (cl << 2);
+  return smix(y * kC2 ^ z * kC0) * kC2;
 }
 
 // ---------------------------------------------------------------------------
@@ -333,7 +320,7 @@ __global__ __launch_bounds__(kThreads) void bucket_int64_kernel(const int64_t* _
                                                                 int64_t* __restrict__ out) {
   const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
   if (i >= n) return;
-  out[i] = static_cast<int64_t>(mod_invariant(fp64_text(int64_text(ids[i])), dv));
+  out[i] = static_cast<int64_t>(mod_invariant(fp64_decimal(ids[i]), dv));
 }
 
 // out[i,:] = table[bucket[i],:] (exact copy) or zeros when bucket[i] is
@@ -407,7 +394,7 @@ __global__ __launch_bounds__(kThreads) void hashed_bags_wave_kernel(
       const int64_t p = k0 + lane;
       const bool pv = p < wend;
       const int64_t id = ids[pv ? p : wend - 1];
-      const uint64_t bucket = mod_invariant(fp64_text(int64_text(id)), dv);
+      const uint64_t bucket = mod_invariant(fp64_decimal(id), dv);
       if (buckets_out && pv && c0 == 0) buckets_out[p] = static_cast<int64_t>(bucket);
       const uint32_t my_off = pv ? static_cast<uint32_t>(bucket) * row_bytes : kMaskedOff;
       // this bag's positions inside the chunk: [lo, lo + cnt) relative to k0
@@ -450,6 +437,324 @@ void launch_hashed_wave_g(const FieldSet& fs, int64_t f0, int64_t nf, int64_t ba
   else
     hipLaunchKernelGGL((hashed_bags_wave_kernel<G, false>), grid, dim3(kThreads), 0, s, fs, f0,
                        nf, batch, dim, wpf, ids, offsets, out, ldo, buckets_out);
+}
+
+// ---------------------------------------------------------------------------
+// Pipelined hashed bags for rows of at most 16 floats.
+// ---------------------------------------------------------------------------
+// A run is 16 consecutive bags of one field; bag j of a run belongs to the
+// lane group j (4 lanes, 4 floats each).  A wave walks a contiguous range of
+// runs (field-major) with a three-deep software pipeline, so that the row
+// gathers of one run are in flight while the next run is hashed:
+//   offsets of run i+3 and ids of run i+2 are loaded,
+//   run i+1 is hashed and its row loads are issued,
+//   run i's rows (issued one step earlier) are summed and stored.
+// A run whose positions span more than two 64-position chunks takes the
+// synchronous path of hashed_bags_wave_kernel instead.
+constexpr int kPipeBags = 16;  // bags per run
+constexpr int kPipeU = 8;      // positions per bag whose rows are issued in one batch
+
+struct RunCursor {  // run = (field fl of the launch, run j within the field)
+  int64_t fl, j;
+};
+
+__device__ __forceinline__ void advance(RunCursor& c, int64_t runs_per_field) {
+  if (++c.j == runs_per_field) {
+    c.j = 0;
+    ++c.fl;
+  }
+}
+
+__device__ __forceinline__ int64_t readlane64(int64_t v, int l) {
+  const uint32_t lo = __builtin_amdgcn_readlane(static_cast<uint32_t>(v), l);
+  const uint32_t hi = __builtin_amdgcn_readlane(static_cast<uint32_t>(static_cast<uint64_t>(v) >> 32), l);
+  return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
+__device__ __forceinline__ int64_t shfl64(int64_t v, int src_lane) {
+  const int lo = __builtin_amdgcn_ds_bpermute(src_lane << 2, static_cast<int>(v));
+  const int hi = __builtin_amdgcn_ds_bpermute(src_lane << 2, static_cast<int>(v >> 32));
+  return static_cast<int64_t>((static_cast<uint64_t>(static_cast<uint32_t>(hi)) << 32) |
+                              static_cast<uint32_t>(lo));
+}
+
+// Row chunk of position q (relative to the run's first position) from the
+// lane that hashed it.
+__device__ __forceinline__ uint32_t row_offset_of(int q, uint32_t off0, uint32_t off1,
+                                                  bool two_chunks) {
+  const uint32_t a = static_cast<uint32_t>(
+      __builtin_amdgcn_ds_bpermute((q & 63) << 2, static_cast<int>(off0)));
+  if (!two_chunks) return a;
+  const uint32_t b = static_cast<uint32_t>(
+      __builtin_amdgcn_ds_bpermute((q & 63) << 2, static_cast<int>(off1)));
+  return q < 64 ? a : b;
+}
+
+template <bool MEAN>
+__global__ __launch_bounds__(kThreads) void hashed_bags_pipe_kernel(
+    FieldSet fs, int64_t field0, int64_t batch, int64_t dim, int64_t runs_per_field,
+    int64_t total_runs, int64_t runs_per_wave, const int64_t* __restrict__ ids,
+    const int64_t* __restrict__ offsets, float* __restrict__ out, int64_t ldo,
+    int64_t* __restrict__ buckets_out) {
+  typedef float f32x4 __attribute__((ext_vector_type(4)));
+  // Prefetched offsets (two runs) and ids (one run) wait here: a register
+  // still waiting on a load must not be carried across the loop's back edge
+  // (the copy would wait for every older load, row gathers included).
+  // (volatile: the compiler must not forward these stores to the next
+  // iteration's loads through registers)
+  __shared__ int64_t sh_starts_mem[kThreads / 64][2][64];
+  __shared__ int64_t sh_ids_mem[kThreads / 64][2][64];
+  typedef volatile __attribute__((address_space(3))) int64_t lds_i64;
+  lds_i64(*sh_starts)[2][64] = (lds_i64(*)[2][64])sh_starts_mem;
+  lds_i64(*sh_ids)[2][64] = (lds_i64(*)[2][64])sh_ids_mem;
+  const int lane = threadIdx.x & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  // XCD-aware block order: consecutive hardware blocks go to different XCDs
+  // (round robin over 8), so give each XCD a contiguous share of the runs
+  // and the L2 of that XCD a few fields' tables.
+  const uint32_t nblk = gridDim.x, xcd = blockIdx.x & 7u, k = blockIdx.x >> 3;
+  const uint32_t per = nblk >> 3, rem = nblk & 7u;
+  const uint32_t blk = xcd * per + (xcd < rem ? xcd : rem) + k;
+  const int64_t w = (int64_t)blk * (kThreads / 64) + wid;
+  const int64_t r0 = w * runs_per_wave;
+  if (r0 >= total_runs) return;
+  const int64_t n = total_runs - r0 < runs_per_wave ? total_runs - r0 : runs_per_wave;
+  const int grp = lane >> 2;
+  const int c = (lane & 3) * 4;
+  const bool active = c < dim;
+  const uint32_t c_off = active ? static_cast<uint32_t>(c * sizeof(float)) : kMaskedOff;
+  const uint32_t row_bytes = static_cast<uint32_t>(dim * sizeof(float));
+
+  auto nbag_of = [&](const RunCursor& rc) -> int {
+    const int64_t left = batch - rc.j * kPipeBags;
+    return static_cast<int>(left < kPipeBags ? left : kPipeBags);
+  };
+  // lane l: start of bag min(l, nbag) of the run (the run's end for l >= nbag)
+  auto load_starts = [&](const RunCursor& rc) -> int64_t {
+    const int nb = nbag_of(rc);
+    const int64_t base = (field0 + rc.fl) * batch + rc.j * kPipeBags;
+    return offsets[base + (lane < nb ? lane : nb)];
+  };
+  struct Ids {
+    int64_t a, b;  // positions wbeg + lane and wbeg + 64 + lane
+  };
+  // Always two loads; lanes without a position read offsets[0] instead.
+  auto load_ids = [&](const RunCursor& rc, int64_t starts) -> Ids {
+    const int nb = nbag_of(rc);
+    const int64_t wbeg = readlane64(starts, 0), wend = readlane64(starts, nb);
+    const bool ok = wend > wbeg && wend - wbeg <= 128;
+    const int64_t p = wbeg + lane;
+    const int64_t* pa = ok ? ids + (p < wend ? p : wend - 1) : offsets;
+    const int64_t* pb = ok && wend - wbeg > 64 ? ids + (p + 64 < wend ? p + 64 : wend - 1) : offsets;
+    return Ids{*pa, *pb};
+  };
+  auto field_of = [&](const RunCursor& rc) {
+    return __builtin_amdgcn_readfirstlane(static_cast<int>(rc.fl));
+  };
+  auto rsrc_of = [&](const RunCursor& rc) {
+    const int fl = field_of(rc);
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(fs.table[fl]), 0,
+                                             static_cast<int>(fs.rows[fl] * row_bytes),
+                                             kRawBufferFlags);
+  };
+  // The run's 16 output rows through a buffer store: lanes without a bag
+  // (or past dim) store past the range and are dropped, so the store is one
+  // unconditional instruction.
+  auto store = [&](const RunCursor& rc, int cnt, f32x4 acc) {
+    if (MEAN && cnt > 0) acc *= 1.0f / static_cast<float>(cnt);
+    const int nb = nbag_of(rc);
+    float* base = out + (rc.j * kPipeBags) * ldo + (field0 + rc.fl) * dim;
+    const auto orsrc = __builtin_amdgcn_make_buffer_rsrc(
+        base, 0, static_cast<int>(nb * ldo * static_cast<int64_t>(sizeof(float))), kRawBufferFlags);
+    const uint32_t o = active && grp < nb ? static_cast<uint32_t>((grp * ldo + c) * sizeof(float))
+                                          : kMaskedOff;
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc), orsrc,
+                                           static_cast<int>(o), 0, 0);
+  };
+
+  // A hashed run: row byte offsets of its positions, held by the lanes that
+  // hashed them (chunk 0: positions wbeg + lane, chunk 1: wbeg + 64 + lane).
+  struct Hashed {
+    RunCursor rc;
+    int64_t starts;
+    bool slow, two;
+    int rel, cnt;  // this lane group's bag: first position - wbeg, length
+    uint32_t off0, off1;
+  };
+  auto hash_run = [&](const RunCursor& rc, int64_t starts, const Ids& iv) -> Hashed {
+    const int nb = nbag_of(rc);
+    const int64_t wbeg = readlane64(starts, 0), wend = readlane64(starts, nb);
+    Hashed h;
+    h.rc = rc;
+    h.starts = starts;
+    h.slow = wend - wbeg > 128;
+    h.two = wend - wbeg > 64;
+    h.off0 = kMaskedOff;
+    h.off1 = kMaskedOff;
+    const int64_t beg = shfl64(starts, grp), end = shfl64(starts, grp + 1);
+    h.rel = static_cast<int>(beg - wbeg);
+    h.cnt = grp < nb ? static_cast<int>(end - beg) : 0;
+    if (h.slow || wend == wbeg) return h;
+    const U64Divisor dv = fs.div[field_of(rc)];
+    const int64_t p = wbeg + lane;
+    const uint64_t b0 = mod_invariant(fp64_decimal(iv.a), dv);
+    if (p < wend) {
+      h.off0 = static_cast<uint32_t>(b0) * row_bytes;
+      if (buckets_out) buckets_out[p] = static_cast<int64_t>(b0);
+    }
+    if (h.two) {
+      const uint64_t b1 = mod_invariant(fp64_decimal(iv.b), dv);
+      if (p + 64 < wend) {
+        h.off1 = static_cast<uint32_t>(b1) * row_bytes;
+        if (buckets_out) buckets_out[p + 64] = static_cast<int64_t>(b1);
+      }
+    }
+    return h;
+  };
+  // Row loads of positions u0 .. u0+kPipeU-1 of this lane group's bag
+  // (masked for a run on the synchronous path).
+  auto issue = [&](const Hashed& h, int u0, f32x4* v) {
+    const auto rsrc = rsrc_of(h.rc);
+    const int cnt = h.slow ? 0 : h.cnt;
+    if (h.two) {
+#pragma unroll
+      for (int i = 0; i < kPipeU; ++i) {
+        const int u = u0 + i;
+        const uint32_t o = row_offset_of(h.rel + u, h.off0, h.off1, true);
+        v[i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                             rsrc, static_cast<int>((u < cnt ? o : kMaskedOff) + c_off), 0, 0));
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < kPipeU; ++i) {
+        const int u = u0 + i;
+        const uint32_t o = row_offset_of(h.rel + u, h.off0, h.off1, false);
+        v[i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                             rsrc, static_cast<int>((u < cnt ? o : kMaskedOff) + c_off), 0, 0));
+      }
+    }
+  };
+  // Synchronous path for a run of more than 128 positions: 64 at a time,
+  // sums carried across chunks in position order.
+  auto run_slow = [&](const Hashed& h) {
+    const RunCursor& rc = h.rc;
+    const int nb = nbag_of(rc);
+    const int64_t wbeg = readlane64(h.starts, 0), wend = readlane64(h.starts, nb);
+    const int64_t beg = wbeg + h.rel, end = beg + h.cnt;
+    const U64Divisor dv = fs.div[field_of(rc)];
+    const auto rsrc = rsrc_of(rc);
+    f32x4 acc = f32x4(0.0f);
+    for (int64_t k0 = wbeg; k0 < wend; k0 += 64) {
+      const int64_t p = k0 + lane;
+      const bool pv = p < wend;
+      const uint64_t bucket = mod_invariant(fp64_decimal(ids[pv ? p : wend - 1]), dv);
+      if (buckets_out && pv) buckets_out[p] = static_cast<int64_t>(bucket);
+      const uint32_t my_off = pv ? static_cast<uint32_t>(bucket) * row_bytes : kMaskedOff;
+      const int64_t lo64 = beg > k0 ? beg : k0;
+      const int64_t hi64 = end < k0 + 64 ? end : k0 + 64;
+      const int cnt = hi64 > lo64 ? static_cast<int>(hi64 - lo64) : 0;
+      const int lo = static_cast<int>(lo64 - k0);
+      for (int u0 = 0; __ballot(cnt > u0) != 0; u0 += kPipeU) {
+        f32x4 v[kPipeU];
+#pragma unroll
+        for (int i = 0; i < kPipeU; ++i) {
+          const int u = u0 + i;
+          const uint32_t o = static_cast<uint32_t>(
+              __builtin_amdgcn_ds_bpermute(((lo + u) & 63) << 2, static_cast<int>(my_off)));
+          v[i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                               rsrc, static_cast<int>((u < cnt ? o : kMaskedOff) + c_off), 0, 0));
+        }
+#pragma unroll
+        for (int i = 0; i < kPipeU; ++i) acc += v[i];
+      }
+    }
+    store(rc, h.cnt, acc);
+  };
+  // Sum the issued rows (plus further batches for bags longer than kPipeU)
+  // and store the run; a run of more than 128 positions is done here.
+  auto finish = [&](const Hashed& h, const f32x4* v) {
+    if (h.slow) {
+      run_slow(h);
+      return;
+    }
+    f32x4 acc = f32x4(0.0f);
+#pragma unroll
+    for (int i = 0; i < kPipeU; ++i) acc += v[i];
+    for (int u0 = kPipeU; __ballot(h.cnt > u0) != 0; u0 += kPipeU) {
+      f32x4 w2[kPipeU];
+      issue(h, u0, w2);
+#pragma unroll
+      for (int i = 0; i < kPipeU; ++i) acc += w2[i];
+    }
+    store(h.rc, h.cnt, acc);
+  };
+
+  // Cursors over the wave's runs; the prefetch cursors stop at the last run
+  // (its loads are repeated, never used), so every step issues the same
+  // loads and each consumer waits only for its own.
+  const int64_t last = n - 1;
+  RunCursor cs{r0 / runs_per_field, r0 % runs_per_field};  // next offsets load
+  RunCursor ci = cs, ch = cs;                              // next ids load, next hash
+  int64_t ks = 0, ki = 0;
+  auto next = [&](RunCursor& cur, int64_t& kk) {
+    if (kk < last) {
+      advance(cur, runs_per_field);
+      ++kk;
+    }
+  };
+  const int64_t s0 = load_starts(cs);
+  next(cs, ks);
+  const int64_t s1 = load_starts(cs);
+  next(cs, ks);
+  const int64_t s2 = load_starts(cs);
+  next(cs, ks);
+  const Ids i0 = load_ids(ci, s0);
+  next(ci, ki);
+  const Ids i1 = load_ids(ci, s1);
+  next(ci, ki);
+  Hashed hc = hash_run(ch, s0, i0);
+  advance(ch, runs_per_field);
+  sh_starts[wid][1][lane] = s1;
+  sh_starts[wid][0][lane] = s2;
+  sh_ids[wid][0][lane] = i1.a;
+  sh_ids[wid][1][lane] = i1.b;
+  // Iteration i issues run i's row loads, hashes run i+1 while they are in
+  // flight, then sums and stores run i.  Every load is consumed in the
+  // iteration that issued it; only hashed offsets (registers, no pending
+  // loads) and LDS carry over.  LDS holds the offsets of runs i+1 and i+2
+  // (slots (i+1)&1 and i&1) and the ids of run i+1.
+  for (int64_t i = 0; i < n; ++i) {
+    f32x4 v[kPipeU];
+    issue(hc, 0, v);
+    const int64_t spre = sh_starts[wid][i & 1][lane];  // run i+2
+    const Ids ipf = load_ids(ci, spre);                // ids of run i+2
+    next(ci, ki);
+    const int64_t sld = load_starts(cs);               // offsets of run i+3
+    next(cs, ks);
+    Hashed hn;
+    if (i + 1 < n) {
+      const Ids inx{sh_ids[wid][0][lane], sh_ids[wid][1][lane]};
+      hn = hash_run(ch, sh_starts[wid][(i + 1) & 1][lane], inx);
+      advance(ch, runs_per_field);
+    }
+    finish(hc, v);
+    sh_ids[wid][0][lane] = ipf.a;
+    sh_ids[wid][1][lane] = ipf.b;
+    sh_starts[wid][(i + 1) & 1][lane] = sld;
+    hc = hn;
+  }
+}
+
+template <bool MEAN>
+void launch_hashed_pipe(const FieldSet& fs, int64_t f0, int64_t nf, int64_t batch, int64_t dim,
+                        const int64_t* ids, const int64_t* offsets, float* out, int64_t ldo,
+                        int64_t* buckets_out, int64_t runs_per_wave, hipStream_t s) {
+  const int64_t rpf = (batch + kPipeBags - 1) / kPipeBags;
+  const int64_t total = nf * rpf;
+  const int64_t waves = (total + runs_per_wave - 1) / runs_per_wave;
+  dim3 grid((unsigned)ceil_div(waves, kThreads / 64));
+  hipLaunchKernelGGL((hashed_bags_pipe_kernel<MEAN>), grid, dim3(kThreads), 0, s, fs, f0, batch,
+                     dim, rpf, total, runs_per_wave, ids, offsets, out, ldo, buckets_out);
 }
 
 // Fused multi-field hash -> bucket -> gather -> pool with the row offsets
@@ -526,7 +831,7 @@ __global__ __launch_bounds__(kThreads) void hashed_bags_lds_kernel(
     for (int ch = 0; ch < kChunks; ++ch) {
       if (64 * ch < wlen) {
         const int q = 64 * ch + lane;
-        const uint64_t bucket = mod_invariant(fp64_text(int64_text(idv[ch])), dv);
+        const uint64_t bucket = mod_invariant(fp64_decimal(idv[ch]), dv);
         win[q] = q < wlen ? static_cast<uint32_t>(bucket) * row_bytes : kMaskedOff;
         if (buckets_out && q < wlen) buckets_out[w0 + q] = static_cast<int64_t>(bucket);
       }
@@ -625,7 +930,7 @@ __global__ __launch_bounds__(kThreads) void hashed_bags_kernel(
     for (int64_t j0 = beg; j0 < end; j0 += G) {
       int64_t mine = 0;
       if (j0 + g < end) {
-        mine = static_cast<int64_t>(mod_invariant(fp64_text(int64_text(ids[j0 + g])), dv));
+        mine = static_cast<int64_t>(mod_invariant(fp64_decimal(ids[j0 + g]), dv));
         if (buckets_out && base == 0) buckets_out[j0 + g] = mine;
       }
       const int cnt = (int)((end - j0) < G ? (end - j0) : G);
@@ -810,7 +1115,16 @@ int annc_hip_hashed_embedding_bags(void* stream, int64_t num_fields, int64_t bat
       small_tables = small_tables && table_rows[f0 + i] * dim * 4 < (int64_t(1) << 31);
     }
     if (small_tables) {
-      if (lanes <= 4)
+      // the pipelined kernel stores a run's 16 output rows through one
+      // buffer resource (range < 2 GiB)
+      if (lanes <= 4 && int64_t(kPipeBags) * ldo * 4 < (int64_t(1) << 31)) {
+        // two runs per wave measured best on configs[3] (1 to 13 tried)
+        const int64_t rpw = 2;
+        if (combiner == ANNC_COMBINER_MEAN)
+          launch_hashed_pipe<true>(fs, f0, nf, batch, dim, ids, offsets, out, ldo, buckets_out, rpw, s);
+        else
+          launch_hashed_pipe<false>(fs, f0, nf, batch, dim, ids, offsets, out, ldo, buckets_out, rpw, s);
+      } else if (lanes <= 4)
         launch_hashed_wave_g<4>(fs, f0, nf, batch, dim, ids, offsets, combiner, out, ldo, buckets_out, s);
       else if (lanes <= 8)  // two bags per lane group: more positions hashed per wave
         launch_hashed_lds_g<8, 2>(fs, f0, nf, batch, dim, ids, offsets, combiner, out, ldo, buckets_out, s);

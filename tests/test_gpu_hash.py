@@ -146,3 +146,36 @@ def test_tf_sparse_embedding():
     ref = ora.sparse_embedding(strs, 7)
     for a, b in zip(got, ref):
         np.testing.assert_array_equal(a, b)
+
+
+@pytest.mark.parametrize("dim,combiner", [(4, 0), (8, 1), (12, 0), (16, 1)])
+def test_hashed_bags_ragged_mixed_ids(dim, combiner):
+    """Rows of at most 16 floats (the pipelined run kernel): empty and
+    ragged bags, a padded output stride, ids of every decimal length and
+    sign in one wave, fields whose runs straddle waves."""
+    note(f"hashed bags ragged mixed dim={dim} combiner={combiner}")
+    g = workloads.rng(100 + dim)
+    nf, batch, rows = 5, 203, 3001
+    lens = g.integers(0, 7, size=nf * batch)
+    lens[::11] = 0
+    lens[5] = 70    # a run of 64-128 positions (two hashed chunks)
+    lens[40] = 140  # a run of more than 128 positions (synchronous path)
+    lens[300] = 9   # a bag longer than one batch of row loads
+    offsets = np.zeros(nf * batch + 1, dtype=np.int64)
+    np.cumsum(lens, out=offsets[1:])
+    nnz = int(offsets[-1])
+    pool = np.asarray(EDGE_IDS, dtype=np.int64)
+    ids = np.where(g.random(nnz) < 0.5, g.choice(pool, size=nnz),
+                   g.integers(-2**63, 2**63 - 1, size=nnz, dtype=np.int64))
+    tables = [g.standard_normal((rows, dim)).astype(np.float32) for _ in range(nf)]
+    nbk = [rows - 7 * f for f in range(nf)]
+    ldo = nf * dim + 4
+    ref = np.stack([ora.hashed_embedding_bags([tables[f]], nbk[f], ids,
+                                              offsets[f * batch:(f + 1) * batch + 1], batch,
+                                              combiner) for f in range(nf)], axis=1)
+    out_full = to_dev(np.full((batch, ldo), 7.0, dtype=np.float32))
+    dev.hashed_embedding_bags([to_dev(t) for t in tables], nbk, to_dev(ids), to_dev(offsets),
+                              batch, combiner, out=out_full[:, :nf * dim])
+    got = to_host(out_full)
+    np.testing.assert_array_equal(got[:, :nf * dim].reshape(batch, nf, dim), ref)
+    np.testing.assert_array_equal(got[:, nf * dim:], 7.0)  # padding untouched
