@@ -111,6 +111,7 @@ _PROTOTYPES = {
                                                                _c_void_p]),
     "annc_kp_fused_sparse_embedding": (_i32, [_c_void_p, _c_void_p, _i64, _i64, _c_void_p,
                                               _c_void_p, _c_void_p, _c_void_p, _c_void_p]),
+    "annc_hlo_rewrite_instruction": (_i32, [_c_void_p, _i64, _i32, _c_void_p]),
 }
 
 _lock = threading.Lock()

@@ -79,6 +79,25 @@ class MLPTower:
         return [(l.weight.n if isinstance(l.weight, dev.PackedWeight) else l.weight.shape[1])
                 for l in self.layers]
 
+    def lowering(self, batch: int) -> list:
+        """Custom-call target ANNC's rewriters pick for each layer's dot under
+        the current ANNC_FLAGS (None: the dot stays an XLA dot), for the HLO
+        XLA emits from the layer: dot -> add(broadcast(bias)) -> maximum for
+        ReLU, weights as parameters (annc_hlo_rewrite_instruction).  With
+        --layout-matmul the configs[1] tower lowers to __layout_matmul,
+        __layout_matmul, None (256 -> 1 fails the >= 12 rule)."""
+        from . import hlo
+        out, k = [], None
+        for l in self.layers:
+            w = l.weight
+            k, n = (w.k, w.n) if isinstance(w, dev.PackedWeight) else tuple(w.shape)
+            act = "relu" if l.activation == _lib.EPI_RELU else (
+                "sigmoid" if l.activation == _lib.EPI_SIGMOID else None)
+            f, dot, _ = hlo.dense_layer(batch, k, n, activation=act)
+            r = hlo.rewrite(f, dot)
+            out.append(None if r is None else r.target)
+        return out
+
     def flops(self, batch: int) -> int:
         total = 0
         for l in self.layers:

@@ -65,6 +65,75 @@ void annc_flags_reset(const char* flags);
 int64_t annc_flags_dump(char* buf, int64_t len);
 
 /* ------------------------------------------------------------------------ */
+/* Which HLO fragments become ANNC fusions / custom calls                    */
+/* (replaces KDnnRewriter selection: annc/service/cpu/kdnn_rewriter.h:25-59,  */
+/*  kdnn_rewriter.cc:8-69, gemm_rewriter.cc:13-134, graph_opt.cc:8-129).      */
+/* Host-only; reads the process-wide ANNC_FLAGS set.                          */
+/* ------------------------------------------------------------------------ */
+enum {
+  ANNC_HLO_OTHER = 0,
+  ANNC_HLO_PARAMETER = 1,
+  ANNC_HLO_CONSTANT = 2,
+  ANNC_HLO_DOT = 3,
+  ANNC_HLO_ADD = 4,
+  ANNC_HLO_MAXIMUM = 5,
+  ANNC_HLO_MULTIPLY = 6,
+  ANNC_HLO_SELECT = 7,
+  ANNC_HLO_BROADCAST = 8,
+  ANNC_HLO_GATHER = 9,
+  ANNC_HLO_CONVERT = 10,
+  ANNC_HLO_AND = 11,
+  ANNC_HLO_COMPARE = 12,
+  ANNC_HLO_DIVIDE = 13,
+  ANNC_HLO_RESHAPE = 14,
+  ANNC_HLO_REDUCE = 15,
+  ANNC_HLO_SLICE = 16,
+  ANNC_HLO_REDUCE_WINDOW = 17,
+};
+enum { ANNC_DT_OTHER = 0, ANNC_DT_PRED = 1, ANNC_DT_S32 = 2, ANNC_DT_S64 = 3, ANNC_DT_F32 = 4 };
+#define ANNC_HLO_MAX_RANK 8
+#define ANNC_HLO_MAX_OPERANDS 8
+#define ANNC_HLO_MAX_FUSED 16
+
+/* One instruction of the fragment.  Users of a node are the nodes that list
+ * it as an operand, in node-index order (XLA's users() order when nodes are
+ * numbered in program order). */
+typedef struct annc_hlo_node {
+  int32_t opcode;                             /* ANNC_HLO_* */
+  int32_t dtype;                              /* ANNC_DT_* of the result */
+  int32_t rank;
+  int32_t num_operands;
+  int64_t dims[ANNC_HLO_MAX_RANK];
+  int32_t minor_to_major[ANNC_HLO_MAX_RANK];  /* row-major: rank-1, ..., 0 */
+  int32_t operands[ANNC_HLO_MAX_OPERANDS];    /* node indices */
+  int32_t has_control_deps;
+} annc_hlo_node;
+
+typedef struct annc_hlo_rewrite {
+  int32_t matched;     /* 0: no rewriter fired */
+  char target[32];     /* custom-call target or fusion name: "__matmul_add_relu",
+                          "__layout_matmul", "__pooling", "sparse_embedding2", ... */
+  int32_t custom_call; /* 1: a custom call replaces the fusion; 0: fusion only */
+  int32_t benefit;
+  int32_t num_fused;
+  int32_t fused[ANNC_HLO_MAX_FUSED];            /* fusion root first */
+  int32_t num_operands;                         /* call operands before the shape infos */
+  int32_t operands[2 * ANNC_HLO_MAX_OPERANDS];  /* node indices; -1 / -2 = the slice
+                                                   starts / limits constants (__pooling) */
+  int32_t num_shape_infos;                      /* then one s64[2*rank] get_param_info
+                                                   constant per listed node */
+  int32_t shape_info_of[2 * ANNC_HLO_MAX_OPERANDS];
+} annc_hlo_rewrite;
+
+/* Runs the rewriters that ANNC's visitor would run on nodes[instr]
+ * (kDot: graph-opt + GEMM; kMultiply, kSelect: graph-opt), by descending
+ * benefit (ties in registration order), and fills `out` for the first that
+ * matches.  Returns ANNC_OK (out->matched tells whether one fired) or
+ * ANNC_INVALID_ARGUMENT for a malformed fragment. */
+int annc_hlo_rewrite_instruction(const annc_hlo_node* nodes, int64_t num_nodes, int32_t instr,
+                                 annc_hlo_rewrite* out);
+
+/* ------------------------------------------------------------------------ */
 /* XLA-CPU custom-call targets (annc/service/cpu/kdnn_rewriter.h:140-155).    */
 /* Same names, same operand order, same shape-info encoding                  */
 /* (annc/service/hlo_util.h:14-21: s64[2*rank] = dims..., minor_to_major...). */
