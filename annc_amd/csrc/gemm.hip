@@ -522,6 +522,15 @@ __device__ __forceinline__ void dma16(const void* src, uint32_t lds_base) {
                : "memory");
 }
 
+// 4 bytes per lane from `src` into LDS at `lds_base + 4*lane` (rows that
+// are not 16-byte aligned).
+__device__ __forceinline__ void dma4(const void* src, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off"
+               :
+               : "v"(src), "s"(lds_base)
+               : "memory");
+}
+
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
@@ -535,7 +544,7 @@ __device__ __forceinline__ int a_swizzle(int row) { return (row & 7) ^ ((row >> 
 
 }  // namespace pipe
 
-template <int WM, int WN, int BLK_M, int BLK_N, int S, int NACC, int KS, int KSUB>
+template <int WM, int WN, int BLK_M, int BLK_N, int S, int NACC, int KS, int KSUB, bool A16>
 __global__ __launch_bounds__(64 * WM * WN * KS) void gemm_packed_pipe_kernel(GemmParams p) {
   static_assert(NACC == 1 || NACC == 2, "one or two accumulator chains");
   static_assert(KS == 1 || KS == 2, "one or two k groups");
@@ -548,7 +557,12 @@ __global__ __launch_bounds__(64 * WM * WN * KS) void gemm_packed_pipe_kernel(Gem
   static_assert(NBLK % NW == 0, "stage blocks split evenly over the waves");
   static_assert(S >= 2 && S <= 4, "2..4 stages");
   static_assert(KS == 1 || NT * 2 * BLK_M * BLK_N * 2 <= S * KSUB * NBLK, "exchange fits in LDS");
-  constexpr int LPW = NBLK / NW;                    // DMA instructions per wave per k-block
+  constexpr int LPW = NBLK / NW;                    // 1 KiB blocks per wave per k-block
+  // A rows that are not 16-byte aligned load each A block with four 4-byte
+  // DMAs (two rows each); the first LPA blocks of every wave are A blocks.
+  static_assert(A16 || NA % NW == 0, "A blocks split evenly over the waves");
+  constexpr int LPA = NA / NW;
+  constexpr int DMAS = A16 ? LPW : LPW + 3 * LPA;  // DMA instructions per wave per k-block
   constexpr uint32_t kSubBytes = NBLK * 1024;
   constexpr uint32_t kStageBytes = KSUB * kSubBytes;
   __shared__ __attribute__((aligned(1024))) f32x4 lds[S][KSUB * NBLK * 64];
@@ -605,13 +619,39 @@ __global__ __launch_bounds__(64 * WM * WN * KS) void gemm_packed_pipe_kernel(Gem
       step[i] = 1024;
     }
   }
+  // 4-byte DMA sources of the A blocks: instruction j of block i fills LDS
+  // bytes [256j, 256j+256), i.e. rows 2j, 2j+1 of the block; lane l writes
+  // word l%4 of 16-byte chunk (l%32)/4 of row 2j + l/32, which holds k chunk
+  // ((l%32)/4) ^ swz(row) -- the same swizzled layout the 16-byte DMA writes.
+  const float* src4[A16 ? 1 : LPA][4];
+  if constexpr (!A16) {
+#pragma unroll
+    for (int i = 0; i < LPA; ++i) {
+      const int b = wave + NW * i;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int trow = b * 8 + 2 * j + (lane >> 5);
+        const int chunk = ((lane & 31) >> 2) ^ pipe::a_swizzle(trow);
+        const int row = min(m0 + trow, M - 1);
+        src4[i][j] = A + (int64_t)row * p.lda + chunk * 4 + (lane & 3);
+      }
+    }
+  }
   auto issue = [&](int slot, int kb) {
 #pragma unroll
     for (int sub = 0; sub < KSUB; ++sub)
 #pragma unroll
-      for (int i = 0; i < LPW; ++i)
-        pipe::dma16(src[i] + (int64_t)(kb * KSUB + sub) * step[i],
-                    dst[i] + slot * kStageBytes + sub * kSubBytes);
+      for (int i = 0; i < LPW; ++i) {
+        if (!A16 && i < LPA) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            pipe::dma4(src4[A16 ? 0 : i][j] + (int64_t)(kb * KSUB + sub) * 32,
+                       dst[i] + slot * kStageBytes + sub * kSubBytes + 256 * j);
+        } else {
+          pipe::dma16(src[i] + (int64_t)(kb * KSUB + sub) * step[i],
+                      dst[i] + slot * kStageBytes + sub * kSubBytes);
+        }
+      }
   };
 
   // fragment addressing (f32x4 units inside a stage)
@@ -684,9 +724,9 @@ __global__ __launch_bounds__(64 * WM * WN * KS) void gemm_packed_pipe_kernel(Gem
         // stages kb+1 .. kb+S-2 may stay in flight
         const int after = min(KB - 1 - kb, S - 2);
         if (after >= 2)
-          pipe::wait_vmcnt<2 * KSUB * LPW>();
+          pipe::wait_vmcnt<2 * KSUB * DMAS>();
         else if (after == 1)
-          pipe::wait_vmcnt<KSUB * LPW>();
+          pipe::wait_vmcnt<KSUB * DMAS>();
         else
           pipe::wait_vmcnt<0>();
         pipe::block_barrier();
@@ -826,6 +866,41 @@ __global__ void broadcast3_kernel(const float* __restrict__ src, int64_t s0, int
   dst[t] = src[z * s0 + i * s1 + j * s2];
 }
 
+// Packs row-major B[z] (leading dimension ldb, batch stride stride_b, N a
+// multiple of 32) into the layout_matmul format at dst + z*K*N.  Workgroup
+// (t, p) of 256 threads writes the 32x32 block of k-block t and n-panel p:
+// thread (q, lane) gathers k = 32t + 16*(lane/32) + 4q + e, e = 0..3, at
+// n = 32p + lane%32, so each of its four reads is a coalesced 128-byte row
+// segment across the wave and the block's stores fill one contiguous 1 KiB
+// span per wave.  The extra workgroup column t = K/32 copies the K tail
+// rows of panel p into the row-major tail region.
+__global__ __launch_bounds__(256) void pack_rhs_rowmajor_kernel(const float* __restrict__ src,
+                                                                int64_t ldb, int64_t stride_b,
+                                                                float* __restrict__ dst, int K,
+                                                                int N) {
+  const int kb = K >> 5, t = blockIdx.x, pn = blockIdx.y;
+  const float* __restrict__ bz = src + (int64_t)blockIdx.z * stride_b;
+  float* __restrict__ dz = dst + (int64_t)blockIdx.z * K * N;
+  const int tid = threadIdx.x;
+  if (t < kb) {
+    const int q = tid >> 6, lane = tid & 63;
+    const int k = 32 * t + 16 * (lane >> 5) + 4 * q, n = 32 * pn + (lane & 31);
+    const float* __restrict__ b = bz + (int64_t)k * ldb + n;
+    f32x4 v;
+    v[0] = b[0];
+    v[1] = b[ldb];
+    v[2] = b[2 * ldb];
+    v[3] = b[3 * ldb];
+    *reinterpret_cast<f32x4*>(dz + ((int64_t)pn * kb + t) * 1024 + tid * 4) = v;
+    return;
+  }
+  const int kf = kb * 32;  // K tail rows of panel p: row-major [K - kf, N]
+  for (int i = tid; i < (K - kf) * 32; i += 256) {
+    const int k = kf + (i >> 5), n = 32 * pn + (i & 31);
+    dz[(int64_t)N * kf + (int64_t)(k - kf) * N + n] = bz[(int64_t)k * ldb + n];
+  }
+}
+
 __global__ void pack_rhs_kernel(const float* __restrict__ src, float* __restrict__ dst, int64_t K,
                                 int64_t N) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -854,13 +929,18 @@ int launch_pipe(const GemmParams& p0, int64_t batch, hipStream_t stream) {
   p.tiles_m = (p.m + BM - 1) / BM;
   p.tiles_n = (p.n + BN - 1) / BN;
   dim3 grid(p.tiles_m * p.tiles_n, 1, (unsigned)batch);
-  hipLaunchKernelGGL((gemm_packed_pipe_kernel<WM, WN, BMB, BNB, S, NACC, KS, KSUB>), grid,
-                     dim3(64 * WM * WN * KS), 0, stream, p);
+  if (p.a_vec)
+    hipLaunchKernelGGL((gemm_packed_pipe_kernel<WM, WN, BMB, BNB, S, NACC, KS, KSUB, true>), grid,
+                       dim3(64 * WM * WN * KS), 0, stream, p);
+  else
+    hipLaunchKernelGGL((gemm_packed_pipe_kernel<WM, WN, BMB, BNB, S, NACC, KS, KSUB, false>),
+                       grid, dim3(64 * WM * WN * KS), 0, stream, p);
   ANNC_HIP_TRY(hipGetLastError());
   return ANNC_OK;
 }
 
-// Packed B with N % 32 == 0 and 16-byte aligned A rows: the LDS-DMA pipeline.
+// Packed B with N % 32 == 0: the LDS-DMA pipeline (16-byte DMAs for A rows
+// that are 16-byte aligned, 4-byte DMAs otherwise).
 // Largest tile that still gives every CU (256 on MI355X) a workgroup.
 int launch_packed_pipe(const GemmParams& p, int64_t batch, hipStream_t stream) {
   const int64_t cus = 256;
@@ -980,8 +1060,30 @@ int annc_hip_gemm(void* stream, int64_t batch, int64_t m, int64_t n, int64_t k, 
   }
   if (b_packed) {
     ANNC_REQUIRE(aligned16(b) && stride_b % 4 == 0, "packed B must be 16-byte aligned");
-    if (n % 32 == 0 && p.a_vec) return launch_packed_pipe(p, batch, s);
+    if (n % 32 == 0) return launch_packed_pipe(p, batch, s);
     return launch_gemm<true>(p, batch, s);
+  }
+  // Large row-major-B GEMMs (the __matmul* custom calls, whose weights XLA
+  // passes row-major): pack B into the stream workspace and run the LDS-DMA
+  // pipeline.  Packing moves 8*K*N bytes; the pipeline runs the tower
+  // shapes about 1.5x faster than the row-major kernel.
+  const int64_t tiles64 = ceil_div(m, 64) * ceil_div(n, 64) * batch;
+  const int64_t packed_bytes = batch * k * n * static_cast<int64_t>(sizeof(float));
+  if (n % 32 == 0 && k >= 32 && m >= 512 && tiles64 >= 128 &&
+      packed_bytes <= (int64_t(1) << 31)) {
+    float* bp = static_cast<float*>(stream_workspace(s, static_cast<size_t>(packed_bytes)));
+    if (bp) {
+      const dim3 grid((unsigned)((k >> 5) + ((k & 31) ? 1 : 0)), (unsigned)(n >> 5),
+                      (unsigned)batch);
+      hipLaunchKernelGGL(pack_rhs_rowmajor_kernel, grid, dim3(256), 0, s, b, ldb, stride_b, bp,
+                         (int)k, (int)n);
+      ANNC_HIP_TRY(hipGetLastError());
+      GemmParams q = p;
+      q.b = bp;
+      q.ldb = n;
+      q.stride_b = k * n;
+      return launch_packed_pipe(q, batch, s);
+    }
   }
   return launch_gemm<false>(p, batch, s);
 }

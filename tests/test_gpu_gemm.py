@@ -76,11 +76,17 @@ def test_layout_matmul_packed(m, n, k):
     assert_gemm_close(to_host(got), ref, gemm_bound(a, w))
 
 
-# Packed B with N % 32 == 0 and 16-byte aligned A rows runs the LDS-DMA
-# pipelined kernel: each of its three tile configurations (128x128, 128x64,
-# 64x64, chosen by how many tiles the shape yields), partial M and N tiles,
-# a K tail with and without full k-blocks, padded lda, addend and sigmoid.
+# Packed B with N % 32 == 0 runs the LDS-DMA pipelined kernel: each of its
+# three tile configurations (128x128, 128x64, 64x64, chosen by how many tiles
+# the shape yields), partial M and N tiles, a K tail with and without full
+# k-blocks, padded lda, addend and sigmoid; A rows that are not 16-byte
+# aligned (lda % 4 != 0) take the 4-byte DMA variant.
 PIPE_CASES = [
+    (4096, 1024, 845, 845, "128x128 tiles, unaligned A rows (4-byte DMA)"),
+    (4096, 512, 1023, 1023, "128x64 tiles, unaligned A rows"),
+    (4096, 256, 510, 510, "64x64 split-K tiles, unaligned A rows"),
+    (1000, 96, 845, 845, "partial tiles and K tail, unaligned A rows"),
+    (130, 64, 96, 97, "3 k-blocks, lda % 4 == 1"),
     (4096, 1024, 864, 864, "128x128 tiles"),
     (4096, 512, 1024, 1024, "128x64 tiles"),
     (4096, 256, 512, 516, "64x64 tiles, padded lda"),
@@ -281,3 +287,51 @@ def test_batch_matmul_add_sigmoid_broadcasts(bias_shape, rhs_batched):
     ref = ora.batch_matmul_add_sigmoid(lhs, rhs, bias)
     got = tf_ops.kp_fused_batch_matmul_add_sigmoid(lhs, rhs, bias)
     np.testing.assert_allclose(got, ref, rtol=0, atol=1e-5)
+
+
+# (each shape has m >= 512, n % 32 == 0 and at least 128 64x64 tiles, the
+# condition for packing B per call)
+@pytest.mark.parametrize("batch,m,n,k,ldb_pad", [(1, 2048, 320, 845, 80), (1, 4096, 512, 1024, 0),
+                                                 (3, 1024, 256, 200, 0), (1, 8192, 64, 33, 7),
+                                                 (2, 4000, 96, 64, 32)])
+def test_row_major_b_packed_per_call(batch, m, n, k, ldb_pad):
+    """Large row-major-B GEMMs pack B into the stream workspace and run the
+    pipelined kernel: within tolerance of OpenBLAS, and bit-identical to the
+    same GEMM on weights packed ahead of time (so the per-call packing
+    equals the layout_matmul packer, K tails and strided B included, and the
+    pipelined kernel ran)."""
+    note(f"row-major B packed per call b={batch} {m}x{n}x{k} ldb+{ldb_pad}")
+    g = workloads.rng(m + n + k + batch)
+    a = g.standard_normal((batch, m, k)).astype(np.float32)
+    wide = (g.standard_normal((batch, k, n + ldb_pad)) * 0.05).astype(np.float32)
+    b = wide[:, :, :n]
+    e = g.standard_normal((batch, m, n)).astype(np.float32)
+    da, de = to_dev(a), to_dev(e)
+    db = to_dev(wide)[:, :, :n]
+    if batch == 1:
+        got = to_host(dev.gemm(da[0], db[0], addend=de[0], epilogue=EPI_RELU))[None]
+    else:
+        got = to_host(dev.gemm(da, db, addend=de, epilogue=EPI_RELU))
+    for z in range(batch):
+        ref = ora.matmul_add_relu(e[z], a[z], np.ascontiguousarray(b[z]))
+        assert_gemm_close(got[z], ref, gemm_bound(a[z], b[z], e[z]))
+        pw = dev.pack_weight(to_dev(b[z]))
+        pre = to_host(dev.gemm(da[z], pw, addend=de[z], epilogue=EPI_RELU))
+        np.testing.assert_array_equal(got[z], pre)
+
+
+@pytest.mark.parametrize("m,n,k,col0", [(2048, 512, 256, 1), (8192, 64, 333, 3)])
+def test_pipeline_misaligned_a_base(m, n, k, col0):
+    """A starting mid-row of a wider buffer (base not 16-byte aligned, lda a
+    multiple of 4): the 4-byte DMA variant, bit-identical between packed and
+    per-call-packed row-major B."""
+    note(f"misaligned A base {m}x{n}x{k} col0={col0}")
+    g = workloads.rng(m + n + k + col0)
+    buf = g.standard_normal((m, k + 8)).astype(np.float32)
+    a = np.ascontiguousarray(buf[:, col0:col0 + k])
+    w = (g.standard_normal((k, n)) * 0.05).astype(np.float32)
+    da = to_dev(buf)[:, col0:col0 + k]
+    ref = ora.matmul(a, w)
+    got = to_host(dev.gemm(da, dev.pack_weight(to_dev(w))))
+    assert_gemm_close(got, ref, gemm_bound(a, w))
+    np.testing.assert_array_equal(to_host(dev.gemm(da, to_dev(w))), got)
