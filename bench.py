@@ -127,7 +127,7 @@ def bench_tower(args, device):
     k1_flops = 2.0 * m * n * k
     achieved = k1_flops / (k1_ms * 1e-3) / 1e12
     roofline = {
-        "kernel": "gemm_packed_pipe_kernel<4,2,1,1,2,2,1,2> (layer 1: 4096x512x1024 packed B + bias + ReLU)",
+        "kernel": "gemm_packed_pipe_kernel<4,2,1,1,2,2,1,2,true> (layer 1: 4096x512x1024 packed B + bias + ReLU)",
         "bound": "mfma",
         "achieved": round(achieved, 3),
         "peak": FP32_MFMA_PEAK_TFLOPS,
@@ -259,22 +259,25 @@ def bench_config5(device, steps: int):
     ids = torch.from_numpy(h.ids).to(device)
     offs = torch.from_numpy(h.offsets).to(device)
     dense = torch.from_numpy(w.dense).to(device)
-    # One step = one HIP-graph replay of the whole graph (hash bags, dense
-    # copy, 4 GEMMs): with 6 kernels per step the replay beats per-kernel
-    # launches; the launched-on-a-stream time is reported beside it.
+    # One step = the whole graph (hash bags, dense copy, 4 GEMMs), timed both
+    # as one HIP-graph replay and as its 6 kernels launched on one stream;
+    # which is faster varies from box to box (±6%), so the step is the faster
+    # of the two and both are reported.
     replay = CapturedGraph(graph, ids, offs, dense)
-    ms, _ = time_steps(replay.replay, steps, 5)
-    sps = h.batch / (ms * 1e-3)
-    log(f"e2e wide&deep: {ms * 1e3:.1f} us/step, {sps:.0f} samples/s")
+    graph_ms, _ = time_steps(replay.replay, steps, 5)
     eager_ms, _ = time_steps(lambda: graph(ids, offs, dense), steps, 5)
-    log(f"e2e wide&deep (launched per kernel): {eager_ms * 1e3:.1f} us/step")
+    ms = min(graph_ms, eager_ms)
+    mode = "one HIP-graph replay" if graph_ms <= eager_ms else "6 kernels launched on one stream"
+    sps = h.batch / (ms * 1e-3)
+    log(f"e2e wide&deep: graph {graph_ms * 1e3:.1f} us/step, per kernel "
+        f"{eager_ms * 1e3:.1f} us/step; {sps:.0f} samples/s")
     return {"workload": "configs[4] wide&deep: 26 hashed fields dim 32 (Zipf ids, bags 1-5) + 13 "
                         "dense -> concat [4096x845] -> 1024-512-256-1 -> sigmoid",
             "ms_per_step": round(ms, 4), "samples_per_s": round(sps, 1),
             "gemm_tflops": round(graph.flops(h.batch) / (ms * 1e-3) / 1e12, 2),
-            "step": "one HIP-graph replay",
-            "launched_per_kernel_ms_per_step": round(eager_ms, 4),
-            "launched_per_kernel_samples_per_s": round(h.batch / (eager_ms * 1e-3), 1)}
+            "step": mode,
+            "graph_replay_ms_per_step": round(graph_ms, 4),
+            "launched_per_kernel_ms_per_step": round(eager_ms, 4)}
 
 
 # ---------------------------------------------------------------- CPU baseline
