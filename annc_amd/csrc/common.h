@@ -26,8 +26,8 @@ int* stream_status(hipStream_t stream);
 // frees the previous buffer (hipFree synchronises the device first).
 void* stream_workspace(hipStream_t stream, size_t bytes);
 
-// The library's own stream on the current device (default priority), used by
-// the synchronous entry points.
+// The library's own stream of the calling thread on the current device
+// (default priority), used by the synchronous entry points.
 hipStream_t lib_stream();
 
 // True for memory the GPU can address directly (device or managed).

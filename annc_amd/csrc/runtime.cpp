@@ -23,7 +23,10 @@ struct StreamState {
 std::mutex g_mu;
 // Keyed by (device, stream): the NULL stream exists once per device.
 std::map<std::pair<int, hipStream_t>, StreamState> g_streams;
-std::map<int, hipStream_t> g_lib_streams;
+// The synchronous XLA/TF entries run on a library stream of the calling
+// thread: concurrent callers never share a stream, so their kernels cannot
+// interleave and each stream's workspace has a single user.
+thread_local std::map<int, hipStream_t> t_lib_streams;
 
 int current_device() {
   int dev = 0;
@@ -81,13 +84,12 @@ void* stream_workspace(hipStream_t stream, size_t bytes) {
 }
 
 hipStream_t lib_stream() {
-  std::lock_guard<std::mutex> lock(g_mu);
-  int dev = current_device();
-  auto it = g_lib_streams.find(dev);
-  if (it != g_lib_streams.end()) return it->second;
+  const int dev = current_device();
+  auto it = t_lib_streams.find(dev);
+  if (it != t_lib_streams.end()) return it->second;
   hipStream_t s = nullptr;
   if (hipStreamCreateWithFlags(&s, hipStreamNonBlocking) != hipSuccess) s = nullptr;
-  g_lib_streams[dev] = s;
+  t_lib_streams[dev] = s;
   return s;
 }
 

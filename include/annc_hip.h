@@ -11,11 +11,15 @@
  * Pointer classes:
  *   - "any" pointers may be host memory or HIP device memory; the library
  *     inspects them (hipPointerGetAttributes) and stages host data through
- *     the device on an internal stream, synchronising before it returns.
- *     This is the contract of the XLA-CPU custom calls and the TF CPU ops.
+ *     the device on a stream of its own, one per calling thread and device,
+ *     synchronising before it returns.  This is the contract of the XLA-CPU
+ *     custom calls and the TF CPU ops; concurrent callers on different
+ *     threads never share a stream.
  *   - "device" pointers must be device memory; those entry points enqueue on
- *     the caller's stream (a hipStream_t passed as void*, NULL = the
- *     library's per-device stream) and return without synchronising.
+ *     the caller's stream (a hipStream_t passed as void*, NULL = HIP's null
+ *     stream of the current device) and return without synchronising.  The
+ *     library keeps scratch memory per stream, so calls on one stream must
+ *     be issued from one thread at a time.
  */
 #ifndef ANNC_HIP_H_
 #define ANNC_HIP_H_

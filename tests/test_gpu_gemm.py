@@ -335,3 +335,37 @@ def test_pipeline_misaligned_a_base(m, n, k, col0):
     got = to_host(dev.gemm(da, dev.pack_weight(to_dev(w))))
     assert_gemm_close(got, ref, gemm_bound(a, w))
     np.testing.assert_array_equal(to_host(dev.gemm(da, to_dev(w))), got)
+
+
+def test_custom_calls_from_concurrent_threads():
+    """The synchronous custom calls run on a stream of the calling thread:
+    threads calling __matmul_add_relu at once (host buffers, shapes that
+    pack B into the stream workspace) each get their own result."""
+    import threading
+    note("custom calls from 4 threads")
+    g = workloads.rng(77)
+    cases = []
+    for t in range(4):
+        m, k, n = 1024 + 512 * t, 96 + 8 * t, 256
+        a = g.standard_normal((m, k)).astype(np.float32)
+        b = (g.standard_normal((k, n)) * 0.05).astype(np.float32)
+        e = g.standard_normal((m, n)).astype(np.float32)
+        cases.append((a, b, e, np.zeros((m, n), np.float32), np.empty((m, n), np.float32)))
+    errors = []
+
+    def work(c):
+        a, b, e, z, out = c
+        try:
+            for _ in range(5):
+                xla.matmul_add_relu(z, e, a, b, out)
+                assert_gemm_close(out, ora.matmul_add_relu(e, a, b), gemm_bound(a, b, e))
+        except Exception as ex:  # reported below
+            errors.append(ex)
+
+    threads = [threading.Thread(target=work, args=(c,)) for c in cases]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout=100)
+    assert not any(t.is_alive() for t in threads), "a worker thread did not finish"
+    assert not errors, errors[0]
