@@ -39,6 +39,8 @@ int read_i64(const void* src, int64_t count, int64_t* dst);
 // Staging for synchronous entry points whose operands may live in host
 // memory: inputs are copied to device scratch, outputs are produced in
 // device scratch and copied back by finish().  Device operands pass through.
+// The scratch comes from a grow-only arena of the calling thread and is
+// released when the Staging object is destroyed (after its stream drained).
 class Staging {
  public:
   explicit Staging(hipStream_t stream);
@@ -66,6 +68,7 @@ class Staging {
   void* alloc(size_t bytes);
   hipStream_t stream_;
   int status_ = ANNC_OK;
+  bool finished_ = false;
   std::vector<void*> owned_;
   std::vector<Pending> pending_;
 };

@@ -3,6 +3,7 @@
 #include <cstdio>
 #include <cstring>
 #include <map>
+#include <algorithm>
 #include <mutex>
 #include <string>
 #include <utility>
@@ -116,15 +117,56 @@ int read_i64(const void* src, int64_t count, int64_t* dst) {
   return ANNC_OK;
 }
 
-Staging::Staging(hipStream_t stream) : stream_(stream) {}
+namespace {
+// Grow-only device staging memory of the calling thread (one per device).
+// A Staging object carves its buffers from it and releases them when it is
+// destroyed, after its stream has drained, so the next synchronous call of
+// the thread reuses the memory with no hipMalloc/hipFree (hipFree would
+// synchronise the whole device).
+struct Arena {
+  char* base = nullptr;
+  size_t size = 0, used = 0, want = 0;
+  int depth = 0;  // live Staging objects of the thread on this device
+};
+thread_local std::map<int, Arena> t_arenas;
+constexpr size_t kStagingAlign = 256;
+}  // namespace
+
+Staging::Staging(hipStream_t stream) : stream_(stream) { ++t_arenas[current_device()].depth; }
 
 Staging::~Staging() {
+  // Work of a call that returned without finish() may still use the memory:
+  // drain the stream before handing it back.
+  if (!finished_) (void)hipStreamSynchronize(stream_);
   for (void* p : owned_) (void)hipFree(p);
+  Arena& ar = t_arenas[current_device()];
+  if (--ar.depth > 0) return;  // an enclosing Staging still holds its buffers
+  ar.used = 0;
+  if (ar.want > ar.size) {  // grow for the next call: nothing is in flight now
+    (void)hipStreamSynchronize(stream_);
+    if (ar.base) (void)hipFree(ar.base);
+    ar.base = nullptr;
+    ar.size = 0;
+    const size_t grow = ar.want + ar.want / 4;
+    if (hipMalloc(reinterpret_cast<void**>(&ar.base), grow) == hipSuccess)
+      ar.size = grow;
+    else
+      ar.base = nullptr;
+    ar.want = 0;
+  }
 }
 
 void* Staging::alloc(size_t bytes) {
-  void* p = nullptr;
   if (bytes == 0) bytes = 4;
+  const size_t rounded = (bytes + kStagingAlign - 1) / kStagingAlign * kStagingAlign;
+  Arena& ar = t_arenas[current_device()];
+  if (ar.base && ar.used + rounded <= ar.size) {
+    void* p = ar.base + ar.used;
+    ar.used += rounded;
+    return p;
+  }
+  ar.want = std::max(ar.want, ar.used + rounded);
+  void* p = nullptr;
   hipError_t e = hipMalloc(&p, bytes);
   if (e != hipSuccess) {
     status_ = set_error(ANNC_RESOURCE_EXHAUSTED, "hipMalloc(%zu) failed: %s", bytes,
@@ -175,6 +217,7 @@ int Staging::finish() {
     return status_ = set_error(ANNC_INTERNAL, "stream synchronize failed: %s",
                                hipGetErrorString(e));
   pending_.clear();
+  finished_ = true;
   return ANNC_OK;
 }
 
