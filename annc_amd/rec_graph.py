@@ -169,6 +169,14 @@ class WideDeepGraph:
     def flops(self, batch: int) -> int:
         return self.tower.flops(batch)
 
+    def dense_view(self, batch: int) -> torch.Tensor:
+        """The dense-feature columns of the concat buffer ([batch, num_dense],
+        row stride ld).  A producer that writes the dense features here (the
+        host-to-device copy of a serving loop) makes the concat free: forward()
+        skips the copy when it is given this view."""
+        emb_cols = self.cfg.num_fields * self.cfg.dim
+        return self.concat_buffer(batch)[:, emb_cols:self.concat_width]
+
     def forward(self, ids: torch.Tensor, offsets: torch.Tensor, dense: torch.Tensor,
                 stream=None) -> torch.Tensor:
         batch = dense.shape[0]
@@ -177,7 +185,10 @@ class WideDeepGraph:
         emb_cols = cfg.num_fields * cfg.dim
         dev.hashed_embedding_bags(self.tables, [cfg.num_buckets] * cfg.num_fields, ids, offsets,
                                   batch, cfg.combiner, out=buf[:, :emb_cols], stream=stream)
-        buf[:, emb_cols:self.concat_width].copy_(dense)
+        view = buf[:, emb_cols:self.concat_width]
+        if not (dense.data_ptr() == view.data_ptr() and dense.stride() == view.stride()
+                and dense.shape == view.shape):
+            view.copy_(dense)
         x = buf[:, :self.concat_width]
         return self.tower.forward(x, stream=stream)
 

@@ -252,6 +252,13 @@ def test_config5_wide_deep_graph():
     concat = to_host(graph.concat_buffer(h.batch))[:, :x.shape[1]]
     np.testing.assert_array_equal(concat, x)  # embeddings bit-exact, dense copied
     np.testing.assert_allclose(y, ora.mlp_tower(x, w.weights, w.biases), rtol=1e-3, atol=1e-5)
+    # dense features written straight into the concat buffer: same result, no copy
+    graph.concat_buffer(h.batch).zero_()
+    view = graph.dense_view(h.batch)
+    view.copy_(to_dev(w.dense))
+    y2 = to_host(graph(to_dev(h.ids), to_dev(h.offsets), view))
+    np.testing.assert_array_equal(to_host(graph.concat_buffer(h.batch))[:, :x.shape[1]], x)
+    np.testing.assert_array_equal(y2, y)
 
 
 # ---------------------------------------------------------------- KPFusedBatchMatMulAddSigmoid
