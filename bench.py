@@ -263,15 +263,16 @@ def bench_config5(device, steps: int):
     # needs no concat copy; the embedding kernel writes its columns in place
     dense = graph.dense_view(h.batch)
     dense.copy_(torch.from_numpy(w.dense).to(device))
-    # One step = the whole graph (hash bags, dense copy, 4 GEMMs), timed both
-    # as one HIP-graph replay and as its 6 kernels launched on one stream;
+    # One step = the whole graph (hashed bags into the concat buffer, 4 GEMMs),
+    # timed both as one HIP-graph replay and as its kernels launched on one
+    # stream;
     # which is faster varies from box to box (±6%), so the step is the faster
     # of the two and both are reported.
     replay = CapturedGraph(graph, ids, offs, dense)
     graph_ms, _ = time_steps(replay.replay, steps, 5)
     eager_ms, _ = time_steps(lambda: graph(ids, offs, dense), steps, 5)
     ms = min(graph_ms, eager_ms)
-    mode = "one HIP-graph replay" if graph_ms <= eager_ms else "6 kernels launched on one stream"
+    mode = "one HIP-graph replay" if graph_ms <= eager_ms else "kernels launched on one stream"
     sps = h.batch / (ms * 1e-3)
     log(f"e2e wide&deep: graph {graph_ms * 1e3:.1f} us/step, per kernel "
         f"{eager_ms * 1e3:.1f} us/step; {sps:.0f} samples/s")
