@@ -221,3 +221,37 @@ def test_fused_gather_negative_and_huge_keys_group_correctly():
     du, didx, _ = dev.unique_gather(to_dev(table[:, :0].copy()), to_dev(keys), col=0)
     assert to_host(du).tolist() == [5, -(2**63), 2**63 - 1, -1, 0]
     assert to_host(didx).tolist() == [0, 1, 2, 0, 3, 1, 4]
+
+
+def _formula_table_dev(rows, dim):
+    """[rows, dim] float32 on the device with value ((r % 1000) - 500) * 0.001 + c,
+    exactly reproducible on the host for any row subset."""
+    r = ((torch.arange(rows, device=device(), dtype=torch.int64) % 1000) - 500).to(torch.float32)
+    c = torch.arange(dim, device=device(), dtype=torch.float32)
+    return (r * torch.tensor(0.001, dtype=torch.float32, device=device()))[:, None] + c[None, :]
+
+
+def _formula_rows_host(row_ids, dim):
+    r = ((np.asarray(row_ids, dtype=np.int64) % 1000) - 500).astype(np.float32)
+    return (r * np.float32(0.001))[:, None] + np.arange(dim, dtype=np.float32)[None, :]
+
+
+@pytest.mark.parametrize("combiner", [0, 1])
+def test_embedding_bag_table_over_2gib(combiner):
+    """A table of 2.15 GB (the 64-bit address path): rows past byte 2^31
+    gathered bit-exactly."""
+    rows, dim = 8_400_000, 64  # 8_400_000 * 256 B > 2^31
+    note(f"embedding bag 2.15 GB table combiner={combiner}")
+    table = _formula_table_dev(rows, dim)
+    g = workloads.rng(2024 + combiner)
+    lens = g.integers(1, 9, size=300)
+    offsets = np.zeros(301, dtype=np.int64)
+    np.cumsum(lens, out=offsets[1:])
+    ids = g.integers(0, rows, size=int(offsets[-1]), dtype=np.int64)
+    ids[::3] = g.integers((1 << 31) // (4 * dim), rows, size=ids[::3].size)  # past 2 GiB
+    uniq, inv = np.unique(ids, return_inverse=True)
+    ref = ora.embedding_bag(_formula_rows_host(uniq, dim), inv.astype(np.int64), offsets, combiner)
+    got = to_host(dev.embedding_bag(table, to_dev(ids), to_dev(offsets), combiner))
+    np.testing.assert_array_equal(got, ref)
+    del table
+    torch.cuda.empty_cache()

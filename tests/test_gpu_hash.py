@@ -6,6 +6,7 @@ import os
 
 import numpy as np
 import pytest
+import torch
 
 from annc_amd import tf_ops, workloads
 from annc_amd import device as dev
@@ -179,3 +180,34 @@ def test_hashed_bags_ragged_mixed_ids(dim, combiner):
     got = to_host(out_full)
     np.testing.assert_array_equal(got[:, :nf * dim].reshape(batch, nf, dim), ref)
     np.testing.assert_array_equal(got[:, nf * dim:], 7.0)  # padding untouched
+
+
+def test_hashed_bags_table_of_2gib():
+    """A field table of exactly 2 GiB (2^25 rows x 16 floats) takes the
+    64-bit-address kernel; buckets from the oracle's FarmHash, sums in index
+    order."""
+    rows, dim, batch = 1 << 25, 16, 512
+    note("hashed bags 2 GiB table")
+    r = ((torch.arange(rows, device=device(), dtype=torch.int64) % 1000) - 500).to(torch.float32)
+    table = (r * torch.tensor(0.001, dtype=torch.float32, device=device()))[:, None] + \
+        torch.arange(dim, device=device(), dtype=torch.float32)[None, :]
+    del r
+    g = workloads.rng(4096)
+    ids, offsets = workloads.hashed_structure(g, 1, batch, lo=1, hi=6)
+    buckets = ora.hash_bucket_int64(ids, rows)
+    vals = (((buckets % 1000) - 500).astype(np.float32) * np.float32(0.001))[:, None] + \
+        np.arange(dim, dtype=np.float32)[None, :]
+    ref = np.zeros((batch, dim), dtype=np.float32)
+    for b in range(batch):
+        acc = np.zeros(dim, dtype=np.float32)
+        for p in range(offsets[b], offsets[b + 1]):
+            acc = acc + vals[p]
+        n = offsets[b + 1] - offsets[b]
+        ref[b] = acc * np.float32(1.0 / np.float32(n)) if n else acc
+    got_b = to_dev(np.full(ids.size, -7, dtype=np.int64))
+    out = dev.hashed_embedding_bags([table], [rows], to_dev(ids), to_dev(offsets), batch, 1,
+                                    buckets_out=got_b)
+    np.testing.assert_array_equal(to_host(got_b), buckets)
+    np.testing.assert_array_equal(to_host(out), ref)
+    del table
+    torch.cuda.empty_cache()
