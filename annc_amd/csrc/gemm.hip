@@ -484,11 +484,13 @@ __global__ __launch_bounds__(64 * W) void gemm_small_kernel(GemmParams p) {
 //
 // Operand tiles stream global -> LDS through gfx950's 16-byte LDS-DMA loads
 // (global_load_lds_dwordx4: lane i of a wave writes bytes [16i, 16i+16) of a
-// 1 KiB LDS block), S stages deep, so no VGPRs stage the data and up to S-1
+// 1 KiB LDS block), S stages deep, so no VGPRs stage the data and up to S-2
 // stages are in flight while the MFMAs run on the oldest.  A stage holds
-// KSUB consecutive 32-k blocks.  One barrier per stage: a wave waits for its
-// own DMAs of the stage (vmcnt), the barrier publishes everyone's, and only
-// then is the slot freed by the previous stage refilled.
+// KSUB consecutive 32-k blocks.  One barrier per stage, halfway through it:
+// a wave waits for its own DMAs of the next stage (vmcnt), the barrier
+// publishes everyone's, and the slot of the previous stage is refilled.  The
+// next stage's first fragments are then read under the current stage's last
+// MFMAs, so the stage boundary itself has no barrier or LDS-latency gap.
 //   * WM x WN waves own BLK_M x BLK_N 32x32 accumulator blocks each; with
 //     KS = 2 a second group of WM x WN waves takes the other half of every
 //     k-block (quads 2-3) and the two partial tiles are added through LDS
@@ -540,6 +542,10 @@ __device__ __forceinline__ void block_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
+// Barrier with no LDS wait: for points where this wave's LDS reads of the
+// slot about to be refilled were consumed by MFMAs long before.
+__device__ __forceinline__ void barrier_only() { asm volatile("s_barrier" ::: "memory"); }
+
 __device__ __forceinline__ int a_swizzle(int row) { return (row & 7) ^ ((row >> 3) & 1); }
 
 }  // namespace pipe
@@ -555,7 +561,7 @@ __global__ __launch_bounds__(64 * WM * WN * KS) void gemm_packed_pipe_kernel(Gem
   constexpr int BM = WM * BLK_M * 32, BN = WN * BLK_N * 32;
   constexpr int NA = BM / 8, NB = BN / 8, NBLK = NA + NB;  // 1 KiB blocks per stage
   static_assert(NBLK % NW == 0, "stage blocks split evenly over the waves");
-  static_assert(S >= 2 && S <= 4, "2..4 stages");
+  static_assert(S >= 3 && S <= 4, "3 or 4 stages: the next stage is published mid-stage");
   static_assert(KS == 1 || NT * 2 * BLK_M * BLK_N * 2 <= S * KSUB * NBLK, "exchange fits in LDS");
   constexpr int LPW = NBLK / NW;                    // 1 KiB blocks per wave per k-block
   // A rows that are not 16-byte aligned load each A block with four 4-byte
@@ -676,62 +682,79 @@ __global__ __launch_bounds__(64 * WM * WN * KS) void gemm_packed_pipe_kernel(Gem
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[c][i][j][r] = 0.0f;
 
-  auto compute_sub = [&](const f32x4* cur) {
+#pragma unroll
+  for (int s = 0; s < S - 1; ++s)
+    if (s < KB) issue(s, s);
+  {
+    // Mid-stage barrier.  Halfway through stage kb every wave waits for its
+    // DMAs of stage kb+1 and meets the others; stage kb+S-1 then refills the
+    // slot of stage kb-1, which no wave reads any more.  So stage kb+1 is
+    // published half a stage before it is needed, and the fragments of its
+    // first quad are read during the last MFMAs of stage kb: the MFMA pipes
+    // see no barrier or LDS-latency gap at the stage boundary.
+    constexpr int QPS = KSUB * NQ;  // 8-k quads per wave per stage (even)
+    constexpr int HALF = QPS / 2;
     f32x4 af[2][BLK_M], bf[2][BLK_N];
-    auto frag = [&](int qi, int buf) {
-      const int q = q0 + qi;
+    auto frag_at = [&](const f32x4* stage, int t, int buf) {
+      const f32x4* cur = stage + (t / NQ) * NBLK * 64;
+      const int q = q0 + t % NQ;
 #pragma unroll
       for (int i = 0; i < BLK_M; ++i) af[buf][i] = cur[a_off[i] + ((4 * half + q) ^ a_swz[i])];
 #pragma unroll
       for (int j = 0; j < BLK_N; ++j) bf[buf][j] = cur[(NA + (wn * BLK_N + j) * 4 + q) * 64 + lane];
     };
-    frag(0, 0);
-#pragma unroll
-    for (int qi = 0; qi < NQ; ++qi) {
-      if (qi < NQ - 1) frag(qi + 1, (qi + 1) & 1);
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-#pragma unroll
-        for (int i = 0; i < BLK_M; ++i)
-#pragma unroll
-          for (int j = 0; j < BLK_N; ++j)
-            acc[e % NACC][i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(
-                af[qi & 1][i][e], bf[qi & 1][j][e], acc[e % NACC][i][j], 0, 0, 0);
-      if (qi < NQ - 1) {
-        // one fragment read between consecutive MFMAs, then the rest
-#pragma unroll
-        for (int r = 0; r < BLK_M + BLK_N; ++r) {
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-        }
-        __builtin_amdgcn_sched_group_barrier(0x008, 4 * BLK_M * BLK_N - (BLK_M + BLK_N), 0);
-      }
+    if (KB > 0) {
+      const int inflight = min(KB - 1, S - 2);  // stages 1 .. S-2 may stay in flight
+      if (inflight >= 2)
+        pipe::wait_vmcnt<2 * KSUB * DMAS>();
+      else if (inflight == 1)
+        pipe::wait_vmcnt<KSUB * DMAS>();
+      else
+        pipe::wait_vmcnt<0>();
+      pipe::barrier_only();
+      frag_at(&lds[0][0], 0, 0);
     }
-  };
-  auto compute = [&](int slot) {
+    for (int kb0 = 0; kb0 < KB; kb0 += S) {
 #pragma unroll
-    for (int sub = 0; sub < KSUB; ++sub) compute_sub(&lds[slot][sub * NBLK * 64]);
-  };
-
+      for (int u = 0; u < S; ++u) {
+        const int kb = kb0 + u;
+        if (kb < KB) {
+          const f32x4* cur = &lds[u][0];
+          const f32x4* nxt = &lds[(u + 1) % S][0];
 #pragma unroll
-  for (int s = 0; s < S - 1; ++s)
-    if (s < KB) issue(s, s);
-  for (int kb0 = 0; kb0 < KB; kb0 += S) {
+          for (int t = 0; t < QPS; ++t) {
+            const int b = t & 1;
+            // next quad's fragments; after the last stage this reads a stale
+            // slot whose values are never used (no branch around the reads)
+            if (t + 1 < QPS)
+              frag_at(cur, t + 1, b ^ 1);
+            else
+              frag_at(nxt, 0, b ^ 1);
 #pragma unroll
-    for (int u = 0; u < S; ++u) {
-      const int kb = kb0 + u;
-      if (kb < KB) {
-        // stages kb+1 .. kb+S-2 may stay in flight
-        const int after = min(KB - 1 - kb, S - 2);
-        if (after >= 2)
-          pipe::wait_vmcnt<2 * KSUB * DMAS>();
-        else if (after == 1)
-          pipe::wait_vmcnt<KSUB * DMAS>();
-        else
-          pipe::wait_vmcnt<0>();
-        pipe::block_barrier();
-        if (kb + S - 1 < KB) issue((u + S - 1) % S, kb + S - 1);
-        compute(u);
+            for (int e = 0; e < 4; ++e)
+#pragma unroll
+              for (int i = 0; i < BLK_M; ++i)
+#pragma unroll
+                for (int j = 0; j < BLK_N; ++j)
+                  acc[e % NACC][i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(
+                      af[b][i][e], bf[b][j][e], acc[e % NACC][i][j], 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < BLK_M + BLK_N; ++r) {
+              __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+              __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x008, 4 * BLK_M * BLK_N - (BLK_M + BLK_N), 0);
+            if (t == HALF - 1 && kb + 1 < KB) {
+              // stages kb+2 .. kb+S-2 may stay in flight (S <= 4: at most one)
+              if (S >= 4 && kb + 2 < KB)
+                pipe::wait_vmcnt<KSUB * DMAS>();
+              else
+                pipe::wait_vmcnt<0>();
+              pipe::barrier_only();
+              if (kb + S - 1 < KB) issue((u + S - 1) % S, kb + S - 1);
+            }
+          }
+        }
       }
     }
   }
@@ -930,8 +953,8 @@ int launch_pipe(const GemmParams& p0, int64_t batch, hipStream_t stream) {
   p.tiles_n = (p.n + BN - 1) / BN;
   dim3 grid(p.tiles_m * p.tiles_n, 1, (unsigned)batch);
   if (p.a_vec)
-    hipLaunchKernelGGL((gemm_packed_pipe_kernel<WM, WN, BMB, BNB, S, NACC, KS, KSUB, true>), grid,
-                       dim3(64 * WM * WN * KS), 0, stream, p);
+    hipLaunchKernelGGL((gemm_packed_pipe_kernel<WM, WN, BMB, BNB, S, NACC, KS, KSUB, true>),
+                       grid, dim3(64 * WM * WN * KS), 0, stream, p);
   else
     hipLaunchKernelGGL((gemm_packed_pipe_kernel<WM, WN, BMB, BNB, S, NACC, KS, KSUB, false>),
                        grid, dim3(64 * WM * WN * KS), 0, stream, p);
@@ -940,26 +963,21 @@ int launch_pipe(const GemmParams& p0, int64_t batch, hipStream_t stream) {
 }
 
 // Packed B with N % 32 == 0: the LDS-DMA pipeline (16-byte DMAs for A rows
-// that are 16-byte aligned, 4-byte DMAs otherwise).
+// that are 16-byte aligned, 4-byte DMAs otherwise), 32 k per stage, 4 stages
+// (3 for 128x128 tiles over unaligned A rows, measured faster there).
 // Largest tile that still gives every CU (256 on MI355X) a workgroup.
 int launch_packed_pipe(const GemmParams& p, int64_t batch, hipStream_t stream) {
   const int64_t cus = 256;
   auto tiles = [&](int bm, int bn) {
     return ((int64_t)(p.m + bm - 1) / bm) * ((p.n + bn - 1) / bn) * batch;
   };
-  // An even number of full k-blocks streams 64 k per stage (half the
-  // barriers); an odd one 32.
-  const bool k64 = ((p.k >> 5) & 1) == 0;
   if (tiles(128, 128) >= cus)
-    return k64 ? launch_pipe<4, 2, 1, 2, 2, 1, 1, 2>(p, batch, stream)
-               : launch_pipe<4, 2, 1, 2, 3, 1, 1, 1>(p, batch, stream);
-  if (tiles(128, 64) >= cus)
-    return k64 ? launch_pipe<4, 2, 1, 1, 2, 2, 1, 2>(p, batch, stream)
-               : launch_pipe<4, 2, 1, 1, 3, 2, 1, 1>(p, batch, stream);
+    return p.a_vec ? launch_pipe<4, 2, 1, 2, 4, 1, 1, 1>(p, batch, stream)
+                   : launch_pipe<4, 2, 1, 2, 3, 1, 1, 1>(p, batch, stream);
+  if (tiles(128, 64) >= cus) return launch_pipe<4, 2, 1, 1, 4, 2, 1, 1>(p, batch, stream);
   // 64x64 tiles leave one wave per SIMD; split each k-block over two wave
   // groups so every SIMD runs two
-  return k64 ? launch_pipe<2, 2, 1, 1, 2, 2, 2, 2>(p, batch, stream)
-             : launch_pipe<2, 2, 1, 1, 2, 1, 2, 1>(p, batch, stream);
+  return launch_pipe<2, 2, 1, 1, 4, 1, 2, 1>(p, batch, stream);
 }
 
 template <int W>

@@ -127,7 +127,7 @@ def bench_tower(args, device):
     k1_flops = 2.0 * m * n * k
     achieved = k1_flops / (k1_ms * 1e-3) / 1e12
     roofline = {
-        "kernel": "gemm_packed_pipe_kernel<4,2,1,1,2,2,1,2,true> (layer 1: 4096x512x1024 packed B + bias + ReLU)",
+        "kernel": "gemm_packed_pipe_kernel<4,2,1,1,4,2,1,1,true> (layer 1: 4096x512x1024 packed B + bias + ReLU)",
         "bound": "mfma",
         "achieved": round(achieved, 3),
         "peak": FP32_MFMA_PEAK_TFLOPS,
@@ -294,6 +294,17 @@ def cpu_cores() -> int:
     return max(1, min(n, int(os.environ.get("OMP_NUM_THREADS", n))))
 
 
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(inputs, bag_inputs):
     """Oracle (OpenBLAS 0.3.29 sgemm + loops) on the host: the whole config-2
     tower at batch 4096, median of 5 after one warm-up, 1 thread and all cores."""
@@ -316,7 +327,8 @@ def cpu_baseline(inputs, bag_inputs):
     out = {"value": round(res[cores], 4), "unit": "TFLOP/s", "cores": cores, "kind": "port",
            "sample": "full configs[1] tower (batch 4096, 5.37 GFLOP) x5 reps, median; "
                      "OpenBLAS 0.3.29 sgemm + bias/ReLU/sigmoid loops",
-           "single_thread_value": round(res[1], 4), "blas": ora.blas_config()}
+           "single_thread_value": round(res[1], 4), "blas": ora.blas_config(),
+           "cpu_model": cpu_model(), "affinity_cpus": len(os.sched_getaffinity(0))}
     if bag_inputs is not None:
         w = bag_inputs
         bags, dim = w.offsets.size - 1, w.table.shape[1]
