@@ -1,8 +1,12 @@
-"""annc-opt: the offline model rewriter, `layout_matmul` pass.
+"""annc-opt: the offline model rewriter: the `layout_matmul` pass and the
+hash-bucket embedding passes `embed_hash_bucket` / `lookup_embedding_hash`.
 
 Command line, as python/annc/main.py:14-68 (`annc-opt -I <in> -O <out> passes...`):
 
-    python -m annc_amd.annc_opt -I <input model dir> -O <output model dir> layout_matmul
+    python -m annc_amd.annc_opt -I <input model dir> -O <output model dir> \
+        embed_hash_bucket layout_matmul
+
+Passes run in the order given, except that layout_matmul always runs last.
 
 The reference rewrites a TensorFlow SavedModel.  TensorFlow is not part of
 this build, so a model here is a directory holding
@@ -23,6 +27,16 @@ is this library's MFMA-fragment format (`annc_layout_matmul_rhs_format()`,
 reference is never read as the new format by mistake.  Like the reference,
 the pass always runs last.
 
+`embed_hash_bucket` (rec_embedding.py:490-785) replaces each TF feature-column
+subgraph of an embedding_column over a hash-bucket categorical column (the
+SparseFillEmptyRows / Unique / gather / SparseSegmentSum-or-Mean chain, about
+45 nodes) by one KPFusedEmbeddingWithHashBucket node with inputs (the string
+tensor, the embedding weight) and attrs num_buckets, combiner (0 sum, 1 mean)
+and T_weight.  `lookup_embedding_hash` emits KPLookupEmbeddingByHash for the
+same subgraph.  The other pattern passes of the reference (dnn_sparse,
+dnn_hash_bucket, embed, linear_sparse, softmax) emit ops outside this
+library and are refused.
+
 Differences from the reference, each deliberate:
   * lhs variables are not packed: the reference's "k4m4" lhs packing has no
     consumer (no custom call reads a packed lhs); the reference's rule that a
@@ -36,6 +50,11 @@ Differences from the reference, each deliberate:
   * weights already packed by the reference (`rhs_format: "kn4"`) are
     converted: unpacked with the kn4 order (data_pack.py:24-149, restated in
     `kn4_permutation`) and re-packed into the MFMA format.
+  * an embedding subgraph is fused only if nothing outside it reads a node
+    the rewrite removes; the reference removes them regardless, leaving
+    dangling inputs.  Users are taken from the graph as it stands before
+    each match, and every SparseFillEmptyRows is visited (the reference
+    walks its node list while editing it).
 """
 from __future__ import annotations
 
@@ -56,10 +75,10 @@ REF_RHS_FORMAT = "kn4"
 MATMUL_OPS = frozenset(["MatMul", "BatchMatMul", "BatchMatMulV2", "BatchMatMulV3"])
 PASS_THROUGH_OPS = frozenset(["Identity", "ReadVariableOp"])
 VARIABLE_OPS = frozenset(["VarHandleOp", "VariableV2", "Variable"])
-# TensorFlow graph pattern rewrites of the reference (rec_embedding.py); they
-# match TF subgraphs that this build's model format does not describe
-TF_PATTERN_PASSES = ("lookup_embedding_hash", "dnn_sparse", "dnn_hash_bucket", "embed",
-                     "embed_hash_bucket", "linear_sparse", "softmax")
+# Pattern passes of the reference (rec_embedding.py) this build implements,
+# and the ones it does not (their fused ops are not part of this library)
+EMBEDDING_PASSES = ("embed_hash_bucket", "lookup_embedding_hash")
+UNSUPPORTED_PASSES = ("dnn_sparse", "dnn_hash_bucket", "embed", "linear_sparse", "softmax")
 
 
 def mfma_rhs_format() -> str:
@@ -254,20 +273,246 @@ def layout_matmul(model: Model) -> List[str]:
     return done
 
 
+# ---------------------------------------------------------------------------
+# embed_hash_bucket / lookup_embedding_hash
+# ---------------------------------------------------------------------------
+# The TF feature-column lowering of embedding_column(categorical_column_with_
+# hash_bucket(...)) that EmbeddingWithHashBucketPatternRewriter
+# (rec_embedding.py:490-785) replaces by one fused op.  A pattern is a list of
+# steps over named pattern variables, anchored at the SparseFillEmptyRows
+# node "sfer":
+#   ("in",  v, [(op, w), ...], count)  operands of v, by position
+#   ("out", v, [(op, w), ...], count)  users of v, in graph order
+# Entry i must have type `op` (None: any).  `w` names the variable it is: a
+# new name binds it, a bound name must be the same node, None checks the type
+# only.  `count` (or None) is the exact number of operands / users.
+_SEGMENT_SUM_PATTERN = [
+    ("in", "sfer", [("GatherV2", "g0"), ("GatherV2", "g1"), ("Identity", "id0")], None),
+    ("in", "g0", [("SparseReshape", "sr0"), ("Reshape", "rs0")], None),
+    ("in", "g1", [("Identity", "id1"), ("Reshape", "rs0")], None),
+    ("in", "id0", [("SparseReshape", "sr0")], None),
+    ("in", "rs0", [("Where", "wh0")], None),
+    ("in", "wh0", [("GreaterEqual", "ge0")], None),
+    ("in", "ge0", [("Identity", "id1")], None),
+    ("in", "id1", [("Identity", "id2")], None),
+    ("in", "id2", [("StringToHashBucketFast", "hash")], None),
+    ("in", "sr0", [("SparseReshape", "sr1"), ("SparseReshape", None), ("Pack", "pk0")], None),
+    ("in", "pk0", [("Prod", "pr0"), ("GatherV2", "g2")], None),
+    ("in", "pr0", [("Slice", "sl0")], None),
+    ("in", "sl0", [("SparseReshape", "sr1")], None),
+    ("in", "g2", [("SparseReshape", "sr1")], None),
+    ("in", "sr1", [("Where", "wh1"), ("Shape", "sh0"), ("Cast", "c0")], None),
+    ("in", "c0", [("Pack", "pk1")], None),
+    ("in", "pk1", [("StridedSlice", "ss0")], None),
+    ("in", "ss0", [(None, "c1")], None),
+    ("in", "c1", [("Shape", "sh0")], None),
+    ("in", "wh1", [("NotEqual", "ne")], None),
+    ("in", "ne", [("ExpandDims", "ed")], None),
+    ("in", "hash", [("GatherNd", "gnd")], None),
+    ("in", "gnd", [("ExpandDims", "ed"), ("Where", "wh1")], None),
+    ("out", "sfer", [("StridedSlice", "ss1"), ("Unique", "uq"), ("Reshape", "rs1")], 3),
+    ("out", "uq", [("ResourceGather", "gather"), ("SparseSegmentSum", "seg")], 2),
+    ("out", "gather", [("Identity", "id3")], None),
+    ("out", "id3", [("Identity", "id4")], None),
+    ("out", "id4", [("SparseSegmentSum", "seg")], None),
+    ("out", "ss1", [("Cast", "c2")], None),
+    ("out", "c2", [("SparseSegmentSum", "seg")], None),
+    ("out", "seg", [("Shape", "sh1"), ("ZerosLike", "zl"), ("Select", "sel")], None),
+    ("out", "sh1", [("StridedSlice", "ss2")], None),
+    ("out", "ss2", [("Pack", "pk2")], None),
+    ("out", "pk2", [("Tile", "tl")], None),
+    ("out", "rs1", [("Tile", "tl")], None),
+    ("out", "tl", [("Select", "sel")], None),
+    ("out", "zl", [("Select", "sel")], None),
+    ("out", "sel", [("Shape", "sh2"), ("Reshape", "result")], None),
+    ("out", "sh2", [("Slice", "sl1")], None),
+    ("out", "sl1", [("ConcatV2", "cc")], None),
+    ("out", "sr1", [("Slice", None), ("GatherV2", None), ("SparseReshape", None),
+                    ("SparseReshape", None), ("Cast", "c3")], None),
+    ("out", "c3", [("Slice", "sl2")], None),
+    ("out", "sl2", [("ConcatV2", "cc")], None),
+    ("out", "cc", [("Reshape", "result")], None),
+]
+
+_SEGMENT_MEAN_PATTERN = [
+    ("in", "sfer", [("GatherV2", "g0"), ("GatherV2", "g1"), ("Identity", "id0")], None),
+    ("in", "g0", [("SparseReshape", "sr0"), ("Reshape", "rs0")], None),
+    ("in", "g1", [("Identity", "id1"), ("Reshape", "rs0")], None),
+    ("in", "id0", [("SparseReshape", "sr0")], None),
+    ("in", "rs0", [("Where", "wh0")], None),
+    ("in", "wh0", [("GreaterEqual", "ge0")], None),
+    ("in", "ge0", [("Identity", "id1")], None),
+    ("in", "id1", [("StringToHashBucketFast", "hash")], None),
+    ("in", "sr0", [("Where", "wh1"), ("Shape", "sh0"), ("Pack", "pk0")], None),
+    ("in", "pk0", [("Prod", "pr0"), ("GatherV2", "g2")], None),
+    ("in", "pr0", [("Slice", "sl0")], None),
+    ("in", "sl0", [("Shape", "sh0")], None),
+    ("in", "g2", [("Shape", "sh0")], None),
+    ("in", "sh0", [("ExpandDims", "ed")], None),
+    ("in", "hash", [("GatherNd", "gnd")], None),
+    ("in", "gnd", [("ExpandDims", "ed"), ("Where", "wh1")], None),
+    ("in", "wh1", [("NotEqual", "ne")], None),
+    ("in", "ne", [("ExpandDims", "ed")], None),
+    ("out", "sfer", [("StridedSlice", "ss1"), ("Unique", "uq"), ("Reshape", "rs1")], 3),
+    ("out", "uq", [("GatherV2", "gather"), ("SparseSegmentMean", "seg")], None),
+    ("out", "gather", [("Identity", "id3")], None),
+    ("out", "id3", [("SparseSegmentMean", "seg")], None),
+    ("out", "ss1", [("Cast", "c2")], None),
+    ("out", "c2", [("SparseSegmentMean", "seg")], None),
+    ("out", "seg", [("Shape", "sh1"), ("ZerosLike", "zl"), ("Select", "sel")], None),
+    ("out", "sh1", [("StridedSlice", "ss2")], None),
+    ("out", "ss2", [("Pack", "pk1")], None),
+    ("out", "pk1", [("Tile", "tl")], None),
+    ("out", "rs1", [("Tile", "tl")], None),
+    ("out", "tl", [("Select", "sel")], None),
+    ("out", "zl", [("Select", "sel")], None),
+    ("out", "sel", [("Shape", "sh2"), ("Reshape", "rs2")], None),
+    ("out", "sh2", [("Slice", "sl1")], None),
+    ("out", "sl1", [("ConcatV2", "cc")], None),
+    ("out", "sh0", [("Slice", None), ("GatherV2", None), ("SparseReshape", None),
+                    ("Cast", "c3")], None),
+    ("out", "c3", [("Slice", "sl2")], None),
+    ("out", "sl2", [("ConcatV2", "cc")], None),
+    ("out", "cc", [("Reshape", "rs2")], None),
+    ("out", "rs2", [("Shape", "sh3"), ("Reshape", "result")], None),
+    ("out", "sh3", [("StridedSlice", "ss3")], None),
+    ("out", "ss3", [("Pack", "pk2")], None),
+    ("out", "pk2", [("Reshape", "result")], None),
+]
+
+# pass -> (fused op type, name suffix); rec_embedding.py:490-492, 787-789
+_EMBEDDING_FUSED_OPS = {
+    "embed_hash_bucket": ("KPFusedEmbeddingWithHashBucket", "/rec_embed_kp_bucket"),
+    "lookup_embedding_hash": ("KPLookupEmbeddingByHash", "/rec_embed_kp_hash"),
+}
+
+
+def _input_node(inp: str) -> str:
+    return inp.split(":")[0]
+
+
+class _GraphIndex:
+    """Data operands (node, output index) and users of every node; a user
+    appears once per data input it takes from the node, in graph order, and
+    control inputs ("^name") are neither."""
+
+    def __init__(self, model: Model):
+        self.by_name = {n.name: n for n in model.nodes}
+        self.users: Dict[str, List[Node]] = {n.name: [] for n in model.nodes}
+        for n in model.nodes:
+            for inp in n.inputs:
+                if not inp.startswith("^") and _input_node(inp) in self.users:
+                    self.users[_input_node(inp)].append(n)
+
+    def operands(self, node: Node) -> List[Optional[Node]]:
+        return [self.by_name.get(_input_node(i)) for i in node.inputs if not i.startswith("^")]
+
+
+def _match(index: _GraphIndex, anchor: Node, pattern) -> Optional[Dict[str, Node]]:
+    bound = {"sfer": anchor}
+    for kind, var, entries, count in pattern:
+        node = bound[var]
+        seq = index.operands(node) if kind == "in" else index.users[node.name]
+        if count is not None and len(seq) != count:
+            return None
+        if len(entries) > len(seq):
+            return None
+        for (op, name), cand in zip(entries, seq):
+            if cand is None or (op is not None and cand.op != op):
+                return None
+            if name is None:
+                continue
+            if name in bound:
+                if bound[name] is not cand:
+                    return None
+            else:
+                bound[name] = cand
+    return bound
+
+
+def _rewrite_embedding(model: Model, anchor: Node, bound: Dict[str, Node], mean: bool,
+                       op: str, suffix: str) -> Node:
+    """Replace the matched subgraph by one fused node: inputs (the string
+    tensor ExpandDims reads, the embedding weight the gather reads); attrs
+    the hash node's (num_buckets), combiner 0 / T_weight resource for
+    SparseSegmentSum, combiner 1 / T_weight float for SparseSegmentMean
+    (rec_embedding.py:614-621, 749-756)."""
+    ed, gather, result, hash_node = bound["ed"], bound["gather"], bound["result"], bound["hash"]
+    attrs = {k: v for k, v in hash_node.attrs.items() if k != "_output_shapes"}
+    attrs["combiner"] = 1 if mean else 0
+    attrs["T_weight"] = "DT_FLOAT" if mean else "DT_RESOURCE"
+    if "_output_shapes" in result.attrs:
+        attrs["_output_shapes"] = result.attrs["_output_shapes"]
+    fused = Node(anchor.name + suffix, op, [ed.inputs[0], gather.inputs[0]], attrs)
+    gone = {n.name for n in bound.values()}
+    for n in model.nodes:
+        if n.name in gone:
+            continue
+        for i, inp in enumerate(n.inputs):
+            if inp in (result.name, result.name + ":0"):
+                n.inputs[i] = fused.name
+            elif inp == "^" + result.name:
+                n.inputs[i] = "^" + fused.name
+    at = model.nodes.index(anchor)
+    model.nodes.insert(at + 1, fused)
+    model.nodes[:] = [n for n in model.nodes if n.name not in gone]
+    return fused
+
+
+def embedding_with_hash_bucket(model: Model, pass_name: str = "embed_hash_bucket") -> List[str]:
+    """EmbeddingWithHashBucketPatternRewriter / LookupEmbeddingWithHash-
+    PatternRewriter (rec_embedding.py:490-792): every SparseFillEmptyRows at
+    the centre of a hash-bucket embedding_column subgraph (segment sum or
+    segment mean) becomes one fused node.  Returns the fused node names.
+
+    A match is rewritten only when no node outside it reads a node it
+    removes (other than through the result, which the fused node replaces);
+    the reference removes the nodes regardless."""
+    op, suffix = _EMBEDDING_FUSED_OPS[pass_name]
+    made: List[str] = []
+    anchors = [n.name for n in model.nodes if n.op == "SparseFillEmptyRows"]
+    for name in anchors:
+        index = _GraphIndex(model)
+        anchor = index.by_name.get(name)
+        if anchor is None:
+            continue
+        mean = False
+        bound = _match(index, anchor, _SEGMENT_SUM_PATTERN)
+        if bound is None:
+            bound = _match(index, anchor, _SEGMENT_MEAN_PATTERN)
+            mean = True
+        if bound is None:
+            continue
+        gone = {n.name for n in bound.values()}
+        inner = gone - {bound["result"].name}
+        escapes = any(u.name not in gone for v in inner for u in index.users[v])
+        escapes = escapes or any(i.startswith("^") and i[1:] in inner
+                                 for n in model.nodes if n.name not in gone for i in n.inputs)
+        if escapes:
+            continue
+        made.append(_rewrite_embedding(model, anchor, bound, mean, op, suffix).name)
+    return made
+
+
 def optimize(input_path: str, output_path: str, passes: Sequence[str]) -> List[str]:
-    """main.opt (main.py:43-68): load, run the passes (layout_matmul last),
-    save.  Returns the variables layout_matmul packed."""
+    """main.opt (main.py:43-68): load, run the passes in the order given with
+    layout_matmul moved last, save.  Returns the variables layout_matmul
+    packed."""
     passes = list(passes)
     for p in passes:
-        if p in TF_PATTERN_PASSES:
-            raise TypeError(f"Pass '{p}' rewrites TensorFlow subgraphs; this build's model "
-                            f"format carries the fused ops directly")
-        if p != "layout_matmul":
+        if p in UNSUPPORTED_PASSES:
+            raise TypeError(f"Pass '{p}' emits a fused op this build does not implement")
+        if p != "layout_matmul" and p not in EMBEDDING_PASSES:
             raise TypeError(f"Pass '{p}' not found")
+    if "layout_matmul" in passes:
+        passes = [p for p in passes if p != "layout_matmul"] + ["layout_matmul"]
     model = load_model(input_path)
     packed: List[str] = []
-    if "layout_matmul" in passes:
-        packed = layout_matmul(model)
+    for p in passes:
+        if p == "layout_matmul":
+            packed = layout_matmul(model)
+        else:
+            embedding_with_hash_bucket(model, p)
     save_model(model, output_path, source=input_path)
     return packed
 
@@ -277,9 +522,8 @@ def parse_args(argv=None):
     parser.add_argument("-I", "--input", required=True, help="Input model path")
     parser.add_argument("-O", "--output", required=True, help="Output model path")
     parser.add_argument("passes", nargs="+",
-                        help="opt: 'layout_matmul' (the TF pattern passes "
-                             + ", ".join(repr(p) for p in TF_PATTERN_PASSES)
-                             + " apply to TensorFlow graphs only)")
+                        help="opt: " + ", ".join(repr(p) for p in EMBEDDING_PASSES)
+                             + ", 'layout_matmul'")
     return parser.parse_args(argv)
 
 
