@@ -95,6 +95,14 @@ PIPE_CASES = [
     (33, 160, 64, 64, "2 k-blocks"),
     (130, 64, 96, 100, "3 k-blocks (one full pipeline round), lda not a multiple of 32"),
     (7, 64, 300, 300, "tiny M"),
+    # few k-blocks in each tile class: the prologue and the mid-stage waits
+    # of the 4-stage (3-stage for unaligned 128x128) pipeline
+    (4096, 1024, 40, 40, "128x128 tiles, 1 k-block + tail"),
+    (4096, 1024, 97, 97, "128x128 tiles, unaligned A, 3 k-blocks + tail (3 stages)"),
+    (4096, 1024, 128, 128, "128x128 tiles, 4 k-blocks"),
+    (4096, 512, 160, 160, "128x64 tiles, 5 k-blocks"),
+    (4096, 512, 64, 67, "128x64 tiles, 2 k-blocks, unaligned A"),
+    (4096, 256, 224, 224, "64x64 split-K tiles, 7 k-blocks"),
 ]
 
 
