@@ -486,7 +486,7 @@ __global__ __launch_bounds__(64 * W) void gemm_small_kernel(GemmParams p) {
 // (global_load_lds_dwordx4: lane i of a wave writes bytes [16i, 16i+16) of a
 // 1 KiB LDS block), S stages deep, so no VGPRs stage the data and up to S-2
 // stages are in flight while the MFMAs run on the oldest.  A stage holds
-// KSUB consecutive 32-k blocks.  One barrier per stage, halfway through it:
+// one 32-k block.  One barrier per stage, halfway through it:
 // a wave waits for its own DMAs of the next stage (vmcnt), the barrier
 // publishes everyone's, and the slot of the previous stage is refilled.  The
 // next stage's first fragments are then read under the current stage's last
@@ -550,11 +550,10 @@ __device__ __forceinline__ int a_swizzle(int row) { return (row & 7) ^ ((row >> 
 
 }  // namespace pipe
 
-template <int WM, int WN, int BLK_M, int BLK_N, int S, int NACC, int KS, int KSUB, bool A16>
+template <int WM, int WN, int BLK_M, int BLK_N, int S, int NACC, int KS, bool A16>
 __global__ __launch_bounds__(64 * WM * WN * KS) void gemm_packed_pipe_kernel(GemmParams p) {
   static_assert(NACC == 1 || NACC == 2, "one or two accumulator chains");
   static_assert(KS == 1 || KS == 2, "one or two k groups");
-  static_assert(KSUB == 1 || KSUB == 2, "one or two 32-k blocks per stage");
   constexpr int NT = WM * WN;                      // waves per k group
   constexpr int NW = NT * KS;
   constexpr int NQ = 4 / KS;                       // 8-k quads per wave per k-block
@@ -562,16 +561,15 @@ __global__ __launch_bounds__(64 * WM * WN * KS) void gemm_packed_pipe_kernel(Gem
   constexpr int NA = BM / 8, NB = BN / 8, NBLK = NA + NB;  // 1 KiB blocks per stage
   static_assert(NBLK % NW == 0, "stage blocks split evenly over the waves");
   static_assert(S >= 3 && S <= 4, "3 or 4 stages: the next stage is published mid-stage");
-  static_assert(KS == 1 || NT * 2 * BLK_M * BLK_N * 2 <= S * KSUB * NBLK, "exchange fits in LDS");
+  static_assert(KS == 1 || NT * 2 * BLK_M * BLK_N * 2 <= S * NBLK, "exchange fits in LDS");
   constexpr int LPW = NBLK / NW;                    // 1 KiB blocks per wave per k-block
   // A rows that are not 16-byte aligned load each A block with four 4-byte
   // DMAs (two rows each); the first LPA blocks of every wave are A blocks.
   static_assert(A16 || NA % NW == 0, "A blocks split evenly over the waves");
   constexpr int LPA = NA / NW;
   constexpr int DMAS = A16 ? LPW : LPW + 3 * LPA;  // DMA instructions per wave per k-block
-  constexpr uint32_t kSubBytes = NBLK * 1024;
-  constexpr uint32_t kStageBytes = KSUB * kSubBytes;
-  __shared__ __attribute__((aligned(1024))) f32x4 lds[S][KSUB * NBLK * 64];
+  constexpr uint32_t kStageBytes = NBLK * 1024;
+  __shared__ __attribute__((aligned(1024))) f32x4 lds[S][NBLK * 64];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -593,7 +591,7 @@ __global__ __launch_bounds__(64 * WM * WN * KS) void gemm_packed_pipe_kernel(Gem
   const float* __restrict__ B = p.b + z * p.stride_b;
   const int M = p.m, N = p.n, K = p.k;
   const int KT = K >> 5;          // full k-blocks
-  const int KB = KT / KSUB;       // stages (KT % KSUB == 0 on this path)
+  const int KB = KT;              // stages
   const int panels = N >> 5;      // N % 32 == 0 on this path
 
   // bias of this lane's columns, fetched before the pipeline starts
@@ -645,20 +643,17 @@ __global__ __launch_bounds__(64 * WM * WN * KS) void gemm_packed_pipe_kernel(Gem
   }
   auto issue = [&](int slot, int kb) {
 #pragma unroll
-    for (int sub = 0; sub < KSUB; ++sub)
+    for (int i = 0; i < LPW; ++i) {
+      if (!A16 && i < LPA) {
 #pragma unroll
-      for (int i = 0; i < LPW; ++i) {
-        if (!A16 && i < LPA) {
-#pragma unroll
-          for (int j = 0; j < 4; ++j)
-            pipe::dma4(src4[A16 ? 0 : i][j] + (int64_t)(kb * KSUB + sub) * 32,
-                       dst[i] + slot * kStageBytes + sub * kSubBytes + 256 * j);
-        } else {
-          pipe::dma16(src[i] + (int64_t)(kb * KSUB + sub) * step[i],
-                      dst[i] + slot * kStageBytes + sub * kSubBytes);
-        }
+        for (int j = 0; j < 4; ++j)
+          pipe::dma4(src4[A16 ? 0 : i][j] + (int64_t)kb * 32, dst[i] + slot * kStageBytes + 256 * j);
+      } else {
+        pipe::dma16(src[i] + (int64_t)kb * step[i], dst[i] + slot * kStageBytes);
       }
+    }
   };
+
 
   // fragment addressing (f32x4 units inside a stage)
   const int q0 = kg * NQ;
@@ -692,23 +687,23 @@ __global__ __launch_bounds__(64 * WM * WN * KS) void gemm_packed_pipe_kernel(Gem
     // published half a stage before it is needed, and the fragments of its
     // first quad are read during the last MFMAs of stage kb: the MFMA pipes
     // see no barrier or LDS-latency gap at the stage boundary.
-    constexpr int QPS = KSUB * NQ;  // 8-k quads per wave per stage (even)
+    constexpr int QPS = NQ;  // 8-k quads per wave per stage (4, or 2 with two k groups)
     constexpr int HALF = QPS / 2;
     f32x4 af[2][BLK_M], bf[2][BLK_N];
     auto frag_at = [&](const f32x4* stage, int t, int buf) {
-      const f32x4* cur = stage + (t / NQ) * NBLK * 64;
-      const int q = q0 + t % NQ;
+      const int q = q0 + t;
 #pragma unroll
-      for (int i = 0; i < BLK_M; ++i) af[buf][i] = cur[a_off[i] + ((4 * half + q) ^ a_swz[i])];
+      for (int i = 0; i < BLK_M; ++i) af[buf][i] = stage[a_off[i] + ((4 * half + q) ^ a_swz[i])];
 #pragma unroll
-      for (int j = 0; j < BLK_N; ++j) bf[buf][j] = cur[(NA + (wn * BLK_N + j) * 4 + q) * 64 + lane];
+      for (int j = 0; j < BLK_N; ++j)
+        bf[buf][j] = stage[(NA + (wn * BLK_N + j) * 4 + q) * 64 + lane];
     };
     if (KB > 0) {
       const int inflight = min(KB - 1, S - 2);  // stages 1 .. S-2 may stay in flight
       if (inflight >= 2)
-        pipe::wait_vmcnt<2 * KSUB * DMAS>();
+        pipe::wait_vmcnt<2 * DMAS>();
       else if (inflight == 1)
-        pipe::wait_vmcnt<KSUB * DMAS>();
+        pipe::wait_vmcnt<DMAS>();
       else
         pipe::wait_vmcnt<0>();
       pipe::barrier_only();
@@ -747,7 +742,7 @@ __global__ __launch_bounds__(64 * WM * WN * KS) void gemm_packed_pipe_kernel(Gem
             if (t == HALF - 1 && kb + 1 < KB) {
               // stages kb+2 .. kb+S-2 may stay in flight (S <= 4: at most one)
               if (S >= 4 && kb + 2 < KB)
-                pipe::wait_vmcnt<KSUB * DMAS>();
+                pipe::wait_vmcnt<DMAS>();
               else
                 pipe::wait_vmcnt<0>();
               pipe::barrier_only();
@@ -945,7 +940,7 @@ int launch_tile(const GemmParams& p0, int64_t batch, hipStream_t stream) {
   return ANNC_OK;
 }
 
-template <int WM, int WN, int BMB, int BNB, int S, int NACC, int KS, int KSUB = 1>
+template <int WM, int WN, int BMB, int BNB, int S, int NACC, int KS>
 int launch_pipe(const GemmParams& p0, int64_t batch, hipStream_t stream) {
   constexpr int BM = WM * BMB * 32, BN = WN * BNB * 32;
   GemmParams p = p0;
@@ -953,10 +948,10 @@ int launch_pipe(const GemmParams& p0, int64_t batch, hipStream_t stream) {
   p.tiles_n = (p.n + BN - 1) / BN;
   dim3 grid(p.tiles_m * p.tiles_n, 1, (unsigned)batch);
   if (p.a_vec)
-    hipLaunchKernelGGL((gemm_packed_pipe_kernel<WM, WN, BMB, BNB, S, NACC, KS, KSUB, true>),
+    hipLaunchKernelGGL((gemm_packed_pipe_kernel<WM, WN, BMB, BNB, S, NACC, KS, true>),
                        grid, dim3(64 * WM * WN * KS), 0, stream, p);
   else
-    hipLaunchKernelGGL((gemm_packed_pipe_kernel<WM, WN, BMB, BNB, S, NACC, KS, KSUB, false>),
+    hipLaunchKernelGGL((gemm_packed_pipe_kernel<WM, WN, BMB, BNB, S, NACC, KS, false>),
                        grid, dim3(64 * WM * WN * KS), 0, stream, p);
   ANNC_HIP_TRY(hipGetLastError());
   return ANNC_OK;
@@ -972,12 +967,12 @@ int launch_packed_pipe(const GemmParams& p, int64_t batch, hipStream_t stream) {
     return ((int64_t)(p.m + bm - 1) / bm) * ((p.n + bn - 1) / bn) * batch;
   };
   if (tiles(128, 128) >= cus)
-    return p.a_vec ? launch_pipe<4, 2, 1, 2, 4, 1, 1, 1>(p, batch, stream)
-                   : launch_pipe<4, 2, 1, 2, 3, 1, 1, 1>(p, batch, stream);
-  if (tiles(128, 64) >= cus) return launch_pipe<4, 2, 1, 1, 4, 2, 1, 1>(p, batch, stream);
+    return p.a_vec ? launch_pipe<4, 2, 1, 2, 4, 1, 1>(p, batch, stream)
+                   : launch_pipe<4, 2, 1, 2, 3, 1, 1>(p, batch, stream);
+  if (tiles(128, 64) >= cus) return launch_pipe<4, 2, 1, 1, 4, 2, 1>(p, batch, stream);
   // 64x64 tiles leave one wave per SIMD; split each k-block over two wave
   // groups so every SIMD runs two
-  return launch_pipe<2, 2, 1, 1, 4, 1, 2, 1>(p, batch, stream);
+  return launch_pipe<2, 2, 1, 1, 4, 1, 2>(p, batch, stream);
 }
 
 template <int W>

@@ -127,7 +127,7 @@ def bench_tower(args, device):
     k1_flops = 2.0 * m * n * k
     achieved = k1_flops / (k1_ms * 1e-3) / 1e12
     roofline = {
-        "kernel": "gemm_packed_pipe_kernel<4,2,1,1,4,2,1,1,true> (layer 1: 4096x512x1024 packed B + bias + ReLU)",
+        "kernel": "gemm_packed_pipe_kernel<4,2,1,1,4,2,1,true> (layer 1: 4096x512x1024 packed B + bias + ReLU)",
         "bound": "mfma",
         "achieved": round(achieved, 3),
         "peak": FP32_MFMA_PEAK_TFLOPS,
