@@ -297,29 +297,178 @@ __global__ void init_scan_kernel(long long* minmax, int* unsorted) {
   *unsorted = 0;
 }
 
-// offsets[s] = first position whose segment id is >= s, for s in [0, batch];
-// the segment ids read through `seg` (stride) must be non-decreasing.
+// offsets[s] = first position whose segment id is >= s, for s in [0, batch],
+// from non-decreasing segment ids: position i fills the s in
+// (seg[i-1], seg[i]] (ids clamped to [-1, batch]; i = n closes the range).
 template <typename KeyT>
-__global__ void lower_bound_kernel(const KeyT* __restrict__ seg, int64_t stride, int64_t n,
-                                   int64_t batch, int64_t* __restrict__ offsets) {
-  const int64_t s = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (s > batch) return;
-  int64_t lo = 0, hi = n;
-  while (lo < hi) {
-    const int64_t mid = (lo + hi) >> 1;
-    if (static_cast<int64_t>(seg[mid * stride]) < s)
-      lo = mid + 1;
-    else
-      hi = mid;
-  }
-  offsets[s] = lo;
+__global__ void seg_bounds_kernel(const KeyT* __restrict__ seg, int64_t stride, int64_t n,
+                                  int64_t batch, int64_t* __restrict__ offsets) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i > n) return;
+  auto key = [&](int64_t j) {
+    const int64_t v = static_cast<int64_t>(seg[j * stride]);
+    return v < -1 ? int64_t(-1) : (v > batch ? batch : v);
+  };
+  const int64_t prev = i == 0 ? int64_t(-1) : key(i - 1);
+  const int64_t cur = i == n ? batch : key(i);
+  for (int64_t s = prev + 1; s <= cur; ++s) offsets[s] = i;
 }
 
+// ---------------------------------------------------------------------------
+// Stable counting sort of positions by segment id, for segment ids below
+// kCsMaxSegments (the per-block counters live in LDS).  Positions are cut
+// into blocks of kCsBlock:
+//   1. cs_hist:    H[b][s] = positions of block b in segment s
+//   2. cs_prefix:  P[b][s] = positions of segment s in blocks before b,
+//                  total[s]
+//   3. cs_offsets: offsets = exclusive scan of total (one workgroup)
+//   4. cs_scatter: one wave per block walks its positions in order, 64 at a
+//                  time; lanes holding the same segment rank themselves by
+//                  lane order (ballots over the id bits), so each segment's
+//                  positions land in increasing order: perm is stable.
+// Segment ids outside [0, batch) are left out, as the sort path leaves them
+// past offsets[batch].
+// ---------------------------------------------------------------------------
+constexpr int kCsBlock = 1024;
+constexpr int64_t kCsMaxSegments = 16384;
+constexpr int kCsBits = 14;  // bits of a segment id below kCsMaxSegments
+
+__global__ __launch_bounds__(kThreads) void cs_hist_kernel(const int64_t* __restrict__ seg,
+                                                          int64_t stride, int64_t n, int batch,
+                                                          uint32_t* __restrict__ H) {
+  extern __shared__ uint32_t cs_lds[];
+  for (int s = threadIdx.x; s < batch; s += kThreads) cs_lds[s] = 0;
+  __syncthreads();
+  const int64_t b0 = (int64_t)blockIdx.x * kCsBlock;
+  for (int t = threadIdx.x; t < kCsBlock; t += kThreads) {
+    const int64_t i = b0 + t;
+    if (i < n) {
+      const int64_t s = seg[i * stride];
+      if (s >= 0 && s < batch) atomicAdd(&cs_lds[s], 1u);
+    }
+  }
+  __syncthreads();
+  uint32_t* row = H + (int64_t)blockIdx.x * batch;
+  for (int s = threadIdx.x; s < batch; s += kThreads) row[s] = cs_lds[s];
+}
+
+__global__ __launch_bounds__(kThreads) void cs_prefix_kernel(const uint32_t* __restrict__ H,
+                                                            int batch, int nblk,
+                                                            uint32_t* __restrict__ P,
+                                                            uint32_t* __restrict__ total) {
+  const int s = blockIdx.x * kThreads + threadIdx.x;
+  if (s >= batch) return;
+  constexpr int U = 32;  // block counts in flight per segment
+  uint32_t run = 0;
+  int b = 0;
+  for (; b + U <= nblk; b += U) {
+    uint32_t c[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) c[u] = H[(int64_t)(b + u) * batch + s];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      P[(int64_t)(b + u) * batch + s] = run;
+      run += c[u];
+    }
+  }
+  for (; b < nblk; ++b) {
+    const uint32_t c = H[(int64_t)b * batch + s];
+    P[(int64_t)b * batch + s] = run;
+    run += c;
+  }
+  total[s] = run;
+}
+
+__global__ __launch_bounds__(1024) void cs_offsets_kernel(const uint32_t* __restrict__ total,
+                                                         int batch, int64_t* __restrict__ offsets) {
+  __shared__ int64_t part[1024];
+  const int per = (batch + 1023) / 1024;
+  const int s0 = threadIdx.x * per;
+  int64_t sum = 0;
+  for (int s = s0; s < s0 + per && s < batch; ++s) sum += total[s];
+  part[threadIdx.x] = sum;
+  __syncthreads();
+  for (int off = 1; off < 1024; off <<= 1) {  // inclusive Hillis-Steele scan
+    const int64_t v = threadIdx.x >= off ? part[threadIdx.x - off] : 0;
+    __syncthreads();
+    part[threadIdx.x] += v;
+    __syncthreads();
+  }
+  int64_t run = threadIdx.x == 0 ? 0 : part[threadIdx.x - 1];
+  for (int s = s0; s < s0 + per && s < batch; ++s) {
+    offsets[s] = run;
+    run += total[s];
+  }
+  if (threadIdx.x == 1023) offsets[batch] = part[1023];
+}
+
+__global__ __launch_bounds__(kThreads) void cs_scatter_kernel(const int64_t* __restrict__ seg,
+                                                             int64_t stride, int64_t n, int batch,
+                                                             const uint32_t* __restrict__ P,
+                                                             const int64_t* __restrict__ offsets,
+                                                             int32_t* __restrict__ perm) {
+  extern __shared__ uint32_t cs_lds[];  // next slot of each segment
+  const uint32_t* pre = P + (int64_t)blockIdx.x * batch;
+  constexpr int kInit = 16;  // cursor loads in flight per thread
+  for (int s0 = threadIdx.x; s0 < batch; s0 += kThreads * kInit) {
+    uint32_t v[kInit];
+#pragma unroll
+    for (int u = 0; u < kInit; ++u) {
+      const int s = s0 + u * kThreads;
+      v[u] = s < batch ? static_cast<uint32_t>(offsets[s]) + pre[s] : 0u;
+    }
+#pragma unroll
+    for (int u = 0; u < kInit; ++u) {
+      const int s = s0 + u * kThreads;
+      if (s < batch) cs_lds[s] = v[u];
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x >= 64) return;
+  // One wave walks the block in order.  LDS operations of a wave complete
+  // in program order, so each step sees the cursors the previous one left.
+  const int lane = threadIdx.x;
+  const uint64_t lt = (uint64_t(1) << lane) - 1;
+  const int64_t b0 = (int64_t)blockIdx.x * kCsBlock;
+  // every segment id of the block is fetched before the ordered walk
+  constexpr int T = kCsBlock / 64;
+  int64_t sv[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    const int64_t i = b0 + 64 * t + lane;
+    sv[t] = i < n ? seg[i * stride] : -1;
+  }
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    const int64_t i = b0 + 64 * t + lane;
+    const int64_t s = sv[t];
+    const bool ok = s >= 0 && s < batch;
+    uint64_t same = __ballot(ok);
+#pragma unroll
+    for (int bit = 0; bit < kCsBits; ++bit) {
+      const bool on = (s >> bit) & 1;
+      const uint64_t b = __ballot(on);
+      same &= on ? b : ~b;
+    }
+    const uint32_t rank = static_cast<uint32_t>(__popcll(same & lt));
+    const uint32_t cnt = static_cast<uint32_t>(__popcll(same));
+    const uint32_t base = ok ? cs_lds[s] : 0u;
+    if (ok) {
+      perm[base + rank] = static_cast<int32_t>(i);
+      if (rank + 1 == cnt) cs_lds[s] = base + cnt;
+    }
+  }
+}
+
+// Sort keys: the segment id, or `batch` for ids outside [0, batch), which
+// then sort after every kept position.
 __global__ void make_keys_kernel(const int64_t* __restrict__ seg, int64_t stride, int64_t n,
-                                 uint32_t* __restrict__ keys, int32_t* __restrict__ vals) {
+                                 int64_t batch, uint32_t* __restrict__ keys,
+                                 int32_t* __restrict__ vals) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
-  keys[i] = static_cast<uint32_t>(seg[i * stride]);
+  const int64_t v = seg[i * stride];
+  keys[i] = static_cast<uint32_t>(v >= 0 && v < batch ? v : batch);
   vals[i] = static_cast<int32_t>(i);
 }
 
@@ -337,6 +486,89 @@ __global__ __launch_bounds__(kThreads) void sparse_embedding2_kernel(
   const bool valid = id >= 0 && id < rows;
   const float mask = valid ? 1.0f : 0.0f;
   out[t] = table[(valid ? id : fallback) * dim + d] * mask;
+}
+
+// Rows of dim % 4 == 0 with 16-byte aligned table and output: G lanes per
+// id (G = dim/4 rounded up to a power of two, at most 64), one 16-byte load
+// and store per lane per chunk of 4*G floats.
+template <typename IdxT, int G>
+__global__ __launch_bounds__(kThreads) void sparse_embedding2_vec_kernel(
+    const float* __restrict__ table, int64_t rows, int64_t dim, const IdxT* __restrict__ ids,
+    int64_t n, int64_t fallback, float* __restrict__ out) {
+  typedef typename VecT<4>::type V;
+  const int g = threadIdx.x & (G - 1);
+  const int64_t i = ((int64_t)blockIdx.x * kThreads + threadIdx.x) / G;
+  if (i >= n) return;
+  const int64_t id = static_cast<int64_t>(ids[i]);
+  const bool valid = id >= 0 && id < rows;
+  const float mask = valid ? 1.0f : 0.0f;
+  const float* src = table + (valid ? id : fallback) * dim;
+  float* dst = out + i * dim;
+  for (int64_t c = 4 * g; c < dim; c += 4 * G) store_row<4>(dst + c, load_row<4>(src + c) * mask);
+}
+
+// __pooling with n % 4 == 0, 16-byte aligned `gathered` below 2 GiB: G lanes
+// per output row (G = n/4 rounded up to a power of two, at most 64), each
+// lane summing 4 columns in j order.  Positions are taken in rounds of
+// kGroupRound: the lanes fetch the round's ids (distinct ids per lane,
+// coalesced) and turn them into byte offsets, and the round's row loads are
+// issued together, offsets broadcast inside the group.  Positions with
+// id <= 0 read zeros past the buffer's range check (no traffic), which add
+// nothing to the +0-seeded sums.  The count of ids > 0 is exact (k < 2^24),
+// as the reference's float count is.
+template <int G>
+__global__ __launch_bounds__(kThreads) void pooling_vec_kernel(
+    const int64_t* __restrict__ ids, const float* __restrict__ gathered, int64_t m, int64_t k,
+    int64_t n, int64_t ss0, int64_t ss1, int64_t ss2, int64_t sl0, int64_t sl1, int64_t sl2,
+    float* __restrict__ out) {
+  typedef typename VecT<4>::type V;
+  constexpr int kPer = (kGroupRound + G - 1) / G;
+  const int g = threadIdx.x & (G - 1);
+  const int64_t i = ((int64_t)blockIdx.x * kThreads + threadIdx.x) / G;
+  if (i >= m) return;
+  const int64_t* row_ids = ids + i * k;
+  int cnt = 0;
+  for (int64_t j = g; j < k; j += G) cnt += row_ids[j] > 0 ? 1 : 0;
+#pragma unroll
+  for (int off = G / 2; off > 0; off >>= 1) cnt += __shfl_xor(cnt, off, G);
+  const float red = static_cast<float>(cnt);
+  const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float*>(gathered), 0, static_cast<int>(m * k * n * 4), kRawBufferFlags);
+  const bool row_in = i >= ss0 && i < sl0;
+  const int64_t j0 = ss1 > 0 ? ss1 : 0;
+  const int64_t j1 = sl1 < k ? sl1 : k;
+  const uint32_t row_base = static_cast<uint32_t>(i * k * n * 4);
+  const uint32_t step = static_cast<uint32_t>(n * 4);
+  for (int64_t c = 4 * g; c < n; c += 4 * G) {
+    V sum = V(0.0f);
+    if (row_in) {
+      for (int64_t jb = j0; jb < j1; jb += kGroupRound) {
+        uint32_t off[kPer];
+#pragma unroll
+        for (int t = 0; t < kPer; ++t) {
+          const int64_t j = jb + g + G * t;
+          const int64_t id = j < j1 ? row_ids[j] : 0;
+          off[t] = id > 0 ? row_base + static_cast<uint32_t>(j) * step : kMaskedOff;
+        }
+        V v[kGroupRound];
+        static_for([&](auto uc) {
+          constexpr int u = decltype(uc)::value;
+          const uint32_t o = group_bcast<G, u % G>(off[u / G]);
+          v[u] = buffer_row<4>(rsrc, o == kMaskedOff ? o : o + static_cast<uint32_t>(c * 4));
+        }, std::make_integer_sequence<int, kGroupRound>{});
+#pragma unroll
+        for (int u = 0; u < kGroupRound; ++u) sum += v[u];
+      }
+    }
+    V res;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int64_t p = c + e;
+      const float s = (p >= ss2 && p < sl2) ? sum[e] : 0.0f;
+      res[e] = red == 0.0f ? 0.0f : s / red;
+    }
+    store_row<4>(out + i * n + c, res);
+  }
 }
 
 __global__ __launch_bounds__(kThreads) void pooling_kernel(
@@ -412,10 +644,11 @@ int segment_reduce(hipStream_t s, const float* data, int64_t rows, int64_t dim,
   a.status = status;
 
   const size_t off_bytes = sizeof(int64_t) * (size_t)(batch + 1);
+  auto align = [](size_t x) { return (x + 255) & ~size_t(255); };
   if (sorted_hint == 1) {
     int64_t* offsets = static_cast<int64_t*>(stream_workspace(s, off_bytes));
     if (!offsets) return set_error(ANNC_RESOURCE_EXHAUSTED, "workspace allocation failed");
-    hipLaunchKernelGGL(lower_bound_kernel<int64_t>, dim3((unsigned)ceil_div(batch + 1, kThreads)),
+    hipLaunchKernelGGL(seg_bounds_kernel<int64_t>, dim3((unsigned)ceil_div(n + 1, kThreads)),
                        dim3(kThreads), 0, s, seg, stride, n, batch, offsets);
     ANNC_HIP_TRY(hipGetLastError());
     a.offsets = offsets;
@@ -423,14 +656,48 @@ int segment_reduce(hipStream_t s, const float* data, int64_t rows, int64_t dim,
     return launch_bag(a, s);
   }
 
-  // General order: stable radix sort of (segment id, position), then CSR.
+  // General order, up to kCsMaxSegments segments: stable counting sort.
+  const int64_t nblk = ceil_div(n, kCsBlock);
+  if (batch <= kCsMaxSegments && nblk * batch <= (int64_t(1) << 24)) {
+    const size_t hb = align(sizeof(uint32_t) * (size_t)std::max<int64_t>(nblk * batch, 1));
+    const size_t tb = align(sizeof(uint32_t) * (size_t)batch);
+    const size_t pb = align(sizeof(int32_t) * (size_t)std::max<int64_t>(n, 1));
+    char* ws = static_cast<char*>(stream_workspace(s, 2 * hb + tb + align(off_bytes) + pb));
+    if (!ws) return set_error(ANNC_RESOURCE_EXHAUSTED, "workspace allocation failed");
+    uint32_t* H = reinterpret_cast<uint32_t*>(ws);
+    uint32_t* P = reinterpret_cast<uint32_t*>(ws + hb);
+    uint32_t* total = reinterpret_cast<uint32_t*>(ws + 2 * hb);
+    int64_t* offsets = reinterpret_cast<int64_t*>(ws + 2 * hb + tb);
+    int32_t* perm = reinterpret_cast<int32_t*>(ws + 2 * hb + tb + align(off_bytes));
+    const int nb = static_cast<int>(batch);
+    const size_t lds = sizeof(uint32_t) * (size_t)batch;
+    if (n > 0) {
+      hipLaunchKernelGGL(cs_hist_kernel, dim3((unsigned)nblk), dim3(kThreads), lds, s, seg, stride,
+                         n, nb, H);
+      ANNC_HIP_TRY(hipGetLastError());
+    }
+    hipLaunchKernelGGL(cs_prefix_kernel, dim3((unsigned)ceil_div(batch, kThreads)), dim3(kThreads),
+                       0, s, H, nb, static_cast<int>(nblk), P, total);
+    ANNC_HIP_TRY(hipGetLastError());
+    hipLaunchKernelGGL(cs_offsets_kernel, dim3(1), dim3(1024), 0, s, total, nb, offsets);
+    ANNC_HIP_TRY(hipGetLastError());
+    if (n > 0) {
+      hipLaunchKernelGGL(cs_scatter_kernel, dim3((unsigned)nblk), dim3(kThreads), lds, s, seg, stride, n,
+                         nb, P, offsets, perm);
+      ANNC_HIP_TRY(hipGetLastError());
+    }
+    a.offsets = offsets;
+    a.perm = perm;
+    return launch_bag(a, s);
+  }
+
+  // More segments: stable radix sort of (segment id, position), then CSR.
   int end_bit = 1;
-  while (end_bit < 32 && (1ull << end_bit) < (uint64_t)batch) ++end_bit;
+  while (end_bit < 32 && (1ull << end_bit) <= (uint64_t)batch) ++end_bit;  // batch fits too
   size_t temp_bytes = 0;
   ANNC_HIP_TRY(hipcub::DeviceRadixSort::SortPairs(nullptr, temp_bytes, (const uint32_t*)nullptr,
                                                   (uint32_t*)nullptr, (const int32_t*)nullptr,
                                                   (int32_t*)nullptr, (int)n, 0, end_bit, s));
-  auto align = [](size_t x) { return (x + 255) & ~size_t(255); };
   const size_t nk = align(sizeof(uint32_t) * (size_t)std::max<int64_t>(n, 1));
   const size_t nv = align(sizeof(int32_t) * (size_t)std::max<int64_t>(n, 1));
   const size_t total = 2 * nk + 2 * nv + align(off_bytes) + align(temp_bytes);
@@ -444,12 +711,12 @@ int segment_reduce(hipStream_t s, const float* data, int64_t rows, int64_t dim,
   void* temp = ws + 2 * nk + 2 * nv + align(off_bytes);
   if (n > 0) {
     hipLaunchKernelGGL(make_keys_kernel, dim3((unsigned)ceil_div(n, kThreads)), dim3(kThreads), 0,
-                       s, seg, stride, n, keys_in, vals_in);
+                       s, seg, stride, n, batch, keys_in, vals_in);
     ANNC_HIP_TRY(hipGetLastError());
     ANNC_HIP_TRY(hipcub::DeviceRadixSort::SortPairs(temp, temp_bytes, keys_in, keys_out, vals_in,
                                                     vals_out, (int)n, 0, end_bit, s));
   }
-  hipLaunchKernelGGL(lower_bound_kernel<uint32_t>, dim3((unsigned)ceil_div(batch + 1, kThreads)),
+  hipLaunchKernelGGL(seg_bounds_kernel<uint32_t>, dim3((unsigned)ceil_div(n + 1, kThreads)),
                      dim3(kThreads), 0, s, keys_out, (int64_t)1, n, batch, offsets);
   ANNC_HIP_TRY(hipGetLastError());
   a.offsets = offsets;
@@ -457,11 +724,48 @@ int segment_reduce(hipStream_t s, const float* data, int64_t rows, int64_t dim,
   return launch_bag(a, s);
 }
 
+namespace {
+
+// Lanes per row for the vector kernels: dim/4 rounded up to a power of two,
+// 1..64 (chunks of 4*64 floats beyond that).
+int vec_group(int64_t dim4) {
+  int g = 1;
+  while (g < 64 && g < dim4) g <<= 1;
+  return g;
+}
+
+template <typename IdxT>
+int launch_se2_vec(hipStream_t s, const float* table, int64_t rows, int64_t dim, const IdxT* ids,
+                   int64_t n, int64_t fallback, float* out) {
+  const int g = vec_group(dim / 4);
+  const dim3 grid((unsigned)ceil_div(n * g, kThreads));
+  switch (g) {
+#define ANNC_SE2(G)                                                                        \
+  case G:                                                                                  \
+    hipLaunchKernelGGL((sparse_embedding2_vec_kernel<IdxT, G>), grid, dim3(kThreads), 0, s, \
+                       table, rows, dim, ids, n, fallback, out);                           \
+    break;
+    ANNC_SE2(1) ANNC_SE2(2) ANNC_SE2(4) ANNC_SE2(8) ANNC_SE2(16) ANNC_SE2(32) ANNC_SE2(64)
+#undef ANNC_SE2
+  }
+  ANNC_HIP_TRY(hipGetLastError());
+  return ANNC_OK;
+}
+
+}  // namespace
+
 int launch_sparse_embedding2(hipStream_t s, const float* table, int64_t rows, int64_t dim,
                              const void* ids, int ids_is_64, int64_t n, int64_t fallback,
                              float* out) {
   const int64_t total = n * dim;
   if (total == 0) return ANNC_OK;
+  auto aligned16 = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
+  if (dim % 4 == 0 && aligned16(table) && aligned16(out) && n < (int64_t(1) << 40)) {
+    return ids_is_64 ? launch_se2_vec(s, table, rows, dim, static_cast<const int64_t*>(ids), n,
+                                      fallback, out)
+                     : launch_se2_vec(s, table, rows, dim, static_cast<const int32_t*>(ids), n,
+                                      fallback, out);
+  }
   dim3 grid((unsigned)ceil_div(total, kThreads));
   if (ids_is_64)
     hipLaunchKernelGGL(sparse_embedding2_kernel<int64_t>, grid, dim3(kThreads), 0, s, table, rows,
@@ -476,6 +780,23 @@ int launch_sparse_embedding2(hipStream_t s, const float* table, int64_t rows, in
 int launch_pooling(hipStream_t s, const int64_t* ids, const float* gathered, int64_t m, int64_t k,
                    int64_t n, const int64_t* ss, const int64_t* sl, float* out) {
   if (m * n == 0) return ANNC_OK;
+  const bool aligned = ((reinterpret_cast<uintptr_t>(gathered) | reinterpret_cast<uintptr_t>(out)) &
+                        15) == 0;
+  if (n % 4 == 0 && aligned && m * k * n * 4 < (int64_t(1) << 31) && k < (int64_t(1) << 24)) {
+    const int g = vec_group(n / 4);
+    const dim3 grid((unsigned)ceil_div(m * g, kThreads));
+    switch (g) {
+#define ANNC_POOL(G)                                                                          \
+  case G:                                                                                     \
+    hipLaunchKernelGGL(pooling_vec_kernel<G>, grid, dim3(kThreads), 0, s, ids, gathered, m, k, \
+                       n, ss[0], ss[1], ss[2], sl[0], sl[1], sl[2], out);                     \
+    break;
+      ANNC_POOL(1) ANNC_POOL(2) ANNC_POOL(4) ANNC_POOL(8) ANNC_POOL(16) ANNC_POOL(32) ANNC_POOL(64)
+#undef ANNC_POOL
+    }
+    ANNC_HIP_TRY(hipGetLastError());
+    return ANNC_OK;
+  }
   hipLaunchKernelGGL(pooling_kernel, dim3((unsigned)ceil_div(m * n, kThreads)), dim3(kThreads), 0,
                      s, ids, gathered, m, k, n, ss[0], ss[1], ss[2], sl[0], sl[1], sl[2], out);
   ANNC_HIP_TRY(hipGetLastError());
@@ -519,7 +840,7 @@ int annc_hip_embedding_bag(void* stream, const float* table, int64_t rows, int64
 int annc_hip_segment_reduce(void* stream, const float* data, int64_t rows, int64_t dim,
                             const void* indices, int indices_is_64, const int64_t* seg_ids,
                             int64_t seg_stride, int64_t n, int combiner, int64_t batch,
-                            float* out) {
+                            float* out, int seg_sorted) {
   using namespace annc;
   ANNC_REQUIRE(rows >= 0 && dim >= 1 && n >= 0 && batch >= 0 && seg_stride >= 1,
                "bad dimensions");
@@ -527,8 +848,9 @@ int annc_hip_segment_reduce(void* stream, const float* data, int64_t rows, int64
                "combiner must be 0 or 1");
   if (batch == 0) return set_error(ANNC_OK, "");
   ANNC_REQUIRE(data && out && (n == 0 || (indices && seg_ids)), "null pointer");
+  ANNC_REQUIRE(seg_sorted == 0 || seg_sorted == 1, "seg_sorted must be 0 or 1");
   int rc = segment_reduce(static_cast<hipStream_t>(stream), data, rows, dim, indices,
-                          indices_is_64, seg_ids, seg_stride, n, combiner, batch, out, 0);
+                          indices_is_64, seg_ids, seg_stride, n, combiner, batch, out, seg_sorted);
   return rc == ANNC_OK ? set_error(ANNC_OK, "") : rc;
 }
 

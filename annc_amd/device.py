@@ -143,8 +143,10 @@ def embedding_bag(table: torch.Tensor, ids: torch.Tensor, offsets: torch.Tensor,
 
 
 def segment_reduce(data: torch.Tensor, indices: torch.Tensor, segment_ids: torch.Tensor,
-                   batch: int, combiner: int = _lib.COMBINER_SUM, stream=None) -> torch.Tensor:
-    """Unsorted segment sum/mean into [batch, dim] (index order per segment)."""
+                   batch: int, combiner: int = _lib.COMBINER_SUM, sorted_ids: bool = False,
+                   stream=None) -> torch.Tensor:
+    """Segment sum/mean into [batch, dim] (index order per segment).
+    sorted_ids=True promises non-decreasing segment ids (skips the sort)."""
     _require_cuda(data, indices, segment_ids)
     rows, dim = data.shape
     seg_stride = segment_ids.stride(0) if segment_ids.dim() == 1 else segment_ids.stride(0)
@@ -152,7 +154,7 @@ def segment_reduce(data: torch.Tensor, indices: torch.Tensor, segment_ids: torch
     check(_lib.lib().annc_hip_segment_reduce(stream_ptr(stream), ptr(data.contiguous()), rows, dim,
                                              ptr(indices), 1 if indices.dtype == torch.int64 else 0,
                                              ptr(segment_ids), seg_stride, indices.numel(),
-                                             combiner, batch, ptr(out)))
+                                             combiner, batch, ptr(out), 1 if sorted_ids else 0))
     return out
 
 
@@ -182,10 +184,14 @@ def unique_gather(table: torch.Tensor, keys: torch.Tensor, col: int = 0, stream=
 
 
 def sparse_embedding2(table: torch.Tensor, ids: torch.Tensor, fallback_row: int = 0,
-                      stream=None) -> torch.Tensor:
-    _require_cuda(table, ids)
+                      out: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+    """Masked gather: out[i] = table[ids[i]] if 0 <= ids[i] < rows else 0."""
+    _require_cuda(table, ids, out)
     rows, dim = table.shape
-    out = torch.empty((ids.numel(), dim), dtype=torch.float32, device=table.device)
+    if out is None:
+        out = torch.empty((ids.numel(), dim), dtype=torch.float32, device=table.device)
+    elif out.shape != (ids.numel(), dim) or not out.is_contiguous():
+        raise ValueError("out must be a contiguous [ids.numel(), dim] tensor")
     check(_lib.lib().annc_hip_sparse_embedding2(stream_ptr(stream), ptr(table.contiguous()), rows,
                                                 dim, ptr(ids.contiguous()),
                                                 1 if ids.dtype == torch.int64 else 0, ids.numel(),

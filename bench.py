@@ -13,7 +13,10 @@ timed with HIP events on the stream the launches run on.
 
 `components` reports the other configurations (fused __matmul_add_relu,
 embedding bag GB/s, hashed multi-field bags GB/s, end-to-end wide&deep
-samples/s); `cpu_baseline` times the oracle's OpenBLAS path on the host.
+samples/s) and, under `other_rows`, the path's remaining operators on those
+inputs (sparse_embedding2 + __pooling in XLA's padded form, segment reduce,
+KPFusedGather, __batch_matmul, bucket ids); `cpu_baseline` times the
+oracle's OpenBLAS path on the host.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-components] [--no-cpu]
 """
@@ -248,6 +251,109 @@ def bench_config4(device):
             "ids_per_s": round(nnz / (k_ms * 1e-3), 1)}
 
 
+def bench_other_rows(device, bag_inputs):
+    """The path's other operators, on the configs' inputs in the form each
+    operator takes them (no benchmark config names them): the XLA form of
+    configs[2] (sparse_embedding2 masked gather over padded [B, L] ids, then
+    __pooling), the TF segment-reduce form of configs[2], the KPFusedGather
+    engine on configs[2]'s ids, __batch_matmul at 32 x configs[0]'s shape,
+    and configs[3]'s bucket ids alone."""
+    import numpy as np
+    import torch
+    from annc_amd import workloads
+    from annc_amd import device as dev
+    res = {}
+    w = bag_inputs
+    bags, dim = w.offsets.size - 1, w.table.shape[1]
+    nnz = int(w.offsets[-1])
+    lens = np.diff(w.offsets)
+    table = torch.from_numpy(w.table).to(device)
+    ids = torch.from_numpy(w.ids).to(device)
+
+    # XLA form: ids padded to [B, L] with -1 (masked), gathered [B, L, dim], pooled
+    width = int(lens.max())
+    pad = np.full((bags, width), -1, dtype=np.int64)
+    pos = np.arange(width)[None, :] < lens[:, None]
+    pad[pos] = w.ids
+    pad_d = torch.from_numpy(pad).to(device)
+    gathered = torch.empty((bags * width, dim), dtype=torch.float32, device=device)
+    se_ms = graph_time_ms(lambda i: dev.sparse_embedding2(table, pad_d, 0, out=gathered),
+                          launches=50, replays=5)
+    g3 = gathered.view(bags, width, dim)
+    pool_ms = graph_time_ms(lambda i: dev.pooling(pad_d, g3, (0, 0, 0), (bags, width, dim)),
+                            launches=50, replays=5)
+    se_bytes = 8 * bags * width + 4 * dim * nnz + 4 * dim * bags * width
+    # __pooling reads the gathered rows of positions with id > 0 only
+    pool_bytes = 8 * bags * width + 4 * dim * nnz + 4 * dim * bags
+    for name, ms, nbytes in (("sparse_embedding2", se_ms, se_bytes),
+                             ("pooling", pool_ms, pool_bytes)):
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        res[f"{name}_config3_padded"] = {
+            "workload": f"configs[2] ids padded to [{bags}, {width}] (-1 = masked), dim {dim}",
+            "algorithmic_bytes": nbytes, "kernel_us": round(ms * 1e3, 3), "GBps": round(gbs, 1),
+            "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
+        log(f"{name} (padded configs[2]): {ms * 1e3:.2f} us, {gbs:.0f} GB/s")
+
+    # KPFusedSparseSegmentReduce form: indices + per-position segment ids
+    seg = torch.from_numpy(np.repeat(np.arange(bags, dtype=np.int64), lens)).to(device)
+    sr_bytes = 16 * nnz + 4 * dim * nnz + 4 * dim * bags
+    for name, sorted_ids in (("sorted_ids", True), ("any_order", False)):
+        sr_ms = graph_time_ms(lambda i: dev.segment_reduce(table, ids, seg, bags, 1,
+                                                           sorted_ids=sorted_ids),
+                              launches=100, replays=5)
+        gbs = sr_bytes / (sr_ms * 1e-3) / 1e9
+        res[f"segment_reduce_config3_mean_{name}"] = {
+            "workload": "configs[2] as KPFusedSparseSegmentReduce inputs (indices, segment "
+                        "ids), " + ("ids promised sorted" if sorted_ids else
+                                    "no order assumed (stable counting sort by segment)"),
+            "algorithmic_bytes": sr_bytes, "kernel_us": round(sr_ms * 1e3, 3),
+            "GBps": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
+        log(f"segment reduce ({name}): {sr_ms * 1e3:.2f} us, {gbs:.0f} GB/s")
+
+    # KPFusedGather engine: sort-based unique + gather; the unique count is
+    # read back, so each call ends with a synchronisation (wall time)
+    for _ in range(3):
+        dev.unique_gather(table, ids)
+    ts = []
+    for _ in range(20):
+        t0 = time.perf_counter()
+        u, _, _ = dev.unique_gather(table, ids)
+        ts.append(time.perf_counter() - t0)
+    res["unique_gather_config3"] = {
+        "workload": f"configs[2] ids ({nnz} keys, {int(u.numel())} unique) -> unique, "
+                    "inverse index, gathered rows",
+        "wall_us_median": round(statistics.median(ts) * 1e6, 1),
+        "keys_per_s": round(nnz / statistics.median(ts), 1)}
+
+    # __batch_matmul: 32 independent configs[0]-shaped products, row-major B
+    g = workloads.rng(5)
+    bm, m, k, n = 32, 512, 256, 256
+    a = torch.from_numpy(g.standard_normal((bm, m, k)).astype(np.float32)).to(device)
+    b = torch.from_numpy((g.standard_normal((bm, k, n)) / 16).astype(np.float32)).to(device)
+    c = torch.empty((bm, m, n), dtype=torch.float32, device=device)
+    bm_ms = graph_time_ms(lambda i: dev.gemm(a, b, out=c), launches=50, replays=5)
+    tf = 2.0 * bm * m * n * k / (bm_ms * 1e-3) / 1e12
+    res["batch_matmul_32x512x256x256"] = {
+        "workload": "__batch_matmul, 32 x [512x256] . [256x256] fp32, row-major B",
+        "kernel_us": round(bm_ms * 1e3, 3), "tflops": round(tf, 2),
+        "mfma_frac": round(tf / FP32_MFMA_PEAK_TFLOPS, 4)}
+    log(f"batch matmul: {bm_ms * 1e3:.2f} us, {tf:.1f} TFLOP/s")
+
+    # bucket ids alone (decimal text -> Fingerprint64 -> % 1e5) on configs[3]'s ids
+    h = workloads.config4(seed=0)
+    hid = torch.from_numpy(h.ids).to(device)
+    hb_ms = graph_time_ms(lambda i: dev.hash_bucket_int64(hid, h.num_buckets),
+                          launches=50, replays=5)
+    res["hash_bucket_int64_config4"] = {
+        "workload": f"configs[3] ids ({h.ids.size}) -> bucket ids, int64 in and out",
+        "kernel_us": round(hb_ms * 1e3, 3),
+        "ids_per_s": round(h.ids.size / (hb_ms * 1e-3), 1),
+        "GBps": round(16 * h.ids.size / (hb_ms * 1e-3) / 1e9, 1)}
+    log(f"hash bucket ids: {hb_ms * 1e3:.2f} us")
+    dev.stream_status()
+    return res
+
+
 def bench_config5(device, steps: int):
     import torch
     from annc_amd import workloads
@@ -450,6 +556,8 @@ def main() -> int:
         components["embedding_bag_config3"], bag_inputs = bench_config3(device)
         components["hashed_bags_config4"] = bench_config4(device)
         components["wide_deep_e2e_config5"] = bench_config5(device, steps=100)
+        torch.cuda.empty_cache()
+        components["other_rows"] = bench_other_rows(device, bag_inputs)
         torch.cuda.empty_cache()
     components["tower_layers_config2"] = tower["per_layer"]
     components["tower_graph_replay_config2"] = tower["graph"]

@@ -214,12 +214,15 @@ int annc_hip_embedding_bag(void* stream, const float* table, int64_t rows, int64
 
 /* Segment reduction with arbitrary (unsorted) segment ids, the engine of
  * KPFusedSparseSegmentReduce: out[seg_ids[i*seg_stride], :] += data[indices[i], :]
- * in index order; out has `batch` rows (rows without ids stay 0).  Segment
- * ids must lie in [0, batch). */
+ * in index order; out has `batch` rows (rows without ids stay 0).  Positions
+ * whose segment id lies outside [0, batch) are skipped.  seg_sorted = 1
+ * promises non-decreasing segment ids (TF's SparseSegment* contract, and the
+ * order a SparseTensor's row indices have), which skips the stable sort by
+ * segment; 0 makes no assumption. */
 int annc_hip_segment_reduce(void* stream, const float* data, int64_t rows, int64_t dim,
                             const void* indices, int indices_is_64, const int64_t* seg_ids,
                             int64_t seg_stride, int64_t n, int combiner, int64_t batch,
-                            float* out);
+                            float* out, int seg_sorted);
 
 /* sparse_embedding2 kLoop fusion (graph_opt.cc:8-41 with the bound checks of
  * bisheng-cpu/embedding_simplify.cc:62-81):

@@ -119,6 +119,47 @@ def test_tf_segment_reduce_empty_indices():
     assert int(so) == 4
 
 
+SEG_ORDER_CASES = [
+    ("reversed", 3000, 50000),
+    ("one segment over 5 blocks of 1024 positions", 1, 5000),
+    ("largest counting-sort batch", 16384, 70000),
+    ("radix-sort batch", 16385, 70000),
+    ("mostly empty segments", 10000, 100),
+    ("ids outside [0, batch) dropped", 1000, 30000),
+    ("ids outside [0, batch) dropped, radix sort", 20000, 30000),
+    ("sorted", 4096, 81857),
+]
+
+
+@pytest.mark.parametrize("what,batch,n", SEG_ORDER_CASES)
+@pytest.mark.parametrize("combiner", [0, 1])
+def test_device_segment_reduce_orders(what, batch, n, combiner):
+    """Every segment's rows are summed in position order whatever the order
+    of the segment ids (stable counting sort up to 16384 segments, radix
+    sort beyond): bit-exact against the sequential loop."""
+    note(f"device segment reduce: {what} (batch {batch}, n {n}, combiner {combiner})")
+    g = workloads.rng(batch + n)
+    data = g.standard_normal((2000, 8)).astype(np.float32)
+    idx = g.integers(0, 2000, size=n).astype(np.int64)
+    seg = g.integers(0, batch, size=n).astype(np.int64)
+    if what.startswith("reversed"):
+        seg = np.sort(seg)[::-1].copy()
+    elif what.startswith("sorted"):
+        seg.sort()
+    keep = np.ones(n, bool)
+    if what.startswith("ids outside"):
+        bad = g.choice(n, size=n // 10, replace=False)
+        seg[bad] = g.choice([-1, -7, batch, batch + 5, 2**40], size=bad.size)
+        keep[bad] = False
+    out = dev.segment_reduce(to_dev(data), to_dev(idx), to_dev(seg), batch, combiner)
+    ref = ora.segment_reduce(data, idx[keep], seg[keep], batch, combiner)
+    np.testing.assert_array_equal(to_host(out), ref)
+    if what.startswith("sorted"):  # the caller's promise skips the sort: same bits
+        out = dev.segment_reduce(to_dev(data), to_dev(idx), to_dev(seg), batch, combiner,
+                                 sorted_ids=True)
+        np.testing.assert_array_equal(to_host(out), ref)
+
+
 def test_device_segment_reduce_unsorted():
     note("device segment reduce")
     g = workloads.rng(8)
@@ -129,28 +170,46 @@ def test_device_segment_reduce_unsorted():
     np.testing.assert_array_equal(to_host(out), ora.segment_reduce(data, idx, seg, 700, 1))
 
 
-def test_sparse_embedding2_bit_exact():
-    note("sparse_embedding2")
-    g = workloads.rng(3)
-    table = g.standard_normal((1000, 16)).astype(np.float32)
-    ids = g.integers(-50, 1050, size=3000).astype(np.int64)
+@pytest.mark.parametrize("dim", [16, 1, 3, 64, 300, 1028])
+@pytest.mark.parametrize("idx_dtype", [np.int64, np.int32])
+def test_sparse_embedding2_bit_exact(dim, idx_dtype):
+    """dims divisible by 4 take the lane-group float4 kernel (1028: chunks of
+    256 floats), the others the scalar one; masked ids multiply the fallback
+    row by 0, so a NaN there stays NaN, as in the reference's mul."""
+    note(f"sparse_embedding2 dim={dim} ids={np.dtype(idx_dtype).name}")
+    g = workloads.rng(3 + dim)
+    table = g.standard_normal((1000, dim)).astype(np.float32)
+    table[0, 0] = np.nan   # the fallback row
+    table[7, -1] = -0.0
+    ids = g.integers(-50, 1050, size=3000).astype(idx_dtype)
+    ids[:4] = [7, -1, 999, 1000]
     out = dev.sparse_embedding2(to_dev(table), to_dev(ids), fallback_row=0)
     got = to_host(out)
     ref = ora.sparse_embedding2(table, ids, 0)
     np.testing.assert_array_equal(got, ref)
     assert (np.signbit(got) == np.signbit(ref)).all()
+    assert np.isnan(got[1, 0])
 
 
-@pytest.mark.parametrize("ss,sl", [((0, 0, 0), (64, 30, 16)), ((3, 2, 1), (60, 25, 12))])
-def test_pooling_bit_exact(ss, sl):
-    note(f"pooling {ss} {sl}")
-    g = workloads.rng(4)
+POOL_CASES = [((0, 0, 0), (64, 30, 16)), ((3, 2, 1), (60, 25, 12))]
+
+
+@pytest.mark.parametrize("n", [16, 64, 6, 260])
+@pytest.mark.parametrize("ss,sl", POOL_CASES)
+def test_pooling_bit_exact(ss, sl, n):
+    """n % 4 == 0 takes the lane-group kernel (masked positions are never
+    read: NaNs there must not leak), other widths the scalar one."""
+    note(f"pooling n={n} {ss} {sl}")
+    g = workloads.rng(4 + n)
     ids = g.integers(-2, 50, size=(64, 30)).astype(np.int64)
     ids[5] = 0
-    gathered = g.standard_normal((64, 30, 16)).astype(np.float32)
+    gathered = g.standard_normal((64, 30, n)).astype(np.float32)
+    gathered[ids <= 0] = np.nan
+    sl = (sl[0], sl[1], min(sl[2], n) if n >= 16 else n)
     ref = ora.pooling(ids, gathered, ss, sl)
-    np.testing.assert_array_equal(to_host(dev.pooling(to_dev(ids), to_dev(gathered), ss, sl)), ref)
-    out = np.empty((64, 16), np.float32)
+    got = to_host(dev.pooling(to_dev(ids), to_dev(gathered), ss, sl))
+    np.testing.assert_array_equal(got, ref)
+    out = np.empty((64, n), np.float32)
     xla.pooling(ids, gathered, ss, sl, out)  # __pooling custom call on host buffers
     np.testing.assert_array_equal(out, ref)
 
