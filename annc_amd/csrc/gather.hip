@@ -5,14 +5,18 @@
 // unordered_map walk over the rows), every row gets the index of its key in
 // that order, and the table rows of the unique keys are copied out.
 //
-// Device formulation (all steps keep the reference's order exactly):
-//   1. (key, position) pairs sorted by key with a stable radix sort, so the
-//      first element of each run of equal keys is the key's first occurrence;
-//   2. run heads flagged and inclusive-summed: run id of every sorted element,
-//      U = number of runs;
-//   3. the runs sorted by first position (positions of absent runs padded to
-//      INT32_MAX so they sort last): rank of a run = its place in that order;
-//   4. unique[rank] = key, indices[position] = rank, out_data[rank] = row.
+// Device formulation (the outputs do not depend on thread timing):
+//   1. every key goes into an open-addressing hash table (64-bit CAS on the
+//      key, linear probing, capacity a power of two >= 2n, a separate slot
+//      for the empty marker's own value) and the slot keeps the smallest
+//      position of its key (atomicMin): the key's first occurrence;
+//   2. position i is a first occurrence iff its slot's minimum is i; an
+//      inclusive scan of those marks numbers the unique keys in order of
+//      first occurrence (the reference's order), U = the last sum;
+//   3. indices[i] = number of the first occurrence of i's key; that
+//      occurrence also writes unique[number] = key;
+//   4. out rows of the U unique keys, G lanes per row, 16-byte loads where
+//      the rows allow.
 // U is only known on the device; kernels sized by n test r < U themselves.
 #include <hip/hip_runtime.h>
 #include <hipcub/hipcub.hpp>
@@ -26,77 +30,181 @@ namespace annc {
 namespace {
 
 constexpr int kThreads = 256;
+constexpr int64_t kEmpty = INT64_MIN;  // key of an unused slot
 
-__global__ void extract_keys_kernel(const int64_t* __restrict__ keys, int64_t stride, int64_t n,
-                                    int64_t* __restrict__ k_out, int32_t* __restrict__ pos_out) {
-  const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-  if (i >= n) return;
-  k_out[i] = keys[i * stride];
-  pos_out[i] = static_cast<int32_t>(i);
+// MurmurHash3's 64-bit finaliser (fmix64): spreads nearby keys over the table.
+__device__ __forceinline__ uint64_t mix64(uint64_t x) {
+  x ^= x >> 33;
+  x *= 0xff51afd7ed558ccdull;
+  x ^= x >> 33;
+  x *= 0xc4ceb9fe1a85ec53ull;
+  x ^= x >> 33;
+  return x;
 }
 
-__global__ void run_heads_kernel(const int64_t* __restrict__ sk, int64_t n,
-                                 int32_t* __restrict__ head, int32_t* __restrict__ first_pos) {
-  const int64_t j = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-  if (j >= n) return;
-  head[j] = (j == 0 || sk[j] != sk[j - 1]) ? 1 : 0;
-  first_pos[j] = INT_MAX;  // padding for runs that do not exist
+__global__ void ug_clear_kernel(int64_t* __restrict__ tab_key, int32_t* __restrict__ tab_first,
+                                int64_t slots) {
+  const int64_t c = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (c >= slots) return;
+  tab_key[c] = kEmpty;
+  tab_first[c] = INT_MAX;
 }
 
-// run = runid[j] - 1 for the head j of every run
-__global__ void run_first_kernel(const int64_t* __restrict__ sk, const int32_t* __restrict__ sp,
-                                 const int32_t* __restrict__ head,
-                                 const int32_t* __restrict__ runid, int64_t n,
-                                 int32_t* __restrict__ first_pos, int32_t* __restrict__ run_idx,
-                                 int64_t* __restrict__ run_key) {
-  const int64_t j = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-  if (j >= n) return;
-  run_idx[j] = static_cast<int32_t>(j);
-  if (head[j]) {
-    const int32_t r = runid[j] - 1;
-    first_pos[r] = sp[j];
-    run_key[r] = sk[j];
+// Probe for `key` from its hash, inserting it into a free slot if it is
+// new; returns the slot, or -1 after `cap` probes (cannot happen while at
+// most cap/2 distinct keys are inserted).  A slot's key never changes once
+// set, so a plain read that already shows a key decides without an atomic.
+__device__ __forceinline__ int64_t probe_insert(int64_t* tab_key, int64_t cap, int64_t key) {
+  int64_t h = static_cast<int64_t>(mix64(static_cast<uint64_t>(key)) & (uint64_t)(cap - 1));
+  for (int64_t probe = 0; probe < cap; ++probe) {
+    int64_t seen = __hip_atomic_load(tab_key + h, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    if (seen == kEmpty)
+      seen = static_cast<int64_t>(atomicCAS(reinterpret_cast<unsigned long long*>(tab_key + h),
+                                            static_cast<unsigned long long>(kEmpty),
+                                            static_cast<unsigned long long>(key)));
+    if (seen == kEmpty || seen == key) return h;
+    h = (h + 1) & (cap - 1);
+  }
+  return -1;
+}
+
+constexpr int kUgBlock = 256;            // positions per workgroup
+constexpr int kUgLocal = 2 * kUgBlock;   // LDS table slots (+1 for the empty marker's value)
+
+// Slot of every position's key in the global table, whose slots keep their
+// key's smallest position.  Each workgroup first de-duplicates its 256
+// positions in an LDS table (block minimum per key), then inserts each of
+// its distinct keys once: a key that is frequent in the data costs one
+// global CAS and one atomicMin per workgroup, not one per occurrence.
+__global__ __launch_bounds__(kThreads) void ug_insert_kernel(
+    const int64_t* __restrict__ keys, int64_t stride, int64_t n, int64_t cap,
+    int64_t* __restrict__ tab_key, int32_t* __restrict__ tab_first,
+    int32_t* __restrict__ slot_of, int* __restrict__ status) {
+  __shared__ int64_t lkey[kUgLocal];
+  __shared__ int32_t lfirst[kUgLocal + 1];
+  __shared__ int32_t lslot[kUgLocal + 1];
+  __shared__ int lempty;  // some position holds the empty marker's value
+  constexpr int kPer = kUgBlock / kThreads;
+  for (int l = threadIdx.x; l < kUgLocal; l += kThreads) lkey[l] = kEmpty;
+  for (int l = threadIdx.x; l <= kUgLocal; l += kThreads) lfirst[l] = INT_MAX;
+  if (threadIdx.x == 0) lempty = 0;
+  __syncthreads();
+  const int64_t b0 = (int64_t)blockIdx.x * kUgBlock;
+  int local[kPer];
+#pragma unroll
+  for (int u = 0; u < kPer; ++u) {
+    const int64_t i = b0 + u * kThreads + threadIdx.x;
+    local[u] = -1;
+    if (i >= n) continue;
+    const int64_t key = keys[i * stride];
+    int l = kUgLocal;
+    if (key == kEmpty) {
+      lempty = 1;
+    } else {
+      int h = static_cast<int>(mix64(static_cast<uint64_t>(key)) & (kUgLocal - 1));
+      for (int probe = 0; probe < kUgLocal; ++probe) {  // <= kUgBlock keys in 2x slots
+        const int64_t seen = static_cast<int64_t>(atomicCAS(
+            reinterpret_cast<unsigned long long*>(lkey + h), static_cast<unsigned long long>(kEmpty),
+            static_cast<unsigned long long>(key)));
+        if (seen == kEmpty || seen == key) break;
+        h = (h + 1) & (kUgLocal - 1);
+      }
+      l = h;
+    }
+    atomicMin(lfirst + l, static_cast<int32_t>(i));
+    local[u] = l;
+  }
+  __syncthreads();
+  for (int l = threadIdx.x; l <= kUgLocal; l += kThreads) {
+    const bool used = l < kUgLocal ? lkey[l] != kEmpty : lempty != 0;
+    if (!used) continue;
+    int64_t g = cap;  // the empty marker's value has the extra global slot
+    if (l < kUgLocal) {
+      g = probe_insert(tab_key, cap, lkey[l]);
+      if (g < 0) {  // reported, never hangs
+        atomicOr(status, 2);
+        g = cap;
+      }
+    }
+    const int32_t first = lfirst[l];
+    if (__hip_atomic_load(tab_first + g, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) > first)
+      atomicMin(tab_first + g, first);
+    lslot[l] = static_cast<int32_t>(g);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int u = 0; u < kPer; ++u) {
+    const int64_t i = b0 + u * kThreads + threadIdx.x;
+    if (i < n) slot_of[i] = lslot[local[u]];
   }
 }
 
-__global__ void rank_kernel(const int32_t* __restrict__ order, const int64_t* __restrict__ run_key,
-                            const int32_t* __restrict__ runid, int64_t n,
-                            int32_t* __restrict__ rank_of_run, int64_t* __restrict__ unique,
-                            int64_t* __restrict__ num_unique) {
-  const int64_t r = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-  const int32_t total = runid[n - 1];
-  if (r == 0) num_unique[0] = total;
-  if (r >= total) return;
-  const int32_t run = order[r];
-  rank_of_run[run] = static_cast<int32_t>(r);
-  unique[r] = run_key[run];
+__global__ void ug_mark_kernel(const int32_t* __restrict__ slot_of,
+                               const int32_t* __restrict__ tab_first, int64_t n,
+                               int32_t* __restrict__ first_mark) {
+  const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (i >= n) return;
+  first_mark[i] = tab_first[slot_of[i]] == static_cast<int32_t>(i) ? 1 : 0;
 }
 
-__global__ void indices_kernel(const int32_t* __restrict__ sp, const int32_t* __restrict__ runid,
-                               const int32_t* __restrict__ rank_of_run, int64_t n,
-                               int32_t* __restrict__ indices) {
-  const int64_t j = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-  if (j >= n) return;
-  indices[sp[j]] = rank_of_run[runid[j] - 1];
+// number[i] = inclusive count of first occurrences up to i
+__global__ void ug_output_kernel(const int64_t* __restrict__ keys, int64_t stride, int64_t n,
+                                 const int32_t* __restrict__ slot_of,
+                                 const int32_t* __restrict__ tab_first,
+                                 const int32_t* __restrict__ number, int32_t* __restrict__ indices,
+                                 int64_t* __restrict__ unique, int64_t* __restrict__ num_unique) {
+  const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (i >= n) return;
+  const int32_t first = tab_first[slot_of[i]];
+  const int32_t r = number[first] - 1;
+  indices[i] = r;
+  if (first == static_cast<int32_t>(i)) unique[r] = keys[i * stride];
+  if (i == n - 1) num_unique[0] = number[n - 1];
 }
 
-// out[r, :] = table[unique[r], :] for r < U; ids outside the table give a
-// zero row and set the stream's status word.
-__global__ void gather_unique_kernel(const float* __restrict__ table, int64_t rows, int64_t dim,
-                                     const int64_t* __restrict__ unique,
-                                     const int32_t* __restrict__ runid, int64_t n,
-                                     float* __restrict__ out, int* __restrict__ status) {
-  const int64_t t = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-  const int64_t total = runid[n - 1];
-  if (t >= total * dim) return;
-  const int64_t r = t / dim, d = t - r * dim;
+// out[r, :] = table[unique[r], :] for r < U, G lanes per row (VEC floats per
+// lane); keys outside the table give a zero row and set the status word.
+template <int G, int VEC>
+__global__ __launch_bounds__(kThreads) void ug_gather_kernel(
+    const float* __restrict__ table, int64_t rows, int64_t dim, const int64_t* __restrict__ unique,
+    const int64_t* __restrict__ num_unique, int64_t n, float* __restrict__ out,
+    int* __restrict__ status) {
+  const int g = threadIdx.x & (G - 1);
+  const int64_t r = ((int64_t)blockIdx.x * kThreads + threadIdx.x) / G;
+  if (r >= n || r >= num_unique[0]) return;
   const int64_t id = unique[r];
   const bool ok = id >= 0 && id < rows;
-  if (!ok && d == 0) atomicOr(status, 1);
-  out[t] = ok ? table[id * dim + d] : 0.0f;
+  if (!ok && g == 0) atomicOr(status, 1);
+  const float* src = table + (ok ? id : 0) * dim;
+  float* dst = out + r * dim;
+  for (int64_t c = (int64_t)g * VEC; c < dim; c += (int64_t)G * VEC) {
+    if constexpr (VEC == 4) {
+      typedef float V __attribute__((ext_vector_type(4)));
+      const V v = ok ? *reinterpret_cast<const V*>(src + c) : V(0.0f);
+      *reinterpret_cast<V*>(dst + c) = v;
+    } else {
+      dst[c] = ok ? src[c] : 0.0f;
+    }
+  }
 }
 
 __global__ void store_i64_kernel(int64_t* p, int64_t v) { *p = v; }
+
+template <int VEC>
+void launch_ug_gather(hipStream_t s, int g, const float* table, int64_t rows, int64_t dim,
+                      const int64_t* unique, const int64_t* num_unique, int64_t n, float* out,
+                      int* status) {
+  const dim3 grid((unsigned)ceil_div(n * g, kThreads));
+  switch (g) {
+#define ANNC_UG(G)                                                                          \
+  case G:                                                                                   \
+    hipLaunchKernelGGL((ug_gather_kernel<G, VEC>), grid, dim3(kThreads), 0, s, table, rows, \
+                       dim, unique, num_unique, n, out, status);                            \
+    break;
+    ANNC_UG(1) ANNC_UG(2) ANNC_UG(4) ANNC_UG(8) ANNC_UG(16) ANNC_UG(32) ANNC_UG(64)
+#undef ANNC_UG
+  }
+}
 
 }  // namespace
 
@@ -105,56 +213,46 @@ int unique_gather(hipStream_t s, const float* table, int64_t rows, int64_t dim,
                   int64_t* unique, int32_t* indices, float* out) {
   int* status = stream_status(s);
   if (!status) return set_error(ANNC_RESOURCE_EXHAUSTED, "status allocation failed");
-  size_t sort1 = 0, sort2 = 0, scan = 0;
-  ANNC_HIP_TRY(hipcub::DeviceRadixSort::SortPairs(nullptr, sort1, (const int64_t*)nullptr,
-                                                  (int64_t*)nullptr, (const int32_t*)nullptr,
-                                                  (int32_t*)nullptr, (int)n, 0, 64, s));
-  ANNC_HIP_TRY(hipcub::DeviceRadixSort::SortPairs(nullptr, sort2, (const int32_t*)nullptr,
-                                                  (int32_t*)nullptr, (const int32_t*)nullptr,
-                                                  (int32_t*)nullptr, (int)n, 0, 32, s));
+  int64_t cap = 1024;
+  while (cap < 2 * n) cap <<= 1;
+  size_t scan = 0;
   ANNC_HIP_TRY(hipcub::DeviceScan::InclusiveSum(nullptr, scan, (const int32_t*)nullptr,
                                                 (int32_t*)nullptr, (int)n, s));
   auto align = [](size_t x) { return (x + 255) & ~size_t(255); };
-  const size_t n8 = align(sizeof(int64_t) * (size_t)n), n4 = align(sizeof(int32_t) * (size_t)n);
-  const size_t temp = align(std::max(sort1, std::max(sort2, scan)));
-  char* ws = static_cast<char*>(stream_workspace(s, 3 * n8 + 9 * n4 + temp));
+  const size_t kb = align(sizeof(int64_t) * (size_t)(cap + 1));
+  const size_t fb = align(sizeof(int32_t) * (size_t)(cap + 1));
+  const size_t n4 = align(sizeof(int32_t) * (size_t)n);
+  char* ws = static_cast<char*>(stream_workspace(s, kb + fb + 3 * n4 + align(scan)));
   if (!ws) return set_error(ANNC_RESOURCE_EXHAUSTED, "workspace allocation failed");
-  int64_t* k_in = reinterpret_cast<int64_t*>(ws);
-  int64_t* k_out = reinterpret_cast<int64_t*>(ws + n8);
-  int64_t* run_key = reinterpret_cast<int64_t*>(ws + 2 * n8);
-  char* w4 = ws + 3 * n8;
-  int32_t* p_in = reinterpret_cast<int32_t*>(w4);
-  int32_t* p_out = reinterpret_cast<int32_t*>(w4 + n4);
-  int32_t* head = reinterpret_cast<int32_t*>(w4 + 2 * n4);
-  int32_t* runid = reinterpret_cast<int32_t*>(w4 + 3 * n4);
-  int32_t* first_pos = reinterpret_cast<int32_t*>(w4 + 4 * n4);
-  int32_t* run_idx = reinterpret_cast<int32_t*>(w4 + 5 * n4);
-  int32_t* first_sorted = reinterpret_cast<int32_t*>(w4 + 6 * n4);
-  int32_t* order = reinterpret_cast<int32_t*>(w4 + 7 * n4);
-  int32_t* rank_of_run = reinterpret_cast<int32_t*>(w4 + 8 * n4);
-  void* tmp = w4 + 9 * n4;
+  int64_t* tab_key = reinterpret_cast<int64_t*>(ws);
+  int32_t* tab_first = reinterpret_cast<int32_t*>(ws + kb);
+  int32_t* slot_of = reinterpret_cast<int32_t*>(ws + kb + fb);
+  int32_t* mark = reinterpret_cast<int32_t*>(ws + kb + fb + n4);
+  int32_t* number = reinterpret_cast<int32_t*>(ws + kb + fb + 2 * n4);
+  void* tmp = ws + kb + fb + 3 * n4;
   const dim3 grid((unsigned)ceil_div(n, kThreads));
-  hipLaunchKernelGGL(extract_keys_kernel, grid, dim3(kThreads), 0, s, keys, stride, n, k_in, p_in);
+  hipLaunchKernelGGL(ug_clear_kernel, dim3((unsigned)ceil_div(cap + 1, kThreads)), dim3(kThreads),
+                     0, s, tab_key, tab_first, cap + 1);
   ANNC_HIP_TRY(hipGetLastError());
-  ANNC_HIP_TRY(hipcub::DeviceRadixSort::SortPairs(tmp, sort1, k_in, k_out, p_in, p_out, (int)n, 0,
-                                                  64, s));
-  hipLaunchKernelGGL(run_heads_kernel, grid, dim3(kThreads), 0, s, k_out, n, head, first_pos);
+  hipLaunchKernelGGL(ug_insert_kernel, dim3((unsigned)ceil_div(n, kUgBlock)), dim3(kThreads), 0, s,
+                     keys, stride, n, cap, tab_key, tab_first, slot_of, status);
   ANNC_HIP_TRY(hipGetLastError());
-  ANNC_HIP_TRY(hipcub::DeviceScan::InclusiveSum(tmp, scan, head, runid, (int)n, s));
-  hipLaunchKernelGGL(run_first_kernel, grid, dim3(kThreads), 0, s, k_out, p_out, head, runid, n,
-                     first_pos, run_idx, run_key);
+  hipLaunchKernelGGL(ug_mark_kernel, grid, dim3(kThreads), 0, s, slot_of, tab_first, n, mark);
   ANNC_HIP_TRY(hipGetLastError());
-  ANNC_HIP_TRY(hipcub::DeviceRadixSort::SortPairs(tmp, sort2, first_pos, first_sorted, run_idx,
-                                                  order, (int)n, 0, 32, s));
-  hipLaunchKernelGGL(rank_kernel, grid, dim3(kThreads), 0, s, order, run_key, runid, n,
-                     rank_of_run, unique, num_unique);
-  ANNC_HIP_TRY(hipGetLastError());
-  hipLaunchKernelGGL(indices_kernel, grid, dim3(kThreads), 0, s, p_out, runid, rank_of_run, n,
-                     indices);
+  ANNC_HIP_TRY(hipcub::DeviceScan::InclusiveSum(tmp, scan, mark, number, (int)n, s));
+  hipLaunchKernelGGL(ug_output_kernel, grid, dim3(kThreads), 0, s, keys, stride, n, slot_of,
+                     tab_first, number, indices, unique, num_unique);
   ANNC_HIP_TRY(hipGetLastError());
   if (dim > 0) {
-    hipLaunchKernelGGL(gather_unique_kernel, dim3((unsigned)ceil_div(n * dim, kThreads)),
-                       dim3(kThreads), 0, s, table, rows, dim, unique, runid, n, out, status);
+    int g = 1;
+    const bool vec = dim % 4 == 0 && ((reinterpret_cast<uintptr_t>(table) |
+                                       reinterpret_cast<uintptr_t>(out)) & 15) == 0;
+    const int64_t lanes = vec ? dim / 4 : dim;
+    while (g < 64 && g < lanes) g <<= 1;
+    if (vec)
+      launch_ug_gather<4>(s, g, table, rows, dim, unique, num_unique, n, out, status);
+    else
+      launch_ug_gather<1>(s, g, table, rows, dim, unique, num_unique, n, out, status);
     ANNC_HIP_TRY(hipGetLastError());
   }
   return ANNC_OK;
