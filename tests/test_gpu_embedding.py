@@ -314,3 +314,31 @@ def test_embedding_bag_table_over_2gib(combiner):
     np.testing.assert_array_equal(got, ref)
     del table
     torch.cuda.empty_cache()
+
+
+# ------------------------------------------------------------ randomized sweep
+@pytest.mark.parametrize("seed", range(12))
+def test_bag_random_shapes_bit_exact(seed):
+    """Seeded random shapes: dims 1..300, bags empty to 1500 long, int32 or
+    int64 ids, padded output rows; every bag bit-exact against the oracle."""
+    g = workloads.rng(7000 + seed)
+    dim = int(g.choice([1, 2, 3, 5, 8, 12, 16, 24, 31, 48, 64, 96, 128, 200, 300]))
+    rows = int(g.integers(1, 40000))
+    nbags = int(g.integers(1, 700))
+    lens = g.integers(0, 12, size=nbags)
+    longs = g.random(nbags) < 0.05
+    lens[longs] = g.integers(30, 1500, size=int(longs.sum()))
+    offsets = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    idx_dtype = np.int32 if seed % 2 else np.int64
+    ids = g.integers(0, rows, size=int(offsets[-1])).astype(idx_dtype)
+    combiner = seed % 3 % 2
+    ldo = dim + int(g.integers(0, 5))
+    note(f"bag random seed={seed}: dim={dim} rows={rows} bags={nbags} nnz={int(offsets[-1])} "
+         f"ids={np.dtype(idx_dtype).name} combiner={combiner} ldo={ldo}")
+    table = g.standard_normal((rows, dim)).astype(np.float32)
+    ref = ora.embedding_bag(table, ids.astype(np.int64), offsets, combiner)
+    out = to_dev(np.full((nbags, ldo), 3.0, dtype=np.float32))
+    dev.embedding_bag(to_dev(table), to_dev(ids), to_dev(offsets), combiner, out=out[:, :dim])
+    got = to_host(out)
+    np.testing.assert_array_equal(got[:, :dim], ref)
+    np.testing.assert_array_equal(got[:, dim:], 3.0)

@@ -211,3 +211,32 @@ def test_hashed_bags_table_of_2gib():
     np.testing.assert_array_equal(to_host(out), ref)
     del table
     torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("seed", range(10))
+def test_hashed_bags_random_shapes_bit_exact(seed):
+    """Seeded random multi-field shapes across the three hashed-bag kernels
+    (dims up to 16, 17-64 and wider): 1-30 fields, ragged bags with a few
+    over 128 positions, either combiner; bucket ids and sums bit-exact."""
+    g = workloads.rng(9100 + seed)
+    dim = int(g.choice([4, 8, 12, 16, 20, 32, 48, 64, 68, 128]))
+    nf = int(g.integers(1, 31))
+    batch = int(g.integers(1, 600))
+    rows = int(g.integers(50, 20000))
+    lens = g.integers(0, 6, size=nf * batch)
+    longs = g.random(nf * batch) < 0.01
+    lens[longs] = g.integers(60, 300, size=int(longs.sum()))
+    offsets = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    nnz = int(offsets[-1])
+    ids = g.integers(-2**63, 2**63 - 1, size=nnz, dtype=np.int64)
+    combiner = seed % 2
+    nbk = [int(g.integers(1, rows + 1)) for _ in range(nf)]
+    note(f"hashed random seed={seed}: dim={dim} fields={nf} batch={batch} rows={rows} "
+         f"nnz={nnz} combiner={combiner}")
+    tables = [g.standard_normal((rows, dim)).astype(np.float32) for _ in range(nf)]
+    ref = np.stack([ora.hashed_embedding_bags([tables[f]], nbk[f], ids,
+                                              offsets[f * batch:(f + 1) * batch + 1], batch,
+                                              combiner) for f in range(nf)], axis=1)
+    out = dev.hashed_embedding_bags([to_dev(t) for t in tables], nbk, to_dev(ids),
+                                    to_dev(offsets), batch, combiner)
+    np.testing.assert_array_equal(to_host(out).reshape(batch, nf, dim), ref)
