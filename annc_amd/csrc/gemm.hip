@@ -501,6 +501,11 @@ __global__ __launch_bounds__(64 * W) void gemm_small_kernel(GemmParams p) {
 //     fragment read (row = lane%32, chunk 4*(lane/32)+q) hits 64 distinct
 //     banks: swz(row) = (row & 7) ^ ((row >> 3) & 1).
 //   * B block = 1 KiB of the packed panel, already in MFMA-fragment order.
+//     With BRM the kernel reads row-major B (rows 16-byte aligned) instead:
+//     a B block is eight 128-byte row segments of one 32-column panel, rows
+//     k and k+16 of the stage side by side, and a fragment is four 4-byte
+//     LDS reads (the packed block's k order, so both forms give the same
+//     bits); no packing pass runs.
 //   * The DMAs are inline asm so the compiler neither tracks them nor adds
 //     its conservative vmcnt(0) before LDS reads; the kernel counts them
 //     itself (wait_vmcnt) and fences the barrier as asm as well.
@@ -550,7 +555,8 @@ __device__ __forceinline__ int a_swizzle(int row) { return (row & 7) ^ ((row >> 
 
 }  // namespace pipe
 
-template <int WM, int WN, int BLK_M, int BLK_N, int S, int NACC, int KS, bool A16>
+template <int WM, int WN, int BLK_M, int BLK_N, int S, int NACC, int KS, bool A16, bool BRM,
+          bool ZMAP>
 __global__ __launch_bounds__(64 * WM * WN * KS) void gemm_packed_pipe_kernel(GemmParams p) {
   static_assert(NACC == 1 || NACC == 2, "one or two accumulator chains");
   static_assert(KS == 1 || KS == 2, "one or two k groups");
@@ -581,12 +587,29 @@ __global__ __launch_bounds__(64 * WM * WN * KS) void gemm_packed_pipe_kernel(Gem
   const int l32 = lane & 31;
   const int half = lane >> 5;
 
+  // Workgroups are dealt to the 8 XCDs round-robin by linear id.  XCD c
+  // takes the contiguous range c*total/8 .. (c+1)*total/8 - 1 of the tiles
+  // (row-major tiles; with ZMAP, of the whole (batch, tile) space, tiles then
+  // batches), so tiles that share A rows, B panels or a batch's operands
+  // share that XCD's L2.  ZMAP is for batched launches only: the one-batch
+  // form avoids its division by T.
   int tile = blockIdx.x;
+  uint32_t zi = blockIdx.z;
   const int T = p.tiles_m * p.tiles_n;
-  if ((T & 7) == 0) tile = (tile & 7) * (T >> 3) + (tile >> 3);
+  if constexpr (ZMAP) {
+    const int total = T * (int)gridDim.z;
+    if ((total & 7) == 0) {
+      const int lin = (int)blockIdx.x + T * (int)blockIdx.z;
+      const int lg = (lin & 7) * (total >> 3) + (lin >> 3);
+      zi = (uint32_t)(lg / T);
+      tile = lg % T;
+    }
+  } else {
+    if ((T & 7) == 0) tile = (tile & 7) * (T >> 3) + (tile >> 3);
+  }
   const int m0 = (tile / p.tiles_n) * BM;
   const int n0 = (tile % p.tiles_n) * BN;
-  const int64_t z = blockIdx.z;
+  const int64_t z = zi;
   const float* __restrict__ A = p.a + z * p.stride_a;
   const float* __restrict__ B = p.b + z * p.stride_b;
   const int M = p.m, N = p.n, K = p.k;
@@ -604,7 +627,7 @@ __global__ __launch_bounds__(64 * WM * WN * KS) void gemm_packed_pipe_kernel(Gem
 
   // this wave's DMA sources (advanced by one k-block per stage) and LDS slots
   const float* src[LPW];
-  int step[LPW];
+  std::conditional_t<BRM, int64_t, int> step[LPW];  // floats per k-block
   uint32_t dst[LPW];
 #pragma unroll
   for (int i = 0; i < LPW; ++i) {
@@ -619,8 +642,18 @@ __global__ __launch_bounds__(64 * WM * WN * KS) void gemm_packed_pipe_kernel(Gem
     } else {
       const int bb = b - NA;
       const int pn = min((n0 >> 5) + (bb >> 2), panels - 1);
-      src[i] = B + (int64_t)pn * KT * 1024 + (bb & 3) * 256 + lane * 4;
-      step[i] = 1024;
+      if constexpr (BRM) {
+        // Row-major B: block bb&3 of a panel's stage holds the 128-byte row
+        // segments of LDS slots 8*(bb&3) .. +7, slot s holding k = s/2 +
+        // 16*(s%2), so rows k and k+16 sit side by side
+        const int slot = 8 * (bb & 3) + (lane >> 3);
+        const int kr = (slot >> 1) + 16 * (slot & 1);
+        src[i] = B + (int64_t)kr * p.ldb + pn * 32 + (lane & 7) * 4;
+        step[i] = 32 * p.ldb;
+      } else {
+        src[i] = B + (int64_t)pn * KT * 1024 + (bb & 3) * 256 + lane * 4;
+        step[i] = 1024;
+      }
     }
   }
   // 4-byte DMA sources of the A blocks: instruction j of block i fills LDS
@@ -695,8 +728,18 @@ __global__ __launch_bounds__(64 * WM * WN * KS) void gemm_packed_pipe_kernel(Gem
 #pragma unroll
       for (int i = 0; i < BLK_M; ++i) af[buf][i] = stage[a_off[i] + ((4 * half + q) ^ a_swz[i])];
 #pragma unroll
-      for (int j = 0; j < BLK_N; ++j)
-        bf[buf][j] = stage[(NA + (wn * BLK_N + j) * 4 + q) * 64 + lane];
+      for (int j = 0; j < BLK_N; ++j) {
+        if constexpr (BRM) {
+          // k = 16*half + 4q + e sits in slot 8q + 2e + half: the lane
+          // halves read adjacent 128-byte rows
+          const float* sf = reinterpret_cast<const float*>(stage) +
+                            (NA + (wn * BLK_N + j) * 4) * 256 + (8 * q + half) * 32 + l32;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) bf[buf][j][e] = sf[64 * e];
+        } else {
+          bf[buf][j] = stage[(NA + (wn * BLK_N + j) * 4 + q) * 64 + lane];
+        }
+      }
     };
     if (KB > 0) {
       const int inflight = min(KB - 1, S - 2);  // stages 1 .. S-2 may stay in flight
@@ -733,12 +776,16 @@ __global__ __launch_bounds__(64 * WM * WN * KS) void gemm_packed_pipe_kernel(Gem
                 for (int j = 0; j < BLK_N; ++j)
                   acc[e % NACC][i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(
                       af[b][i][e], bf[b][j][e], acc[e % NACC][i][j], 0, 0, 0);
+            // interleave the next quad's LDS reads with this quad's MFMAs
+            constexpr int NDS = BLK_M + (BRM ? 4 : 1) * BLK_N, NMF = 4 * BLK_M * BLK_N;
+            constexpr int NIL = NDS < NMF ? NDS : NMF;
 #pragma unroll
-            for (int r = 0; r < BLK_M + BLK_N; ++r) {
+            for (int r = 0; r < NIL; ++r) {
               __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
               __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
             }
-            __builtin_amdgcn_sched_group_barrier(0x008, 4 * BLK_M * BLK_N - (BLK_M + BLK_N), 0);
+            if constexpr (NMF > NIL) __builtin_amdgcn_sched_group_barrier(0x008, NMF - NIL, 0);
+            if constexpr (NDS > NIL) __builtin_amdgcn_sched_group_barrier(0x100, NDS - NIL, 0);
             if (t == HALF - 1 && kb + 1 < KB) {
               // stages kb+2 .. kb+S-2 may stay in flight (S <= 4: at most one)
               if (S >= 4 && kb + 2 < KB)
@@ -774,7 +821,10 @@ __global__ __launch_bounds__(64 * WM * WN * KS) void gemm_packed_pipe_kernel(Gem
 #pragma unroll
         for (int j = 0; j < BLK_N; ++j) {
           const int col = n0 + (wn * BLK_N + j) * 32 + l32;
-          bf[j][e] = (kin && col < N) ? B[tail_base + (int64_t)kk * N + col] : 0.0f;
+          if constexpr (BRM)
+            bf[j][e] = (kin && col < N) ? B[(int64_t)(kf + kk) * p.ldb + col] : 0.0f;
+          else
+            bf[j][e] = (kin && col < N) ? B[tail_base + (int64_t)kk * N + col] : 0.0f;
         }
       }
 #pragma unroll
@@ -885,36 +935,59 @@ __global__ void broadcast3_kernel(const float* __restrict__ src, int64_t s0, int
 }
 
 // Packs row-major B[z] (leading dimension ldb, batch stride stride_b, N a
-// multiple of 32) into the layout_matmul format at dst + z*K*N.  Workgroup
-// (t, p) of 256 threads writes the 32x32 block of k-block t and n-panel p:
-// thread (q, lane) gathers k = 32t + 16*(lane/32) + 4q + e, e = 0..3, at
-// n = 32p + lane%32, so each of its four reads is a coalesced 128-byte row
-// segment across the wave and the block's stores fill one contiguous 1 KiB
-// span per wave.  The extra workgroup column t = K/32 copies the K tail
-// rows of panel p into the row-major tail region.
+// multiple of 32, rows not 16-byte aligned) into the layout_matmul format at
+// dst + z*K*N.  Workgroup (t, g) of 256 threads handles k-block t and the
+// n-panels ppw*g .. ppw*g + ppw - 1 (ppw = 1, 2 or 4; fewer at the right
+// edge).  It reads the 32 x 32*ppw source block as coalesced row segments,
+// transposes it through LDS, and writes each panel's 1 KiB fragment block
+// with one 16-byte store per thread: thread (q, lane) of the block holds
+// k = 32t + 16*(lane/32) + 4q + e, e = 0..3, at n = 32p + lane%32.  The extra
+// workgroup column t = K/32 copies the K-tail rows of its panels into the
+// row-major tail region.
 __global__ __launch_bounds__(256) void pack_rhs_rowmajor_kernel(const float* __restrict__ src,
                                                                 int64_t ldb, int64_t stride_b,
                                                                 float* __restrict__ dst, int K,
-                                                                int N) {
-  const int kb = K >> 5, t = blockIdx.x, pn = blockIdx.y;
+                                                                int N, int ppw) {
+  __shared__ float tile[32][128 + 4];
+  const int kb = K >> 5, t = blockIdx.x;
+  const int p0 = ppw * (int)blockIdx.y;
+  const int np = min(ppw, (N >> 5) - p0);
+  const int n0 = 32 * p0, width = 32 * np;
   const float* __restrict__ bz = src + (int64_t)blockIdx.z * stride_b;
   float* __restrict__ dz = dst + (int64_t)blockIdx.z * K * N;
   const int tid = threadIdx.x;
   if (t < kb) {
+    const int c = tid & 31, r = tid >> 5;
+    if (4 * c < width) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int row = r + 8 * i;
+        const float* __restrict__ b = bz + (int64_t)(32 * t + row) * ldb + n0 + 4 * c;
+        f32x4 v;
+        v[0] = b[0];
+        v[1] = b[1];
+        v[2] = b[2];
+        v[3] = b[3];
+        *reinterpret_cast<f32x4*>(&tile[row][4 * c]) = v;
+      }
+    }
+    __syncthreads();
     const int q = tid >> 6, lane = tid & 63;
-    const int k = 32 * t + 16 * (lane >> 5) + 4 * q, n = 32 * pn + (lane & 31);
-    const float* __restrict__ b = bz + (int64_t)k * ldb + n;
-    f32x4 v;
-    v[0] = b[0];
-    v[1] = b[ldb];
-    v[2] = b[2 * ldb];
-    v[3] = b[3 * ldb];
-    *reinterpret_cast<f32x4*>(dz + ((int64_t)pn * kb + t) * 1024 + tid * 4) = v;
+    const int kk = 16 * (lane >> 5) + 4 * q;
+    for (int j = 0; j < np; ++j) {
+      const int n = 32 * j + (lane & 31);
+      f32x4 v;
+      v[0] = tile[kk][n];
+      v[1] = tile[kk + 1][n];
+      v[2] = tile[kk + 2][n];
+      v[3] = tile[kk + 3][n];
+      *reinterpret_cast<f32x4*>(dz + ((int64_t)(p0 + j) * kb + t) * 1024 + tid * 4) = v;
+    }
     return;
   }
-  const int kf = kb * 32;  // K tail rows of panel p: row-major [K - kf, N]
-  for (int i = tid; i < (K - kf) * 32; i += 256) {
-    const int k = kf + (i >> 5), n = 32 * pn + (i & 31);
+  const int kf = kb * 32;  // K tail rows: row-major [K - kf, N]
+  for (int i = tid; i < (K - kf) * width; i += 256) {
+    const int k = kf + i / width, n = n0 + i % width;
     dz[(int64_t)N * kf + (int64_t)(k - kf) * N + n] = bz[(int64_t)k * ldb + n];
   }
 }
@@ -940,39 +1013,68 @@ int launch_tile(const GemmParams& p0, int64_t batch, hipStream_t stream) {
   return ANNC_OK;
 }
 
-template <int WM, int WN, int BMB, int BNB, int S, int NACC, int KS>
+template <int WM, int WN, int BMB, int BNB, int S, int NACC, int KS, bool BRM>
 int launch_pipe(const GemmParams& p0, int64_t batch, hipStream_t stream) {
   constexpr int BM = WM * BMB * 32, BN = WN * BNB * 32;
   GemmParams p = p0;
   p.tiles_m = (p.m + BM - 1) / BM;
   p.tiles_n = (p.n + BN - 1) / BN;
   dim3 grid(p.tiles_m * p.tiles_n, 1, (unsigned)batch);
-  if (p.a_vec)
-    hipLaunchKernelGGL((gemm_packed_pipe_kernel<WM, WN, BMB, BNB, S, NACC, KS, true>),
-                       grid, dim3(64 * WM * WN * KS), 0, stream, p);
-  else
-    hipLaunchKernelGGL((gemm_packed_pipe_kernel<WM, WN, BMB, BNB, S, NACC, KS, false>),
-                       grid, dim3(64 * WM * WN * KS), 0, stream, p);
+  const dim3 block(64 * WM * WN * KS);
+  if (p.a_vec) {
+    if (batch > 1)
+      hipLaunchKernelGGL((gemm_packed_pipe_kernel<WM, WN, BMB, BNB, S, NACC, KS, true, BRM, true>),
+                         grid, block, 0, stream, p);
+    else
+      hipLaunchKernelGGL((gemm_packed_pipe_kernel<WM, WN, BMB, BNB, S, NACC, KS, true, BRM, false>),
+                         grid, block, 0, stream, p);
+  } else {
+    if (batch > 1)
+      hipLaunchKernelGGL((gemm_packed_pipe_kernel<WM, WN, BMB, BNB, S, NACC, KS, false, BRM, true>),
+                         grid, block, 0, stream, p);
+    else
+      hipLaunchKernelGGL(
+          (gemm_packed_pipe_kernel<WM, WN, BMB, BNB, S, NACC, KS, false, BRM, false>), grid,
+          block, 0, stream, p);
+  }
   ANNC_HIP_TRY(hipGetLastError());
   return ANNC_OK;
 }
 
 // Packed B with N % 32 == 0: the LDS-DMA pipeline (16-byte DMAs for A rows
-// that are 16-byte aligned, 4-byte DMAs otherwise), 32 k per stage, 4 stages
-// (3 for 128x128 tiles over unaligned A rows, measured faster there).
-// Largest tile that still gives every CU (256 on MI355X) a workgroup.
-int launch_packed_pipe(const GemmParams& p, int64_t batch, hipStream_t stream) {
+// that are 16-byte aligned, 4-byte DMAs otherwise), 32 k per stage.
+// Tile choice: the one whose busiest CU (256 on MI355X) computes the least
+// tile area, ceil(tiles / 256) * BM * BN, so that a 1.25-round grid does not
+// pay for two full rounds of large tiles.  On a tie between 128x128 and
+// 128x64, K > 512 takes 128x128 (fewer operand bytes per MFMA); shorter K
+// takes 128x64, whose 3-stage form (72 KiB of LDS) lets two workgroups share
+// a CU when there are at least two tiles per CU, hiding each one's ramp and
+// store phase under the other's MFMAs (measured: 8% faster at K = 256, 3% at
+// K = 512, 3% slower at K = 845).
+template <bool BRM>
+int launch_pipe_tiles(const GemmParams& p, int64_t batch, hipStream_t stream) {
   const int64_t cus = 256;
   auto tiles = [&](int bm, int bn) {
     return ((int64_t)(p.m + bm - 1) / bm) * ((p.n + bn - 1) / bn) * batch;
   };
-  if (tiles(128, 128) >= cus)
-    return p.a_vec ? launch_pipe<4, 2, 1, 2, 4, 1, 1>(p, batch, stream)
-                   : launch_pipe<4, 2, 1, 2, 3, 1, 1>(p, batch, stream);
-  if (tiles(128, 64) >= cus) return launch_pipe<4, 2, 1, 1, 4, 2, 1>(p, batch, stream);
+  auto cost = [&](int bm, int bn) { return ceil_div(tiles(bm, bn), cus) * bm * bn; };
+  const int64_t c128 = cost(128, 128), c128x64 = cost(128, 64), c64 = cost(64, 64);
   // 64x64 tiles leave one wave per SIMD; split each k-block over two wave
   // groups so every SIMD runs two
-  return launch_pipe<2, 2, 1, 1, 4, 1, 2>(p, batch, stream);
+  if (c64 < c128x64 && c64 < c128) return launch_pipe<2, 2, 1, 1, 4, 1, 2, BRM>(p, batch, stream);
+  if (c128 < c128x64 || (c128 == c128x64 && p.k > 512))
+    return p.a_vec ? launch_pipe<4, 2, 1, 2, 4, 1, 1, BRM>(p, batch, stream)
+                   : launch_pipe<4, 2, 1, 2, 3, 1, 1, BRM>(p, batch, stream);
+  if (tiles(128, 64) >= 2 * cus) return launch_pipe<4, 2, 1, 1, 3, 2, 1, BRM>(p, batch, stream);
+  return launch_pipe<4, 2, 1, 1, 4, 2, 1, BRM>(p, batch, stream);
+}
+
+// b_rowmajor: B is row-major with 16-byte aligned rows (p.b_vec), read in
+// place; otherwise B is in the layout_matmul packed format.
+int launch_packed_pipe(const GemmParams& p, int64_t batch, hipStream_t stream,
+                       bool b_rowmajor = false) {
+  return b_rowmajor ? launch_pipe_tiles<true>(p, batch, stream)
+                    : launch_pipe_tiles<false>(p, batch, stream);
 }
 
 template <int W>
@@ -1076,20 +1178,25 @@ int annc_hip_gemm(void* stream, int64_t batch, int64_t m, int64_t n, int64_t k, 
     if (n % 32 == 0) return launch_packed_pipe(p, batch, s);
     return launch_gemm<true>(p, batch, s);
   }
-  // Large row-major-B GEMMs (the __matmul* custom calls, whose weights XLA
-  // passes row-major): pack B into the stream workspace and run the LDS-DMA
-  // pipeline.  Packing moves 8*K*N bytes; the pipeline runs the tower
-  // shapes about 1.5x faster than the row-major kernel.
+  // Large row-major-B GEMMs (the __matmul* and __batch_matmul custom calls,
+  // whose weights XLA passes row-major) run the LDS-DMA pipeline, about 1.5x
+  // faster than the row-major kernel on the tower shapes: in place when B's
+  // rows are 16-byte aligned, else after packing B into the stream workspace
+  // (8*K*N bytes moved).
   const int64_t tiles64 = ceil_div(m, 64) * ceil_div(n, 64) * batch;
   const int64_t packed_bytes = batch * k * n * static_cast<int64_t>(sizeof(float));
-  if (n % 32 == 0 && k >= 32 && m >= 512 && tiles64 >= 128 &&
-      packed_bytes <= (int64_t(1) << 31)) {
+  const bool pipe_shape = n % 32 == 0 && k >= 32 && tiles64 >= 128;
+  if (pipe_shape && p.b_vec) return launch_packed_pipe(p, batch, s, /*b_rowmajor=*/true);
+  if (pipe_shape && m >= 512 && packed_bytes <= (int64_t(1) << 31)) {
     float* bp = static_cast<float*>(stream_workspace(s, static_cast<size_t>(packed_bytes)));
     if (bp) {
-      const dim3 grid((unsigned)((k >> 5) + ((k & 31) ? 1 : 0)), (unsigned)(n >> 5),
-                      (unsigned)batch);
+      // Panels per workgroup: the widest that still gives >= 512 workgroups.
+      const int64_t kcols = (k >> 5) + ((k & 31) ? 1 : 0), panels = n >> 5;
+      int ppw = 4;
+      while (ppw > 1 && kcols * ceil_div(panels, ppw) * batch < 512) ppw >>= 1;
+      const dim3 grid((unsigned)kcols, (unsigned)ceil_div(panels, ppw), (unsigned)batch);
       hipLaunchKernelGGL(pack_rhs_rowmajor_kernel, grid, dim3(256), 0, s, b, ldb, stride_b, bp,
-                         (int)k, (int)n);
+                         (int)k, (int)n, ppw);
       ANNC_HIP_TRY(hipGetLastError());
       GemmParams q = p;
       q.b = bp;

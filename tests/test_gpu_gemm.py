@@ -5,7 +5,7 @@ import numpy as np
 import pytest
 import torch
 
-from annc_amd import EPI_NONE, EPI_RELU, EPI_SIGMOID, workloads, xla
+from annc_amd import EPI_NONE, EPI_RELU, EPI_SIGMOID, _lib, workloads, xla
 from annc_amd import device as dev
 from annc_amd.rec_graph import MLPTower, WideDeepConfig, WideDeepGraph
 from oracle import ora
@@ -77,8 +77,8 @@ def test_layout_matmul_packed(m, n, k):
 
 
 # Packed B with N % 32 == 0 runs the LDS-DMA pipelined kernel: each of its
-# three tile configurations (128x128, 128x64, 64x64, chosen by how many tiles
-# the shape yields), partial M and N tiles, a K tail with and without full
+# tile configurations (128x128, 128x64 in 4 or 3 stages, 64x64, chosen from
+# the tile area the busiest CU computes, and K), partial M and N tiles, a K tail with and without full
 # k-blocks, padded lda, addend and sigmoid; A rows that are not 16-byte
 # aligned (lda % 4 != 0) take the 4-byte DMA variant.
 PIPE_CASES = [
@@ -96,10 +96,11 @@ PIPE_CASES = [
     (130, 64, 96, 100, "3 k-blocks (one full pipeline round), lda not a multiple of 32"),
     (7, 64, 300, 300, "tiny M"),
     # few k-blocks in each tile class: the prologue and the mid-stage waits
-    # of the 4-stage (3-stage for unaligned 128x128) pipeline
-    (4096, 1024, 40, 40, "128x128 tiles, 1 k-block + tail"),
-    (4096, 1024, 97, 97, "128x128 tiles, unaligned A, 3 k-blocks + tail (3 stages)"),
-    (4096, 1024, 128, 128, "128x128 tiles, 4 k-blocks"),
+    # of the 4- and 3-stage pipelines
+    (4096, 1024, 40, 40, "128x64 tiles, two per CU (3 stages), 1 k-block + tail"),
+    (4096, 1024, 97, 97, "128x64 3-stage tiles, unaligned A, 3 k-blocks + tail"),
+    (4096, 1024, 128, 128, "128x64 3-stage tiles, 4 k-blocks"),
+    (4096, 1024, 544, 544, "128x128 tiles (K > 512), 17 k-blocks"),
     (4096, 512, 160, 160, "128x64 tiles, 5 k-blocks"),
     (4096, 512, 64, 67, "128x64 tiles, 2 k-blocks, unaligned A"),
     (4096, 256, 224, 224, "64x64 split-K tiles, 7 k-blocks"),
@@ -304,17 +305,24 @@ def test_batch_matmul_add_sigmoid_broadcasts(bias_shape, rhs_batched):
     np.testing.assert_allclose(got, ref, rtol=0, atol=1e-5)
 
 
-# (each shape has m >= 512, n % 32 == 0 and at least 128 64x64 tiles, the
-# condition for packing B per call)
+# (each shape has n % 32 == 0 and at least 128 64x64 tiles, the condition for
+# the pipelined kernel.  Rows of B that are 16-byte aligned (n + ldb_pad a
+# multiple of 4) are read in place; the others need m >= 512 and are packed
+# per call, the packer grouping 1, 2 or 4 n-panels per workgroup by grid size:
+# (1, 8192, 64, 33, 7) takes 1 and (70, 512, 224, 64, 3) 2 with a remainder
+# group.  The tile rule gives 64x64, 128x64 in 4 and 3 stages, and a grid of
+# 1.25 CU rounds among these shapes.)
 @pytest.mark.parametrize("batch,m,n,k,ldb_pad", [(1, 2048, 320, 845, 80), (1, 4096, 512, 1024, 0),
                                                  (3, 1024, 256, 200, 0), (1, 8192, 64, 33, 7),
-                                                 (2, 4000, 96, 64, 32)])
+                                                 (2, 4000, 96, 64, 32), (32, 512, 256, 256, 0),
+                                                 (64, 512, 160, 101, 4), (70, 512, 224, 64, 3),
+                                                 (64, 256, 128, 256, 0), (4, 2048, 320, 845, 0)])
 def test_row_major_b_packed_per_call(batch, m, n, k, ldb_pad):
-    """Large row-major-B GEMMs pack B into the stream workspace and run the
-    pipelined kernel: within tolerance of OpenBLAS, and bit-identical to the
-    same GEMM on weights packed ahead of time (so the per-call packing
-    equals the layout_matmul packer, K tails and strided B included, and the
-    pipelined kernel ran)."""
+    """Large row-major-B GEMMs run the pipelined kernel, on B read in place or
+    packed into the stream workspace: within tolerance of OpenBLAS, and
+    bit-identical to the same GEMM on weights packed ahead of time (so the
+    in-place reads and the per-call packing both equal the layout_matmul
+    packer, K tails and strided B included, and the pipelined kernel ran)."""
     note(f"row-major B packed per call b={batch} {m}x{n}x{k} ldb+{ldb_pad}")
     g = workloads.rng(m + n + k + batch)
     a = g.standard_normal((batch, m, k)).astype(np.float32)
@@ -327,12 +335,20 @@ def test_row_major_b_packed_per_call(batch, m, n, k, ldb_pad):
         got = to_host(dev.gemm(da[0], db[0], addend=de[0], epilogue=EPI_RELU))[None]
     else:
         got = to_host(dev.gemm(da, db, addend=de, epilogue=EPI_RELU))
+    packed = [dev.pack_weight(to_dev(b[z])).data for z in range(batch)]
+    if batch == 1:
+        pre = to_host(dev.gemm(da[0], dev.PackedWeight(packed[0], k, n), addend=de[0],
+                               epilogue=EPI_RELU))[None]
+    else:  # one batched call over the concatenated packed weights: same tile class
+        pre_d = torch.empty((batch, m, n), dtype=torch.float32, device=device())
+        _lib.check(_lib.lib().annc_hip_gemm(
+            _lib.stream_ptr(), batch, m, n, k, _lib.ptr(da), k, m * k, _lib.ptr(torch.cat(packed)),
+            n, k * n, 1, _lib.ptr(de), n, m * n, None, EPI_RELU, _lib.ptr(pre_d), n, m * n))
+        pre = to_host(pre_d)
     for z in range(batch):
         ref = ora.matmul_add_relu(e[z], a[z], np.ascontiguousarray(b[z]))
         assert_gemm_close(got[z], ref, gemm_bound(a[z], b[z], e[z]))
-        pw = dev.pack_weight(to_dev(b[z]))
-        pre = to_host(dev.gemm(da[z], pw, addend=de[z], epilogue=EPI_RELU))
-        np.testing.assert_array_equal(got[z], pre)
+    np.testing.assert_array_equal(got, pre)
 
 
 @pytest.mark.parametrize("m,n,k,col0", [(2048, 512, 256, 1), (8192, 64, 333, 3)])
