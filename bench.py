@@ -130,7 +130,7 @@ def bench_tower(args, device):
     k1_flops = 2.0 * m * n * k
     achieved = k1_flops / (k1_ms * 1e-3) / 1e12
     roofline = {
-        "kernel": "gemm_packed_pipe_kernel<4,2,1,1,4,2,1,true> (layer 1: 4096x512x1024 packed B + bias + ReLU)",
+        "kernel": "gemm_packed_pipe_kernel<4,2,1,1,4,2,1,true,false,false> (layer 1: 4096x512x1024 packed B + bias + ReLU)",
         "bound": "mfma",
         "achieved": round(achieved, 3),
         "peak": FP32_MFMA_PEAK_TFLOPS,
@@ -461,7 +461,7 @@ def cpu_baseline(inputs, bag_inputs):
     return out
 
 
-KERNELS = ("gemm_l1", "gemm_l2", "bag_sum", "bag_mean", "hashed", "copy")
+KERNELS = ("gemm_l1", "gemm_l2", "batch_matmul", "bag_sum", "bag_mean", "hashed", "copy")
 
 
 def profile_kernel(name: str, launches: int, device) -> dict:
@@ -486,6 +486,17 @@ def profile_kernel(name: str, launches: int, device) -> dict:
         out = torch.empty((x.shape[0], wt.n), dtype=torch.float32, device=device)
         fn = lambda: dev.gemm(x, wt, bias=bias, epilogue=EPI_RELU, out=out)  # noqa: E731
         info.update(m=x.shape[0], n=wt.n, k=wt.k, flops_per_launch=2 * x.shape[0] * wt.n * wt.k)
+    elif name == "batch_matmul":
+        # the components' __batch_matmul case: 32 x configs[0]'s shape, row-major B
+        import numpy as np
+        g = workloads.rng(5)
+        bm, m, k, n = 32, 512, 256, 256
+        a = torch.from_numpy(g.standard_normal((bm, m, k)).astype(np.float32)).to(device)
+        b = torch.from_numpy((g.standard_normal((bm, k, n)) / 16).astype(np.float32)).to(device)
+        out = torch.empty((bm, m, n), dtype=torch.float32, device=device)
+        fn = lambda: dev.gemm(a, b, out=out)  # noqa: E731
+        info.update(batch=bm, m=m, n=n, k=k, flops_per_launch=2 * bm * m * n * k,
+                    algorithmic_bytes=4 * bm * (m * k + k * n + m * n))
     elif name in ("bag_sum", "bag_mean"):
         w = workloads.config3(seed=0)
         table = torch.from_numpy(w.table).to(device)

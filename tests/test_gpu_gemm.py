@@ -370,8 +370,11 @@ def test_pipeline_misaligned_a_base(m, n, k, col0):
 
 def test_custom_calls_from_concurrent_threads():
     """The synchronous custom calls run on a stream of the calling thread:
-    threads calling __matmul_add_relu at once (host buffers, shapes that
-    pack B into the stream workspace) each get their own result."""
+    threads calling __matmul_add_relu at once (host buffers staged through
+    each thread's scratch; threads 2 and 3 have at least 128 64x64 tiles and
+    run the pipelined kernel) each get their own result; so do their device
+    calls on their own streams, where threads 2 and 3 pack an unaligned
+    row-major B into that stream's workspace."""
     import threading
     note("custom calls from 4 threads")
     g = workloads.rng(77)
@@ -387,9 +390,21 @@ def test_custom_calls_from_concurrent_threads():
     def work(c):
         a, b, e, z, out = c
         try:
-            for _ in range(5):
-                xla.matmul_add_relu(z, e, a, b, out)
-                assert_gemm_close(out, ora.matmul_add_relu(e, a, b), gemm_bound(a, b, e))
+            ref = ora.matmul_add_relu(e, a, b)
+            bound = gemm_bound(a, b, e)
+            k, n = b.shape
+            wide = np.zeros((k, n + 3), np.float32)  # rows not 16-byte aligned
+            wide[:, :n] = b
+            s = torch.cuda.Stream(device=device())
+            with torch.cuda.stream(s):
+                da, de, db = to_dev(a), to_dev(e), to_dev(wide)[:, :n]
+                s.synchronize()
+                for _ in range(5):
+                    xla.matmul_add_relu(z, e, a, b, out)
+                    assert_gemm_close(out, ref, bound)
+                    got = dev.gemm(da, db, addend=de, epilogue=EPI_RELU)
+                    s.synchronize()
+                    assert_gemm_close(to_host(got), ref, bound)
         except Exception as ex:  # reported below
             errors.append(ex)
 
