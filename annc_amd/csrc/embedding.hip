@@ -495,7 +495,6 @@ template <typename IdxT, int G>
 __global__ __launch_bounds__(kThreads) void sparse_embedding2_vec_kernel(
     const float* __restrict__ table, int64_t rows, int64_t dim, const IdxT* __restrict__ ids,
     int64_t n, int64_t fallback, float* __restrict__ out) {
-  typedef typename VecT<4>::type V;
   const int g = threadIdx.x & (G - 1);
   const int64_t i = ((int64_t)blockIdx.x * kThreads + threadIdx.x) / G;
   if (i >= n) return;
@@ -539,7 +538,13 @@ __global__ __launch_bounds__(kThreads) void pooling_vec_kernel(
   const int64_t j1 = sl1 < k ? sl1 : k;
   const uint32_t row_base = static_cast<uint32_t>(i * k * n * 4);
   const uint32_t step = static_cast<uint32_t>(n * 4);
-  for (int64_t c = 4 * g; c < n; c += 4 * G) {
+  // Every lane of the group runs every column chunk (lanes past n load
+  // nothing and store nothing), so the broadcasts never read a lane that
+  // has left the loop.
+  const int64_t chunks = (n + 4 * G - 1) / (4 * G);
+  for (int64_t cc = 0; cc < chunks; ++cc) {
+    const int64_t c = cc * 4 * G + 4 * g;
+    const bool active = c < n;
     V sum = V(0.0f);
     if (row_in) {
       for (int64_t jb = j0; jb < j1; jb += kGroupRound) {
@@ -554,7 +559,9 @@ __global__ __launch_bounds__(kThreads) void pooling_vec_kernel(
         static_for([&](auto uc) {
           constexpr int u = decltype(uc)::value;
           const uint32_t o = group_bcast<G, u % G>(off[u / G]);
-          v[u] = buffer_row<4>(rsrc, o == kMaskedOff ? o : o + static_cast<uint32_t>(c * 4));
+          v[u] = buffer_row<4>(rsrc, (o == kMaskedOff || !active)
+                                         ? kMaskedOff
+                                         : o + static_cast<uint32_t>(c * 4));
         }, std::make_integer_sequence<int, kGroupRound>{});
 #pragma unroll
         for (int u = 0; u < kGroupRound; ++u) sum += v[u];
@@ -567,7 +574,76 @@ __global__ __launch_bounds__(kThreads) void pooling_vec_kernel(
       const float s = (p >= ss2 && p < sl2) ? sum[e] : 0.0f;
       res[e] = red == 0.0f ? 0.0f : s / red;
     }
-    store_row<4>(out + i * n + c, res);
+    if (active) store_row<4>(out + i * n + c, res);
+  }
+}
+
+// __pooling for rows of k <= R positions (R = 16, 32 or 48): one round.  The
+// row's ids are loaded once and give both the count of ids > 0 and the row
+// offsets, and all R row loads of a lane are issued before the first add, so
+// the kernel is one id round trip and one row round trip (the multi-round
+// kernel above reloads the ids per round and per column chunk).  Positions
+// past k, outside the slice or with id <= 0 read past the buffer range and
+// add +0.0f, which leaves the in-order sum unchanged.
+// (At most R*G/64 waves per bag row group run per SIMD on the benchmark
+// shapes, so the kernel asks for 1-2 waves per SIMD and the registers to
+// keep every row load in flight.)
+template <int G, int R>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 2))) void
+pooling_round_kernel(
+    const int64_t* __restrict__ ids, const float* __restrict__ gathered, int64_t m, int64_t k,
+    int64_t n, int64_t ss0, int64_t ss1, int64_t ss2, int64_t sl0, int64_t sl1, int64_t sl2,
+    float* __restrict__ out) {
+  typedef typename VecT<4>::type V;
+  constexpr int kPer = (R + G - 1) / G;
+  const int g = threadIdx.x & (G - 1);
+  const int64_t i = ((int64_t)blockIdx.x * kThreads + threadIdx.x) / G;
+  if (i >= m) return;
+  const int64_t* row_ids = ids + i * k;
+  const bool row_in = i >= ss0 && i < sl0;
+  const int64_t j0 = ss1 > 0 ? ss1 : 0;
+  const int64_t j1 = sl1 < k ? sl1 : k;
+  const uint32_t row_base = static_cast<uint32_t>(i * k * n * 4);
+  const uint32_t step = static_cast<uint32_t>(n * 4);
+  int cnt = 0;
+  uint32_t off[kPer];
+#pragma unroll
+  for (int t = 0; t < kPer; ++t) {
+    const int j = g + G * t;
+    const int64_t id_c = row_ids[j < k ? j : k - 1];  // unconditional: one round trip
+    const int64_t id = j < k ? id_c : 0;
+    cnt += id > 0 ? 1 : 0;
+    off[t] = (row_in && id > 0 && j >= j0 && j < j1) ? row_base + static_cast<uint32_t>(j) * step
+                                                     : kMaskedOff;
+  }
+#pragma unroll
+  for (int o = G / 2; o > 0; o >>= 1) cnt += __shfl_xor(cnt, o, G);
+  const float red = static_cast<float>(cnt);
+  const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float*>(gathered), 0, static_cast<int>(m * k * n * 4), kRawBufferFlags);
+  // every lane runs every column chunk (see pooling_vec_kernel)
+  const int64_t chunks = (n + 4 * G - 1) / (4 * G);
+  for (int64_t cc = 0; cc < chunks; ++cc) {
+    const int64_t c = cc * 4 * G + 4 * g;
+    const bool active = c < n;
+    V v[R];
+    static_for([&](auto uc) {
+      constexpr int u = decltype(uc)::value;
+      const uint32_t o = group_bcast<G, u % G>(off[u / G]);
+      v[u] = buffer_row<4>(rsrc, (o == kMaskedOff || !active) ? kMaskedOff
+                                                              : o + static_cast<uint32_t>(c * 4));
+    }, std::make_integer_sequence<int, R>{});
+    V sum = V(0.0f);
+#pragma unroll
+    for (int u = 0; u < R; ++u) sum += v[u];
+    V res;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int64_t p = c + e;
+      const float s = (p >= ss2 && p < sl2) ? sum[e] : 0.0f;
+      res[e] = red == 0.0f ? 0.0f : s / red;
+    }
+    if (active) store_row<4>(out + i * n + c, res);
   }
 }
 
@@ -785,14 +861,27 @@ int launch_pooling(hipStream_t s, const int64_t* ids, const float* gathered, int
   if (n % 4 == 0 && aligned && m * k * n * 4 < (int64_t(1) << 31) && k < (int64_t(1) << 24)) {
     const int g = vec_group(n / 4);
     const dim3 grid((unsigned)ceil_div(m * g, kThreads));
+    // rows of up to 48 positions: the one-round kernel, R = k rounded up to 16
+    const int r = k == 0 ? 0 : k <= 16 ? 16 : k <= 32 ? 32 : k <= 48 ? 48 : 0;
     switch (g) {
+#define ANNC_POOL_R(G, R)                                                                       \
+  hipLaunchKernelGGL((pooling_round_kernel<G, R>), grid, dim3(kThreads), 0, s, ids, gathered, m, \
+                     k, n, ss[0], ss[1], ss[2], sl[0], sl[1], sl[2], out)
 #define ANNC_POOL(G)                                                                          \
   case G:                                                                                     \
-    hipLaunchKernelGGL(pooling_vec_kernel<G>, grid, dim3(kThreads), 0, s, ids, gathered, m, k, \
-                       n, ss[0], ss[1], ss[2], sl[0], sl[1], sl[2], out);                     \
+    if (r == 16)                                                                              \
+      ANNC_POOL_R(G, 16);                                                                     \
+    else if (r == 32)                                                                         \
+      ANNC_POOL_R(G, 32);                                                                     \
+    else if (r == 48)                                                                         \
+      ANNC_POOL_R(G, 48);                                                                     \
+    else                                                                                      \
+      hipLaunchKernelGGL(pooling_vec_kernel<G>, grid, dim3(kThreads), 0, s, ids, gathered, m, \
+                         k, n, ss[0], ss[1], ss[2], sl[0], sl[1], sl[2], out);                \
     break;
       ANNC_POOL(1) ANNC_POOL(2) ANNC_POOL(4) ANNC_POOL(8) ANNC_POOL(16) ANNC_POOL(32) ANNC_POOL(64)
 #undef ANNC_POOL
+#undef ANNC_POOL_R
     }
     ANNC_HIP_TRY(hipGetLastError());
     return ANNC_OK;

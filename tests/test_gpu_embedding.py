@@ -191,21 +191,29 @@ def test_sparse_embedding2_bit_exact(dim, idx_dtype):
     assert np.isnan(got[1, 0])
 
 
-POOL_CASES = [((0, 0, 0), (64, 30, 16)), ((3, 2, 1), (60, 25, 12))]
+# slices as (starts, limits) for rows of k positions: all of it, an inner
+# box, and a late start with every column
+POOL_SLICES = {"full": lambda k, n: ((0, 0, 0), (64, k, n)),
+               "inner": lambda k, n: ((3, 2, 1), (60, max(k - 5, 3), min(12, n))),
+               "late_start": lambda k, n: ((0, min(4, k - 1), 0), (64, k, n))}
 
 
-@pytest.mark.parametrize("n", [16, 64, 6, 260])
-@pytest.mark.parametrize("ss,sl", POOL_CASES)
-def test_pooling_bit_exact(ss, sl, n):
-    """n % 4 == 0 takes the lane-group kernel (masked positions are never
+# k <= 16, 32 and 48 take the one-round kernel (R = 16, 32, 48; 48 is its
+# edge), longer rows the multi-round one; n = 4, 8, 16, 64, 260 give lane
+# groups of 1, 2, 4, 16 and 64 (260: two column chunks), n = 6 the scalar kernel
+@pytest.mark.parametrize("k", [7, 30, 39, 48, 49, 100])
+@pytest.mark.parametrize("n", [4, 8, 16, 64, 6, 260])
+@pytest.mark.parametrize("slice_kind", list(POOL_SLICES))
+def test_pooling_bit_exact(k, n, slice_kind):
+    """n % 4 == 0 takes the lane-group kernels (masked positions are never
     read: NaNs there must not leak), other widths the scalar one."""
-    note(f"pooling n={n} {ss} {sl}")
-    g = workloads.rng(4 + n)
-    ids = g.integers(-2, 50, size=(64, 30)).astype(np.int64)
+    ss, sl = POOL_SLICES[slice_kind](k, n)
+    note(f"pooling k={k} n={n} {ss} {sl}")
+    g = workloads.rng(4 + n + 7 * k)
+    ids = g.integers(-2, 50, size=(64, k)).astype(np.int64)
     ids[5] = 0
-    gathered = g.standard_normal((64, 30, n)).astype(np.float32)
+    gathered = g.standard_normal((64, k, n)).astype(np.float32)
     gathered[ids <= 0] = np.nan
-    sl = (sl[0], sl[1], min(sl[2], n) if n >= 16 else n)
     ref = ora.pooling(ids, gathered, ss, sl)
     got = to_host(dev.pooling(to_dev(ids), to_dev(gathered), ss, sl))
     np.testing.assert_array_equal(got, ref)
