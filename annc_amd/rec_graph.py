@@ -1,7 +1,9 @@
 """Recommendation-model graphs assembled from the fused operators.
 
 These are the graphs the reference reaches through XLA clustering of a TF
-Serving model (SURVEY call stacks 3.2-3.4): dense layers lowered to
+Serving model (the patched cpu_compiler.cc running the KDnnRewriter passes,
+install/tensorflow.patch:187-198, then the rewriters of
+annc/service/cpu/gemm_rewriter.cc and graph_opt.cc): dense layers lowered to
 __layout_matmul / __matmul_add_relu custom calls plus bias/activation loop
 fusions, and hashed categorical fields lowered to the embed_hash_bucket op
 family.  Here every layer is one gfx950 kernel with the bias and activation

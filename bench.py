@@ -546,8 +546,9 @@ def main() -> int:
     ap.add_argument("--launches", type=int, default=20)
     args = ap.parse_args()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build targets one GPU; --gpus must be 1 "
-                                   "(the sharding plan is described in DESIGN.md)"}))
+        print(json.dumps({"error": "this build targets one GPU; --gpus must be 1 (GEMMs "
+                                   "would shard by batch rows with replicated weights, bags "
+                                   "by bag with replicated tables; not built here)"}))
         return 2
     import torch
     if not torch.cuda.is_available():
