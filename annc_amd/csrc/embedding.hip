@@ -352,40 +352,64 @@ __global__ __launch_bounds__(kThreads) void cs_hist_kernel(const int64_t* __rest
   for (int s = threadIdx.x; s < batch; s += kThreads) row[s] = cs_lds[s];
 }
 
-__global__ __launch_bounds__(kThreads) void cs_prefix_kernel(const uint32_t* __restrict__ H,
-                                                            int batch, int nblk,
-                                                            uint32_t* __restrict__ P,
-                                                            uint32_t* __restrict__ total) {
-  const int s = blockIdx.x * kThreads + threadIdx.x;
-  if (s >= batch) return;
-  constexpr int U = 32;  // block counts in flight per segment
-  uint32_t run = 0;
-  int b = 0;
-  for (; b + U <= nblk; b += U) {
-    uint32_t c[U];
+// P[b][s] = sum of H[b'][s] over blocks b' < b, total[s] = the sum over all
+// blocks.  A workgroup of 1024 threads takes 64 segments (one per lane, so
+// every load is a 256-byte row segment) and splits the blocks into 16
+// chunks, one per wave: each wave sums its chunk, the chunk sums meet in LDS,
+// and each wave then writes its chunk's running prefixes from its own
+// offset.  The counts are read once from HBM and once more from L2.
+__global__ __launch_bounds__(1024) void cs_prefix_kernel(const uint32_t* __restrict__ H,
+                                                       int batch, int nblk,
+                                                       uint32_t* __restrict__ P,
+                                                       uint32_t* __restrict__ total) {
+  __shared__ uint32_t part[16][64];
+  constexpr int U = 8;  // counts in flight per thread
+  const int j = threadIdx.x & 63, c = threadIdx.x >> 6;
+  const int s = blockIdx.x * 64 + j;
+  const bool ok = s < batch;
+  const int per = (nblk + 15) / 16;
+  const int b_lo = min(nblk, c * per), b_hi = min(nblk, b_lo + per);
+  uint32_t sum = 0;
+  for (int b = b_lo; b < b_hi; b += U) {
+    uint32_t v[U];
 #pragma unroll
-    for (int u = 0; u < U; ++u) c[u] = H[(int64_t)(b + u) * batch + s];
+    for (int u = 0; u < U; ++u)
+      v[u] = (ok && b + u < b_hi) ? H[(int64_t)(b + u) * batch + s] : 0u;
+#pragma unroll
+    for (int u = 0; u < U; ++u) sum += v[u];
+  }
+  part[c][j] = sum;
+  __syncthreads();
+  uint32_t run = 0;
+  for (int q = 0; q < c; ++q) run += part[q][j];
+  if (ok && c == 15) total[s] = run + sum;
+  if (!ok) return;
+  for (int b = b_lo; b < b_hi; b += U) {
+    uint32_t v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) v[u] = b + u < b_hi ? H[(int64_t)(b + u) * batch + s] : 0u;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      P[(int64_t)(b + u) * batch + s] = run;
-      run += c[u];
+      if (b + u < b_hi) P[(int64_t)(b + u) * batch + s] = run;
+      run += v[u];
     }
   }
-  for (; b < nblk; ++b) {
-    const uint32_t c = H[(int64_t)b * batch + s];
-    P[(int64_t)b * batch + s] = run;
-    run += c;
-  }
-  total[s] = run;
 }
 
+// Exclusive scan of the segment totals (batch <= kCsMaxSegments = 16 * 1024,
+// so each thread keeps its at most 16 totals in registers).
 __global__ __launch_bounds__(1024) void cs_offsets_kernel(const uint32_t* __restrict__ total,
                                                          int batch, int64_t* __restrict__ offsets) {
   __shared__ int64_t part[1024];
+  constexpr int kMaxPer = 16;
   const int per = (batch + 1023) / 1024;
   const int s0 = threadIdx.x * per;
+  uint32_t tv[kMaxPer];
+#pragma unroll
+  for (int u = 0; u < kMaxPer; ++u) tv[u] = (u < per && s0 + u < batch) ? total[s0 + u] : 0u;
   int64_t sum = 0;
-  for (int s = s0; s < s0 + per && s < batch; ++s) sum += total[s];
+#pragma unroll
+  for (int u = 0; u < kMaxPer; ++u) sum += tv[u];
   part[threadIdx.x] = sum;
   __syncthreads();
   for (int off = 1; off < 1024; off <<= 1) {  // inclusive Hillis-Steele scan
@@ -395,9 +419,10 @@ __global__ __launch_bounds__(1024) void cs_offsets_kernel(const uint32_t* __rest
     __syncthreads();
   }
   int64_t run = threadIdx.x == 0 ? 0 : part[threadIdx.x - 1];
-  for (int s = s0; s < s0 + per && s < batch; ++s) {
-    offsets[s] = run;
-    run += total[s];
+#pragma unroll
+  for (int u = 0; u < kMaxPer; ++u) {
+    if (u < per && s0 + u < batch) offsets[s0 + u] = run;
+    run += tv[u];
   }
   if (threadIdx.x == 1023) offsets[batch] = part[1023];
 }
@@ -752,8 +777,8 @@ int segment_reduce(hipStream_t s, const float* data, int64_t rows, int64_t dim,
                          n, nb, H);
       ANNC_HIP_TRY(hipGetLastError());
     }
-    hipLaunchKernelGGL(cs_prefix_kernel, dim3((unsigned)ceil_div(batch, kThreads)), dim3(kThreads),
-                       0, s, H, nb, static_cast<int>(nblk), P, total);
+    hipLaunchKernelGGL(cs_prefix_kernel, dim3((unsigned)ceil_div(batch, 64)), dim3(1024), 0, s, H,
+                       nb, static_cast<int>(nblk), P, total);
     ANNC_HIP_TRY(hipGetLastError());
     hipLaunchKernelGGL(cs_offsets_kernel, dim3(1), dim3(1024), 0, s, total, nb, offsets);
     ANNC_HIP_TRY(hipGetLastError());
