@@ -400,7 +400,7 @@ __global__ __launch_bounds__(1024) void cs_prefix_kernel(const uint32_t* __restr
 // so each thread keeps its at most 16 totals in registers).
 __global__ __launch_bounds__(1024) void cs_offsets_kernel(const uint32_t* __restrict__ total,
                                                          int batch, int64_t* __restrict__ offsets) {
-  __shared__ int64_t part[1024];
+  __shared__ int64_t wave_tot[16];
   constexpr int kMaxPer = 16;
   const int per = (batch + 1023) / 1024;
   const int s0 = threadIdx.x * per;
@@ -410,21 +410,26 @@ __global__ __launch_bounds__(1024) void cs_offsets_kernel(const uint32_t* __rest
   int64_t sum = 0;
 #pragma unroll
   for (int u = 0; u < kMaxPer; ++u) sum += tv[u];
-  part[threadIdx.x] = sum;
-  __syncthreads();
-  for (int off = 1; off < 1024; off <<= 1) {  // inclusive Hillis-Steele scan
-    const int64_t v = threadIdx.x >= off ? part[threadIdx.x - off] : 0;
-    __syncthreads();
-    part[threadIdx.x] += v;
-    __syncthreads();
+  // inclusive scan of the thread sums: within each wave by shuffles, then
+  // over the 16 wave totals through LDS
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int64_t incl = sum;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int64_t v = __shfl_up(incl, off, 64);
+    if (lane >= off) incl += v;
   }
-  int64_t run = threadIdx.x == 0 ? 0 : part[threadIdx.x - 1];
+  if (lane == 63) wave_tot[wave] = incl;
+  __syncthreads();
+  int64_t before = 0;
+  for (int q = 0; q < wave; ++q) before += wave_tot[q];
+  int64_t run = before + incl - sum;  // exclusive prefix of this thread
 #pragma unroll
   for (int u = 0; u < kMaxPer; ++u) {
     if (u < per && s0 + u < batch) offsets[s0 + u] = run;
     run += tv[u];
   }
-  if (threadIdx.x == 1023) offsets[batch] = part[1023];
+  if (threadIdx.x == 1023) offsets[batch] = before + incl;
 }
 
 __global__ __launch_bounds__(kThreads) void cs_scatter_kernel(const int64_t* __restrict__ seg,
