@@ -1019,6 +1019,8 @@ int launch_pipe(const GemmParams& p0, int64_t batch, hipStream_t stream) {
   GemmParams p = p0;
   p.tiles_m = (p.m + BM - 1) / BM;
   p.tiles_n = (p.n + BN - 1) / BN;
+  // the kernel numbers (batch, tile) pairs in 32-bit arithmetic
+  ANNC_REQUIRE((int64_t)p.tiles_m * p.tiles_n * batch < (int64_t(1) << 31), "GEMM grid too large");
   dim3 grid(p.tiles_m * p.tiles_n, 1, (unsigned)batch);
   const dim3 block(64 * WM * WN * KS);
   if (p.a_vec) {
