@@ -222,6 +222,29 @@ def test_pooling_bit_exact(k, n, slice_kind):
     np.testing.assert_array_equal(out, ref)
 
 
+NONZERO_GOLD = json.load(open(os.path.join(os.path.dirname(__file__), "golden",
+                                           "segment_reduce_nonzero_reference_gtest.json")))
+
+
+@pytest.mark.parametrize("where", ["host", "device"])
+@pytest.mark.parametrize("case", NONZERO_GOLD["cases"], ids=lambda c: c["name"])
+def test_segment_reduce_nonzero_reference_goldens(case, where):
+    """The reference's KPFusedSparseSegmentReduceNonzero goldens through the
+    KPFusedSparseSegmentReduce entry (same reduction, dense output): listed
+    as the nonzero op lists its output, the result equals the goldens."""
+    from tests.nonzero_util import case_inputs, check_case
+    note(f"nonzero golden {case['name']} ({where})")
+    data, indices, slice_input, _ = case_inputs(case)
+    data2 = np.ascontiguousarray(data.reshape(data.shape[0], -1))
+    begin = np.asarray(case["begin"], np.int32)
+    begin_1 = np.zeros(1, np.int32)
+    if where == "device":
+        data2, indices, slice_input = to_dev(data2), to_dev(indices), to_dev(slice_input)
+    out, _ = tf_ops.kp_fused_sparse_segment_reduce(data2, indices, slice_input, begin, begin_1,
+                                                   case["combiner"])
+    check_case(case, to_host(out) if where == "device" else np.asarray(out))
+
+
 # ---------------------------------------------------------------- KPFusedGather
 GATHER_GOLD = json.load(open(os.path.join(os.path.dirname(__file__), "golden",
                                           "fused_gather_reference_gtest.json")))

@@ -246,6 +246,34 @@ def test_dense_layer_relu_and_sigmoid():
 
 
 # ---------------------------------------------------------------- KPFusedGather
+NONZERO_GOLD = json.load(open(os.path.join(os.path.dirname(__file__), "golden",
+                                           "segment_reduce_nonzero_reference_gtest.json")))
+
+
+@pytest.mark.parametrize("case", NONZERO_GOLD["cases"], ids=lambda c: c["name"])
+def test_segment_reduce_nonzero_reference_goldens(case):
+    """The reference's KPFusedSparseSegmentReduceNonzero goldens pin the
+    segment reduction (index-order sums, mean = sum * (1/count), max_seg + 1
+    rows): the oracle's dense result, listed as that op lists it, equals
+    them exactly."""
+    from tests.nonzero_util import case_inputs, check_case
+    data, indices, _, seg = case_inputs(case)
+    data2 = data.reshape(data.shape[0], -1)
+    dense = ora.segment_reduce(data2, indices, seg, int(seg.max()) + 1, case["combiner"])
+    check_case(case, dense)
+
+
+def test_segment_reduce_nonzero_check_catches_a_wrong_reduction():
+    """The check fails for a reduction that drops the first position (a
+    mistake planted in the oracle's inputs, on the CPU)."""
+    from tests.nonzero_util import case_inputs, check_case
+    case = [c for c in NONZERO_GOLD["cases"] if c["name"] == "Test2DReduceSum"][0]
+    data, indices, _, seg = case_inputs(case)
+    dense = ora.segment_reduce(data, indices[1:], seg[1:], int(seg.max()) + 1, 0)
+    with pytest.raises(AssertionError):
+        check_case(case, dense)
+
+
 GATHER_GOLD = json.load(open(os.path.join(os.path.dirname(__file__), "golden",
                                           "fused_gather_reference_gtest.json")))
 
