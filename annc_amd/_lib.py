@@ -101,6 +101,11 @@ _PROTOTYPES = {
                                                    _i64, _c_void_p, _i32, _c_void_p, _c_void_p,
                                                    _i64, _c_void_p, _i64, _i32, _c_void_p,
                                                    _c_void_p, _c_void_p]),
+    "annc_kp_fused_sparse_segment_reduce_nonzero": (_i32, [_c_void_p, _i32, _c_void_p, _c_void_p,
+                                                           _i32, _i64, _c_void_p, _i32,
+                                                           _c_void_p, _c_void_p, _i64, _i32,
+                                                           _c_void_p, _c_void_p, _c_void_p,
+                                                           _c_void_p]),
     "annc_kp_fused_embedding_with_hash_bucket": (_i32, [_c_void_p, _c_void_p, _i64, _c_void_p,
                                                         _i64, _i64, _i64, _i32, _c_void_p]),
     "annc_kp_fused_dnn_embedding_with_hash_bucket": (_i32, [_c_void_p, _c_void_p, _i64,

@@ -698,6 +698,36 @@ __global__ __launch_bounds__(kThreads) void pooling_kernel(
   out[t] = red == 0.0f ? 0.0f : sum / red;
 }
 
+__global__ void widen_i32_kernel(const int32_t* __restrict__ src, int64_t n,
+                                 int64_t* __restrict__ dst) {
+  const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (i < n) dst[i] = src[i];
+}
+
+__global__ void nz_flag_kernel(const float* __restrict__ dense, int64_t count,
+                               int32_t* __restrict__ flags) {
+  const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (i < count) flags[i] = dense[i] != 0.0f ? 1 : 0;  // NaN counts as nonzero
+}
+
+__global__ void nz_write_kernel(const float* __restrict__ dense, int64_t count, int64_t dim,
+                                const int64_t* __restrict__ seg_of_row, int one_d,
+                                const int32_t* __restrict__ flags,
+                                const int32_t* __restrict__ incl,
+                                int32_t* __restrict__ out_idx, float* __restrict__ out_val) {
+  const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (i >= count || !flags[i]) return;
+  const int64_t p = incl[i] - 1, r = i / dim;
+  const int32_t seg = static_cast<int32_t>(seg_of_row[r]);
+  if (one_d) {
+    out_idx[p] = seg;
+  } else {
+    out_idx[2 * p] = seg;
+    out_idx[2 * p + 1] = static_cast<int32_t>(i - r * dim);
+  }
+  out_val[p] = dense[i];
+}
+
 }  // namespace
 
 int launch_bag(const BagArgs& a, hipStream_t s) {
@@ -919,6 +949,40 @@ int launch_pooling(hipStream_t s, const int64_t* ids, const float* gathered, int
   hipLaunchKernelGGL(pooling_kernel, dim3((unsigned)ceil_div(m * n, kThreads)), dim3(kThreads), 0,
                      s, ids, gathered, m, k, n, ss[0], ss[1], ss[2], sl[0], sl[1], sl[2], out);
   ANNC_HIP_TRY(hipGetLastError());
+  return ANNC_OK;
+}
+
+int widen_i32(hipStream_t s, const int32_t* src, int64_t n, int64_t* dst) {
+  if (n <= 0) return ANNC_OK;
+  hipLaunchKernelGGL(widen_i32_kernel, dim3((unsigned)ceil_div(n, kThreads)), dim3(kThreads), 0, s,
+                     src, n, dst);
+  ANNC_HIP_TRY(hipGetLastError());
+  return ANNC_OK;
+}
+
+size_t nonzero_scan_temp_bytes(int64_t count) {
+  size_t bytes = 0;
+  if (hipcub::DeviceScan::InclusiveSum(nullptr, bytes, (const int32_t*)nullptr, (int32_t*)nullptr,
+                                       (int)std::max<int64_t>(count, 1), (hipStream_t)0) !=
+      hipSuccess)
+    return 0;
+  return std::max<size_t>(bytes, 1);
+}
+
+int nonzero_compact(hipStream_t s, const float* dense, int64_t count, int64_t dim,
+                    const int64_t* seg_of_row, int one_d, int32_t* flags, int32_t* incl, void* tmp,
+                    size_t tmp_bytes, int32_t* out_idx, float* out_val) {
+  ANNC_REQUIRE(count < (int64_t(1) << 31), "too many reduced values");
+  if (count <= 0) return ANNC_OK;
+  const dim3 grid((unsigned)ceil_div(count, kThreads));
+  hipLaunchKernelGGL(nz_flag_kernel, grid, dim3(kThreads), 0, s, dense, count, flags);
+  ANNC_HIP_TRY(hipGetLastError());
+  ANNC_HIP_TRY(hipcub::DeviceScan::InclusiveSum(tmp, tmp_bytes, flags, incl, (int)count, s));
+  if (out_idx) {
+    hipLaunchKernelGGL(nz_write_kernel, grid, dim3(kThreads), 0, s, dense, count, dim, seg_of_row,
+                       one_d, flags, incl, out_idx, out_val);
+    ANNC_HIP_TRY(hipGetLastError());
+  }
   return ANNC_OK;
 }
 

@@ -155,6 +155,125 @@ int annc_kp_fused_sparse_segment_reduce(const float* data, int data_rank, const 
   return rc == ANNC_OK ? set_error(ANNC_OK, "") : rc;
 }
 
+int annc_kp_fused_sparse_segment_reduce_nonzero(
+    const float* data, int data_rank, const int64_t* data_dims, const void* indices,
+    int indices_is_64, int64_t num_indices, const int64_t* slice_input, int slice_rank,
+    const int64_t* slice_dims, const int32_t* begin, int64_t begin_elems, int combiner,
+    int32_t* output_shape, int64_t* num_nonzero, int32_t* output_indices,
+    float* output_nonzero) {
+  using namespace annc;
+  // OpKernel constructor and Compute() checks, same order and text
+  // (embedding_fused_sparse_segment_reduce_nonzero.cc:33-57).
+  ANNC_REQUIRE(combiner == 0 || combiner == 1, "combiner must be 0 or 1");
+  ANNC_REQUIRE(data_rank == 1 || data_rank == 2, "Input data must be a 1-D vector or 2-D matrix");
+  ANNC_REQUIRE(slice_rank == 2, "slice input must be 2-D");
+  ANNC_REQUIRE(begin_elems == 2, "begin must have 2 elements");
+  ANNC_REQUIRE(data_dims && slice_dims && begin && num_nonzero, "null shape operand");
+  int32_t b[2];
+  int rc = read_i32(begin, 2, b);
+  if (rc != ANNC_OK) return rc;
+  const int32_t col = b[1];
+  ANNC_REQUIRE(col >= 0 && col < slice_dims[1], "Column index out of range");
+  ANNC_REQUIRE(num_indices == slice_dims[0],
+               "indices and slice_input.dim_size(0) should have same size");
+  ANNC_REQUIRE(num_indices == 0 || (indices && slice_input), "null operand");
+  ANNC_REQUIRE(num_indices < INT32_MAX, "too many indices");
+  const int64_t rows = data_dims[0], dim = data_rank == 2 ? data_dims[1] : 1;
+  const int one_d = data_rank == 1 ? 1 : 0;
+  // phase 2 (outputs given) takes the phase-1 count as the output size
+  const bool write = output_indices != nullptr;
+  ANNC_REQUIRE(!write || output_nonzero != nullptr || *num_nonzero == 0, "null output");
+  const int64_t cap = write ? *num_nonzero : 0;
+
+  hipStream_t s = lib_stream();
+  if (!s) return set_error(ANNC_INTERNAL, "no HIP stream");
+  Staging st(s);
+  const int64_t stride = slice_dims[1];
+  const int64_t* d_slice = static_cast<const int64_t*>(
+      st.in(slice_input, sizeof(int64_t) * (size_t)(slice_dims[0] * stride)));
+  if (st.status() != ANNC_OK) return st.status();
+  int64_t seg_min = 0, seg_max = 0;
+  bool sorted = true;
+  rc = segment_scan(s, d_slice + col, stride, num_indices, &seg_min, &seg_max, &sorted);
+  if (rc != ANNC_OK) return rc;
+  // max_seg_id starts at 0 (:63-71)
+  const int64_t batch = (num_indices > 0 && seg_max > 0 ? seg_max : 0) + 1;
+  if (output_shape) {
+    rc = write_i32(output_shape, static_cast<int32_t>(batch));
+    if (rc == ANNC_OK && !one_d) rc = write_i32(output_shape + 1, static_cast<int32_t>(dim));
+    if (rc != ANNC_OK) return rc;
+  }
+  if (num_indices == 0 || dim == 0) {
+    *num_nonzero = 0;
+    return set_error(ANNC_OK, "");
+  }
+
+  // segments in order of first appearance, and each position's rank among them
+  int64_t* d_nu = static_cast<int64_t*>(st.scratch(sizeof(int64_t)));
+  int64_t* d_uniq = static_cast<int64_t*>(st.scratch(sizeof(int64_t) * num_indices));
+  int32_t* d_slot = static_cast<int32_t*>(st.scratch(sizeof(int32_t) * num_indices));
+  int64_t* d_slot64 = static_cast<int64_t*>(st.scratch(sizeof(int64_t) * num_indices));
+  if (!d_nu || !d_uniq || !d_slot || !d_slot64)
+    return set_error(ANNC_RESOURCE_EXHAUSTED, "scratch allocation failed");
+  rc = annc_hip_unique_gather(s, nullptr, 0, 0, d_slice + col, stride, num_indices, d_nu, d_uniq,
+                              d_slot, nullptr);
+  if (rc != ANNC_OK) return rc;
+  int64_t nseg = 0;
+  ANNC_HIP_TRY(hipMemcpyAsync(&nseg, d_nu, sizeof(int64_t), hipMemcpyDeviceToHost, s));
+  ANNC_HIP_TRY(hipStreamSynchronize(s));
+  rc = widen_i32(s, d_slot, num_indices, d_slot64);
+  if (rc != ANNC_OK) return rc;
+
+  // per-segment reduction in index order, rows in first-appearance order
+  const float* d_data = static_cast<const float*>(st.in(data, sizeof(float) * rows * dim));
+  const void* d_idx = st.in(indices, (indices_is_64 ? 8 : 4) * (size_t)num_indices);
+  const int64_t count = nseg * dim;
+  float* d_dense = static_cast<float*>(st.scratch(sizeof(float) * count));
+  int32_t* d_flags = static_cast<int32_t*>(st.scratch(sizeof(int32_t) * count));
+  int32_t* d_incl = static_cast<int32_t*>(st.scratch(sizeof(int32_t) * count));
+  const size_t tmp_bytes = nonzero_scan_temp_bytes(count);
+  void* d_tmp = tmp_bytes ? st.scratch(tmp_bytes) : nullptr;
+  if (st.status() != ANNC_OK) return st.status();
+  if (!d_dense || !d_flags || !d_incl || !d_tmp)
+    return set_error(ANNC_RESOURCE_EXHAUSTED, "scratch allocation failed");
+  int* status = stream_status(s);
+  if (!status) return set_error(ANNC_RESOURCE_EXHAUSTED, "status allocation failed");
+  ANNC_HIP_TRY(hipMemsetAsync(status, 0, sizeof(int), s));
+  rc = segment_reduce(s, d_data, rows, dim, d_idx, indices_is_64, d_slot64, 1, num_indices, combiner,
+                      nseg, d_dense, 0);
+  if (rc != ANNC_OK) return rc;
+
+  int32_t* d_out_idx = nullptr;
+  float* d_out_val = nullptr;
+  if (write && cap > 0) {
+    d_out_idx = static_cast<int32_t*>(st.out(output_indices, sizeof(int32_t) * cap * (one_d ? 1 : 2)));
+    d_out_val = static_cast<float*>(st.out(output_nonzero, sizeof(float) * cap));
+    if (st.status() != ANNC_OK) return st.status();
+  }
+  rc = nonzero_compact(s, d_dense, count, dim, d_uniq, one_d, d_flags, d_incl, d_tmp, tmp_bytes,
+                       d_out_idx, d_out_val);
+  if (rc != ANNC_OK) return rc;
+  int32_t nnz = 0;
+  ANNC_HIP_TRY(hipMemcpyAsync(&nnz, d_incl + (count - 1), sizeof(int32_t), hipMemcpyDeviceToHost, s));
+  int bad = 0;
+  ANNC_HIP_TRY(hipMemcpyAsync(&bad, status, sizeof(int), hipMemcpyDeviceToHost, s));
+  ANNC_HIP_TRY(hipStreamSynchronize(s));
+  if (bad) {
+    ANNC_HIP_TRY(hipMemset(status, 0, sizeof(int)));
+    return set_error(ANNC_INVALID_ARGUMENT, "indices out of range of the %lld data rows",
+                     (long long)rows);
+  }
+  // a phase-2 buffer must be what phase 1 counted (the result is deterministic)
+  ANNC_REQUIRE(!write || nnz == cap, "output size %lld differs from the %lld nonzero values",
+               (long long)cap, (long long)nnz);
+  if (write && cap > 0) {
+    rc = st.finish();
+    if (rc != ANNC_OK) return rc;
+  }
+  *num_nonzero = nnz;
+  return set_error(ANNC_OK, "");
+}
+
 int annc_kp_fused_embedding_with_hash_bucket(const char* bytes, const int64_t* offsets,
                                              int64_t batch, const float* weight, int64_t rows,
                                              int64_t dim, int64_t num_buckets, int combiner,

@@ -87,6 +87,41 @@ def kp_fused_sparse_segment_reduce(data, indices, slice_input, begin, begin_1, c
     return out, np.int32(slice_out[0])
 
 
+def kp_fused_sparse_segment_reduce_nonzero(data, indices, slice_input, begin, combiner: int = 1):
+    """KPFusedSparseSegmentReduceNonzero
+    (annc/tensorflow/ops/embedding_fused_ops.cc:41-51,
+     annc/tensorflow/kernels/embedding_fused_sparse_segment_reduce_nonzero.cc:39-372).
+
+    Returns (output_shape int32 [1] or [2], output_indices int32 [nnz, 1]
+    (1-D data) or [nnz, 2] (2-D data), output_nonzero float32 [nnz]): the
+    segment reductions' values != 0, segments in order of first appearance.
+    """
+    lib = _lib.lib()
+    data = _contig(data)
+    indices = _contig(indices)
+    slice_input = _contig(slice_input)
+    begin_h = _as_host_i32(begin).reshape(-1)
+    idx64 = str(indices.dtype).endswith("int64")
+    if not idx64 and not str(indices.dtype).endswith("int32"):
+        raise TypeError("indices must be int32 or int64 (attr Tidx)")
+    ddims = _dims(data)
+    sdims = _dims(slice_input)
+    num_indices = int(indices.shape[0]) if len(indices.shape) else 0
+    shape = np.zeros(2, dtype=np.int32)
+    nnz = np.zeros(1, dtype=np.int64)
+    args = (ptr(data), len(data.shape), ptr(ddims), ptr(indices), 1 if idx64 else 0, num_indices,
+            ptr(slice_input), len(slice_input.shape), ptr(sdims), ptr(begin_h), begin_h.size,
+            int(combiner), ptr(shape), ptr(nnz))
+    check(lib.annc_kp_fused_sparse_segment_reduce_nonzero(*args, None, None))
+    count = int(nnz[0])
+    width = 1 if len(data.shape) == 1 else 2
+    out_idx = _empty_like_kind(data, (count, width), np.int32)
+    out_val = _empty_like_kind(data, (count,), np.float32)
+    if count:
+        check(lib.annc_kp_fused_sparse_segment_reduce_nonzero(*args, ptr(out_idx), ptr(out_val)))
+    return shape[:width].copy(), out_idx, out_val
+
+
 def kp_fused_gather(data, slice_input, begin):
     """KPFusedGather (annc/tensorflow/ops/embedding_fused_ops.cc:114-121,
     annc/tensorflow/kernels/embedding_fused_gather.cc:26-85).

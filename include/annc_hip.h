@@ -301,6 +301,27 @@ int annc_kp_fused_sparse_segment_reduce(const float* data, int data_rank, const 
                                         int combiner, int64_t* out_rows, float* output,
                                         int32_t* slice_output);
 
+/* KPFusedSparseSegmentReduceNonzero (annc/tensorflow/ops/embedding_fused_ops.cc:41-51,
+ * kernels/embedding_fused_sparse_segment_reduce_nonzero.cc:39-372).
+ * Inputs: data f32 (data_rank 1 or 2, data_dims), indices int32|int64 [N],
+ * slice_input int64 (slice_rank, slice_dims), begin int32[begin_elems]
+ * (segment id = slice_input[i, begin[1]]); attr combiner (0 sum, 1 mean).
+ * The segments are reduced as KPFusedSparseSegmentReduce does (rows in index
+ * order, mean = sum * (1/count)) and the values != 0 are listed, segments in
+ * order of first appearance, dims ascending.  output_shape int32: [max_seg+1]
+ * for 1-D data, [max_seg+1, D] for 2-D.  Phase 1 (output_indices == NULL):
+ * *num_nonzero = the number of listed values.  Phase 2: *num_nonzero holds
+ * that count on entry and output_indices int32 [count, 1] (1-D: segment) or
+ * [count, 2] (2-D: segment, dim) and output_nonzero f32[count] are written.
+ * Errors: the reference OP_REQUIRES messages verbatim; indices outside the
+ * data rows are reported (the reference reads them unchecked). */
+int annc_kp_fused_sparse_segment_reduce_nonzero(
+    const float* data, int data_rank, const int64_t* data_dims, const void* indices,
+    int indices_is_64, int64_t num_indices, const int64_t* slice_input, int slice_rank,
+    const int64_t* slice_dims, const int32_t* begin, int64_t begin_elems, int combiner,
+    int32_t* output_shape, int64_t* num_nonzero, int32_t* output_indices,
+    float* output_nonzero);
+
 /* KPFusedGather (annc/tensorflow/ops/embedding_fused_ops.cc:114-121,
  * kernels/embedding_fused_gather.cc:26-85).  Inputs: data f32 (data_rank,
  * data_dims), slice_input int64 (slice_rank, slice_dims), begin int32

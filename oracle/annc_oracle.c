@@ -14,8 +14,15 @@
  *                          published vector available offline: parity
  *                          unpinned for that branch.
  *   ora_segment_reduce     reference gtest golden vectors
- *                          (embedding_fused_sparse_segment_reduce_test.cc:57-101)
+ *                          (embedding_fused_sparse_segment_reduce_test.cc:57-101,
+ *                          and the nonzero op's goldens,
+ *                          embedding_fused_sparse_segment_reduce_nonzero_test.cc:56-239)
  *                          and brute force in tests/.
+ *   ora_segment_reduce_nonzero
+ *                          reference gtest golden vectors
+ *                          (embedding_fused_sparse_segment_reduce_nonzero_test.cc:56-239)
+ *                          and, on random inputs, the listing of
+ *                          ora_segment_reduce's dense result in tests/.
  *   ora_embedding_bag      same order as ora_segment_reduce (CSR form);
  *                          checked equal to it in tests/.
  *   ora_pooling            brute force on tiny inputs in tests/.
@@ -276,6 +283,59 @@ void ora_embedding_bag(const float* table, int64_t rows, int64_t dim, const void
 /* ======================================================================== */
 /* __pooling (annc/service/cpu/graph_opt.cc:131-176).                       */
 /* ======================================================================== */
+/* KPFusedSparseSegmentReduceNonzero
+ * (annc/tensorflow/kernels/embedding_fused_sparse_segment_reduce_nonzero.cc:39-372):
+ * segments in order of first appearance (:86-113), rows added in index order
+ * per dim, mean = sum * (1/count), values != 0 listed with their (segment) or
+ * (segment, dim) coordinates; shape = max(0, max segment id) + 1 (:62-71).
+ * Writes at most cap values; returns their total number. */
+int64_t ora_segment_reduce_nonzero(const float* data, int64_t rows, int64_t dim,
+                                   const void* indices, int idx64, const int64_t* seg,
+                                   int64_t seg_stride, int64_t n, int combiner, int one_d,
+                                   int32_t* out_shape, int32_t* out_idx, float* out_val,
+                                   int64_t cap) {
+  (void)rows;
+  int64_t max_seg = 0, nseg = 0;
+  int64_t* order = (int64_t*)malloc(sizeof(int64_t) * (size_t)(n > 0 ? n : 1));
+  float* sums = (float*)calloc((size_t)(n > 0 ? n : 1) * (size_t)(dim > 0 ? dim : 1), sizeof(float));
+  int32_t* counts = (int32_t*)calloc((size_t)(n > 0 ? n : 1), sizeof(int32_t));
+  for (int64_t i = 0; i < n; ++i) {
+    const int64_t s = seg[i * seg_stride];
+    if (s > max_seg) max_seg = s;
+    int64_t k = 0;
+    while (k < nseg && order[k] != s) ++k;
+    if (k == nseg) order[nseg++] = s;
+    const int64_t row = idx64 ? ((const int64_t*)indices)[i] : ((const int32_t*)indices)[i];
+    for (int64_t d = 0; d < dim; ++d) sums[k * dim + d] += data[row * dim + d];
+    counts[k]++;
+  }
+  out_shape[0] = (int32_t)(max_seg + 1);
+  if (!one_d) out_shape[1] = (int32_t)dim;
+  int64_t nz = 0;
+  for (int64_t k = 0; k < nseg; ++k) {
+    const float inv = combiner == 1 ? (counts[k] > 0 ? 1.0f / (float)counts[k] : 0.0f) : 1.0f;
+    for (int64_t d = 0; d < dim; ++d) {
+      const float v = sums[k * dim + d] * inv;
+      if (v != 0.0f) {
+        if (nz < cap) {
+          if (one_d) {
+            out_idx[nz] = (int32_t)order[k];
+          } else {
+            out_idx[2 * nz] = (int32_t)order[k];
+            out_idx[2 * nz + 1] = (int32_t)d;
+          }
+          out_val[nz] = v;
+        }
+        ++nz;
+      }
+    }
+  }
+  free(order);
+  free(sums);
+  free(counts);
+  return nz;
+}
+
 void ora_pooling(const int64_t* ids, const float* gathered, int64_t m, int64_t k, int64_t n,
                  const int64_t* ss, const int64_t* sl, float* out) {
   for (int64_t i = 0; i < m; ++i) {

@@ -31,6 +31,8 @@ _PROTO = {
     "ora_hash_bucket_int64": (None, [_v, _i64, _i64, _v]),
     "ora_segment_reduce": (None, [_v, _i64, _i64, _v, _i32, _v, _i64, _i64, _i32, _i64, _v]),
     "ora_embedding_bag": (None, [_v, _i64, _i64, _v, _i32, _v, _i64, _i32, _v, _i64, _i32]),
+    "ora_segment_reduce_nonzero": (_i64, [_v, _i64, _i64, _v, _i32, _v, _i64, _i64, _i32, _i32,
+                                          _v, _v, _v, _i64]),
     "ora_pooling": (None, [_v, _v, _i64, _i64, _i64, _v, _v, _v]),
     "ora_sparse_embedding2": (None, [_v, _i64, _i64, _v, _i32, _i64, _i64, _v]),
     "ora_fused_gather": (_i64, [_v, _i64, _i64, _v, _i64, _i64, _v, _v, _v]),
@@ -152,6 +154,27 @@ def segment_reduce(data, indices, seg, batch, combiner) -> np.ndarray:
     lib().ora_segment_reduce(_p(data), data.shape[0], data.shape[1], _p(indices), int(idx64),
                              _p(seg), 1, indices.size, int(combiner), int(batch), _p(out))
     return out
+
+
+def segment_reduce_nonzero(data, indices, seg, combiner):
+    """KPFusedSparseSegmentReduceNonzero: (output_shape int32, output_indices
+    int32 [nnz, 1 or 2], output_nonzero float32 [nnz]); data 1-D or 2-D."""
+    data = _c(data, np.float32)
+    one_d = data.ndim == 1
+    data2 = data.reshape(data.shape[0], -1) if data.size else data.reshape(data.shape[0], 1)
+    idx64 = indices.dtype == np.int64
+    indices = _c(indices, np.int64 if idx64 else np.int32)
+    seg = _c(seg, np.int64)
+    n, dim = indices.size, data2.shape[1]
+    width = 1 if one_d else 2
+    shape = np.zeros(2, np.int32)
+    cap = max(n * dim, 1)
+    idx = np.empty(cap * width, np.int32)
+    val = np.empty(cap, np.float32)
+    nz = lib().ora_segment_reduce_nonzero(_p(data2), data2.shape[0], dim, _p(indices), int(idx64), _p(seg), 1, n, int(combiner),
+           int(one_d), _p(shape), _p(idx), _p(val), cap)
+    return (shape[:1 if one_d else 2].copy(), idx[:nz * width].reshape(nz, width).copy(),
+            val[:nz].copy())
 
 
 def embedding_bag(table, ids, offsets, combiner, threads=1) -> np.ndarray:

@@ -245,6 +245,57 @@ def test_segment_reduce_nonzero_reference_goldens(case, where):
     check_case(case, to_host(out) if where == "device" else np.asarray(out))
 
 
+@pytest.mark.parametrize("where", ["host", "device"])
+@pytest.mark.parametrize("case", NONZERO_GOLD["cases"], ids=lambda c: c["name"])
+def test_tf_segment_reduce_nonzero_reference_goldens(case, where):
+    """KPFusedSparseSegmentReduceNonzero on the GPU reproduces the reference
+    op's goldens exactly."""
+    from tests.nonzero_util import case_inputs
+    note(f"KPFusedSparseSegmentReduceNonzero golden {case['name']} ({where})")
+    data, indices, slice_input, _ = case_inputs(case)
+    if where == "device":
+        data, indices, slice_input = to_dev(data), to_dev(indices), to_dev(slice_input)
+    shape, idx, val = tf_ops.kp_fused_sparse_segment_reduce_nonzero(
+        data, indices, slice_input, np.asarray(case["begin"], np.int32), case["combiner"])
+    if where == "device":
+        idx, val = to_host(idx), to_host(val)
+    assert shape.tolist() == case["expected_shape"]
+    assert list(idx.shape) == case["expected_indices_shape"]
+    assert idx.reshape(-1).tolist() == case["expected_indices"]
+    np.testing.assert_array_equal(val, np.asarray(case["expected_values"], np.float32))
+
+
+@pytest.mark.parametrize("one_d", [True, False])
+@pytest.mark.parametrize("combiner", [0, 1])
+@pytest.mark.parametrize("idx64", [False, True])
+def test_tf_segment_reduce_nonzero_random_bit_exact(one_d, combiner, idx64):
+    """Shuffled segment ids (first appearance differs from id order), data
+    with exact zeros and a NaN, 5000 positions: equal to the oracle."""
+    note(f"KPFusedSparseSegmentReduceNonzero random one_d={one_d} comb={combiner} idx64={idx64}")
+    g = workloads.rng(100 + 4 * one_d + 2 * combiner + idx64)
+    n, rows, dim = 5000, 300, 1 if one_d else 20
+    data = g.integers(-2, 3, size=(rows, dim)).astype(np.float32)
+    data[7, 0] = np.nan
+    indices = g.integers(0, rows, size=n).astype(np.int64 if idx64 else np.int32)
+    seg = g.permutation(np.repeat(np.arange(700), 8)[:n]).astype(np.int64)
+    slice_input = np.stack([np.zeros(n, np.int64), seg], axis=1)
+    data_in = data[:, 0].copy() if one_d else data
+    want = ora.segment_reduce_nonzero(data_in, indices, seg, combiner)
+    shape, idx, val = tf_ops.kp_fused_sparse_segment_reduce_nonzero(
+        to_dev(data_in), to_dev(indices), to_dev(slice_input), np.array([0, 1], np.int32), combiner)
+    np.testing.assert_array_equal(shape, want[0])
+    np.testing.assert_array_equal(to_host(idx), want[1])
+    np.testing.assert_array_equal(to_host(val), want[2])
+
+
+def test_tf_segment_reduce_nonzero_index_out_of_range():
+    note("KPFusedSparseSegmentReduceNonzero idx out of range")
+    with pytest.raises(tf_ops.InvalidArgumentError, match="out of range"):
+        tf_ops.kp_fused_sparse_segment_reduce_nonzero(
+            np.ones((4, 2), np.float32), np.array([0, 9], np.int32),
+            np.array([[0, 0], [0, 1]], np.int64), np.array([0, 1], np.int32), 0)
+
+
 # ---------------------------------------------------------------- KPFusedGather
 GATHER_GOLD = json.load(open(os.path.join(os.path.dirname(__file__), "golden",
                                           "fused_gather_reference_gtest.json")))

@@ -167,6 +167,32 @@ def test_segment_reduce_bad_combiner():
                                               np.array([0], np.int32), combiner=2)
 
 
+# The KPFusedSparseSegmentReduceNonzero checks, in the reference's order and
+# text (embedding_fused_sparse_segment_reduce_nonzero.cc:33-57); all fail
+# before any device work.
+NONZERO_ERRORS = [
+    ("combiner", dict(combiner=2), "combiner must be 0 or 1"),
+    ("3-D data", dict(data=np.zeros((2, 2, 2), np.float32)),
+     "Input data must be a 1-D vector or 2-D matrix"),
+    ("1-D slice", dict(slice_input=np.zeros(3, np.int64)), "slice input must be 2-D"),
+    ("begin of 3", dict(begin=np.array([0, 0, 0], np.int32)), "begin must have 2 elements"),
+    ("column", dict(begin=np.array([0, 2], np.int32)), "Column index out of range"),
+    ("sizes", dict(indices=np.zeros(2, np.int32)),
+     "indices and slice_input.dim_size(0) should have same size"),
+]
+
+
+@pytest.mark.parametrize("what,override,message", NONZERO_ERRORS, ids=[e[0] for e in NONZERO_ERRORS])
+def test_segment_reduce_nonzero_error_messages(what, override, message):
+    args = dict(data=np.zeros((4, 2), np.float32), indices=np.zeros(3, np.int32),
+                slice_input=np.zeros((3, 2), np.int64), begin=np.array([0, 1], np.int32),
+                combiner=0)
+    args.update(override)
+    with pytest.raises(tf_ops.InvalidArgumentError) as ei:
+        tf_ops.kp_fused_sparse_segment_reduce_nonzero(**args)
+    assert message in str(ei.value)
+
+
 def test_hash_ops_reject_zero_buckets():
     with pytest.raises(tf_ops.InvalidArgumentError):
         tf_ops.kp_fused_embedding_with_hash_bucket([b"a"], np.zeros((4, 2), np.float32), 0)

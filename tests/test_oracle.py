@@ -263,6 +263,37 @@ def test_segment_reduce_nonzero_reference_goldens(case):
     check_case(case, dense)
 
 
+@pytest.mark.parametrize("case", NONZERO_GOLD["cases"], ids=lambda c: c["name"])
+def test_oracle_segment_reduce_nonzero_goldens(case):
+    """ora_segment_reduce_nonzero reproduces the reference op's goldens."""
+    from tests.nonzero_util import case_inputs
+    data, indices, _, seg = case_inputs(case)
+    shape, idx, val = ora.segment_reduce_nonzero(data, indices, seg, case["combiner"])
+    assert shape.tolist() == case["expected_shape"]
+    assert list(idx.shape) == case["expected_indices_shape"]
+    assert idx.reshape(-1).tolist() == case["expected_indices"]
+    np.testing.assert_array_equal(val, np.asarray(case["expected_values"], np.float32))
+
+
+@pytest.mark.parametrize("one_d", [True, False])
+@pytest.mark.parametrize("combiner", [0, 1])
+def test_oracle_segment_reduce_nonzero_random(one_d, combiner):
+    """On shuffled segment ids (first appearance differs from id order) and
+    data with zeros, the op's listing equals the listing of
+    ora_segment_reduce's dense result in first-appearance order."""
+    from tests.nonzero_util import nonzero_coo
+    g = np.random.default_rng(11 + combiner + 2 * one_d)
+    n, rows, dim = 300, 50, 1 if one_d else 7
+    data = g.integers(-2, 3, size=(rows, dim)).astype(np.float32)  # many exact zeros
+    indices = g.integers(0, rows, size=n).astype(np.int32)
+    seg = g.permutation(np.repeat(np.arange(40), 8)[:n]).astype(np.int64)
+    dense = ora.segment_reduce(data, indices, seg, int(seg.max()) + 1, combiner)
+    want = nonzero_coo(dense, seg, one_d)
+    got = ora.segment_reduce_nonzero(data[:, 0] if one_d else data, indices, seg, combiner)
+    for w, o in zip(want, got):
+        np.testing.assert_array_equal(o, w)
+
+
 def test_segment_reduce_nonzero_check_catches_a_wrong_reduction():
     """The check fails for a reduction that drops the first position (a
     mistake planted in the oracle's inputs, on the CPU)."""
