@@ -710,14 +710,18 @@ __global__ void nz_flag_kernel(const float* __restrict__ dense, int64_t count,
   if (i < count) flags[i] = dense[i] != 0.0f ? 1 : 0;  // NaN counts as nonzero
 }
 
+// Writes the p-th listed value for p < cap only: a caller whose buffers hold
+// fewer values than the flags list gets no write past them (the host then
+// reports the count mismatch).
 __global__ void nz_write_kernel(const float* __restrict__ dense, int64_t count, int64_t dim,
                                 const int64_t* __restrict__ seg_of_row, int one_d,
                                 const int32_t* __restrict__ flags,
-                                const int32_t* __restrict__ incl,
+                                const int32_t* __restrict__ incl, int64_t cap,
                                 int32_t* __restrict__ out_idx, float* __restrict__ out_val) {
   const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
   if (i >= count || !flags[i]) return;
   const int64_t p = incl[i] - 1, r = i / dim;
+  if (p >= cap) return;
   const int32_t seg = static_cast<int32_t>(seg_of_row[r]);
   if (one_d) {
     out_idx[p] = seg;
@@ -971,7 +975,7 @@ size_t nonzero_scan_temp_bytes(int64_t count) {
 
 int nonzero_compact(hipStream_t s, const float* dense, int64_t count, int64_t dim,
                     const int64_t* seg_of_row, int one_d, int32_t* flags, int32_t* incl, void* tmp,
-                    size_t tmp_bytes, int32_t* out_idx, float* out_val) {
+                    size_t tmp_bytes, int64_t cap, int32_t* out_idx, float* out_val) {
   ANNC_REQUIRE(count < (int64_t(1) << 31), "too many reduced values");
   if (count <= 0) return ANNC_OK;
   const dim3 grid((unsigned)ceil_div(count, kThreads));
@@ -980,7 +984,7 @@ int nonzero_compact(hipStream_t s, const float* dense, int64_t count, int64_t di
   ANNC_HIP_TRY(hipcub::DeviceScan::InclusiveSum(tmp, tmp_bytes, flags, incl, (int)count, s));
   if (out_idx) {
     hipLaunchKernelGGL(nz_write_kernel, grid, dim3(kThreads), 0, s, dense, count, dim, seg_of_row,
-                       one_d, flags, incl, out_idx, out_val);
+                       one_d, flags, incl, cap, out_idx, out_val);
     ANNC_HIP_TRY(hipGetLastError());
   }
   return ANNC_OK;

@@ -43,12 +43,13 @@ int widen_i32(hipStream_t s, const int32_t* src, int64_t n, int64_t* dst);
 // reduction (row r holds segment seg_of_row[r]): flags[i] = dense[i] != 0,
 // incl = their inclusive scan (incl[count - 1] = the number of nonzeros),
 // and with out_idx the nonzero coordinates ((segment) for one_d, else
-// (segment, dim)) and values in row-major order.  tmp holds
+// (segment, dim)) and values in row-major order, the first `cap` of them
+// (out_idx and out_val hold cap entries).  tmp holds
 // nonzero_scan_temp_bytes(count) bytes.
 size_t nonzero_scan_temp_bytes(int64_t count);
 int nonzero_compact(hipStream_t s, const float* dense, int64_t count, int64_t dim,
                     const int64_t* seg_of_row, int one_d, int32_t* flags, int32_t* incl, void* tmp,
-                    size_t tmp_bytes, int32_t* out_idx, float* out_val);
+                    size_t tmp_bytes, int64_t cap, int32_t* out_idx, float* out_val);
 
 int launch_sparse_embedding2(hipStream_t s, const float* table, int64_t rows, int64_t dim,
                              const void* ids, int ids_is_64, int64_t n, int64_t fallback,

@@ -251,7 +251,7 @@ int annc_kp_fused_sparse_segment_reduce_nonzero(
     if (st.status() != ANNC_OK) return st.status();
   }
   rc = nonzero_compact(s, d_dense, count, dim, d_uniq, one_d, d_flags, d_incl, d_tmp, tmp_bytes,
-                       d_out_idx, d_out_val);
+                       cap, d_out_idx, d_out_val);
   if (rc != ANNC_OK) return rc;
   int32_t nnz = 0;
   ANNC_HIP_TRY(hipMemcpyAsync(&nnz, d_incl + (count - 1), sizeof(int32_t), hipMemcpyDeviceToHost, s));

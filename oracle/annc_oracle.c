@@ -26,6 +26,18 @@
  *   ora_embedding_bag      same order as ora_segment_reduce (CSR form);
  *                          checked equal to it in tests/.
  *   ora_pooling            brute force on tiny inputs in tests/.
+ *   ora_hash_bucket_int64  decimal text checked against Python's str(int);
+ *                          the hash as ora_fingerprint64.
+ *   ora_embedding_with_hash_bucket, ora_dnn_embedding_with_hash_bucket,
+ *   ora_sparse_embedding   closed forms over the pinned hash in tests/
+ *                          (empty string, NUL-terminated prefix, bucket past
+ *                          the rows, the bucket-0 quirk), with planted
+ *                          mistakes the checks must catch.
+ *   ora_hashed_embedding_bags
+ *                          equal, in tests/, to the per-field composition of
+ *                          ora_hash_bucket_int64 and ora_embedding_bag on
+ *                          ragged multi-field inputs, with planted field
+ *                          mix-ups the check must catch.
  *   ora_batch_matmul_add_sigmoid
  *                          float64 closed form (numpy matmul + broadcast) on
  *                          the reference test's shapes and inputs

@@ -288,6 +288,78 @@ def test_tf_segment_reduce_nonzero_random_bit_exact(one_d, combiner, idx64):
     np.testing.assert_array_equal(to_host(val), want[2])
 
 
+@pytest.mark.parametrize("case", ["normal", "negative_ids", "many_segments", "host_5000"])
+def test_tf_segment_reduce_nonzero_order_sensitive(case):
+    """Data from standard_normal, so the summation order shows in the bits:
+    negative segment ids (INT64_MIN among them, listed as the reference's
+    int32 cast lists them), more than 16384 first-appearance segments (the
+    radix-sort path) and host-memory operands at 5000 positions; each equal
+    to the oracle bit for bit."""
+    note(f"KPFusedSparseSegmentReduceNonzero order-sensitive {case}")
+    g = workloads.rng({"normal": 31, "negative_ids": 32, "many_segments": 33,
+                       "host_5000": 34}[case])
+    n, rows, dim, nseg = 6000, 400, 9, 900
+    if case == "many_segments":
+        n, nseg = 40000, 20000
+    seg = g.permutation(np.arange(n) % nseg).astype(np.int64)
+    if case == "negative_ids":
+        seg = seg - nseg // 2
+        seg[seg == -7] = np.iinfo(np.int64).min
+        seg[seg == 5] = -(2 ** 40)
+    data = g.standard_normal((rows, dim)).astype(np.float32)
+    indices = g.integers(0, rows, size=n).astype(np.int64)
+    slice_input = np.stack([np.zeros(n, np.int64), seg, np.ones(n, np.int64)], axis=1)
+    for combiner in (0, 1):
+        want = ora.segment_reduce_nonzero(data, indices, seg, combiner)
+        args = (data, indices, slice_input) if case == "host_5000" else \
+            (to_dev(data), to_dev(indices), to_dev(slice_input))
+        shape, idx, val = tf_ops.kp_fused_sparse_segment_reduce_nonzero(
+            *args, np.array([0, 1], np.int32), combiner)
+        if case != "host_5000":
+            idx, val = to_host(idx), to_host(val)
+        np.testing.assert_array_equal(shape, want[0])
+        np.testing.assert_array_equal(idx, want[1])
+        np.testing.assert_array_equal(val, want[2])
+
+
+def test_tf_segment_reduce_nonzero_short_phase2_buffer():
+    """A phase-2 call whose buffers hold one value fewer than phase 1
+    counted is refused with the count mismatch, and writes nothing past the
+    buffers it was given (a guard word after them keeps its value)."""
+    import ctypes
+    from annc_amd import _lib
+    note("KPFusedSparseSegmentReduceNonzero short phase-2 buffer")
+    g = workloads.rng(35)
+    n, rows, dim = 500, 50, 4
+    data = to_dev(g.standard_normal((rows, dim)).astype(np.float32))
+    indices = to_dev(g.integers(0, rows, size=n).astype(np.int32))
+    slice_input = to_dev(np.stack([np.zeros(n, np.int64),
+                                   g.integers(0, 60, size=n).astype(np.int64)], axis=1))
+    lib = _lib.lib()
+    ddims = np.array([rows, dim], np.int64)
+    sdims = np.array([n, 2], np.int64)
+    begin = np.array([0, 1], np.int32)
+    shape = np.zeros(2, np.int32)
+    nnz = np.zeros(1, np.int64)
+    args = (_lib.ptr(data), 2, _lib.ptr(ddims), _lib.ptr(indices), 0, n, _lib.ptr(slice_input),
+            2, _lib.ptr(sdims), _lib.ptr(begin), 2, 0, _lib.ptr(shape), _lib.ptr(nnz))
+    _lib.check(lib.annc_kp_fused_sparse_segment_reduce_nonzero(*args, None, None))
+    count = int(nnz[0])
+    assert count > 1
+    short = count - 1
+    guard = np.float32(123.5)
+    out_idx = torch.full((short * 2 + 64,), -5, dtype=torch.int32, device=device())
+    out_val = torch.full((short + 64,), float(guard), dtype=torch.float32, device=device())
+    nnz[0] = short
+    rc = lib.annc_kp_fused_sparse_segment_reduce_nonzero(*args, ctypes.c_void_p(out_idx.data_ptr()),
+                                                         ctypes.c_void_p(out_val.data_ptr()))
+    assert rc == 3
+    assert "differs from the" in _lib.last_error()
+    torch.cuda.synchronize()
+    assert (to_host(out_idx)[short * 2:] == -5).all()
+    assert (to_host(out_val)[short:] == guard).all()
+
+
 def test_tf_segment_reduce_nonzero_index_out_of_range():
     note("KPFusedSparseSegmentReduceNonzero idx out of range")
     with pytest.raises(tf_ops.InvalidArgumentError, match="out of range"):

@@ -204,6 +204,132 @@ def test_sparse_embedding_zero_bucket_quirk():
     assert empty.tolist() == [False, True, False]
 
 
+def _dnn_expected(strs, weight, num_buckets):
+    """KPFusedDnn/LinearEmbeddingWithHashBucket, from the pinned pieces
+    (fused_dnn_embedding_with_hash_bucket.cc:33-44,
+    fused_linear_embdedding_with_hash_bucket.cc:43-51): a string equal to ""
+    gives zeros; otherwise Fingerprint64 of the text up to the first NUL
+    (tensorflow::Fingerprint64(const char*)), modulo num_buckets as uint64,
+    and the row only when that bucket is below the weight's rows."""
+    rows, dim = weight.shape
+    out = np.zeros((len(strs), dim), np.float32)
+    for i, s in enumerate(strs):
+        if s == b"":
+            continue
+        b = ora.fingerprint64(s.split(b"\0", 1)[0]) % num_buckets
+        if b < rows:
+            out[i] = weight[b]
+    return out
+
+
+def _dnn_strings():
+    g = np.random.Generator(np.random.PCG64(21))
+    strs = [b"", b"\0", b"\0tail", b"ab\0cd", b"abc", b"x" * 70, b"12345678901234567"]
+    strs += [str(int(v)).encode() for v in g.integers(-2**63, 2**63 - 1, size=120, dtype=np.int64)]
+    return strs
+
+
+def test_dnn_embedding_with_hash_bucket_closed_form():
+    """Buckets at or past the weight's rows (num_buckets 2x rows) give zero
+    rows, the empty string gives zeros, and a string with a NUL hashes only
+    its prefix ("\0tail" hashes as "", whose fingerprint is pinned)."""
+    g = np.random.Generator(np.random.PCG64(22))
+    weight = g.standard_normal((40, 6)).astype(np.float32)
+    strs = _dnn_strings()
+    want = _dnn_expected(strs, weight, 80)
+    got = ora.dnn_embedding_with_hash_bucket(strs, weight, 80)
+    np.testing.assert_array_equal(got, want)
+    # the cases the checks above must tell apart are present
+    past = [i for i, s in enumerate(strs) if s and
+            ora.fingerprint64(s.split(b"\0", 1)[0]) % 80 >= 40]
+    assert len(past) > 10 and not got[past].any()
+    # every bucket inside the table: "\0" and "\0tail" are non-empty strings
+    # whose hashed text is "" (Fingerprint64("") = k2, a pinned vector)
+    k2 = 0x9AE16A3B2F90404F
+    got40 = ora.dnn_embedding_with_hash_bucket(strs, weight, 40)
+    np.testing.assert_array_equal(got40, _dnn_expected(strs, weight, 40))
+    assert got40[1].tolist() == got40[2].tolist() == weight[k2 % 40].tolist()
+    assert ora.fingerprint64(b"\0tail") % 40 != k2 % 40
+    assert ora.fingerprint64(b"ab") % 40 != ora.fingerprint64(b"ab\0cd") % 40
+
+
+def test_dnn_embedding_check_catches_whole_string_hash_and_missing_bound():
+    """The closed form fails for an oracle that hashes the whole string
+    (NUL included) or copies rows for buckets past the table (mistakes
+    planted in the checker's inputs, on the CPU)."""
+    g = np.random.Generator(np.random.PCG64(23))
+    weight = g.standard_normal((40, 6)).astype(np.float32)
+    strs = _dnn_strings()
+    want = _dnn_expected(strs, weight, 80)
+    whole = ora.embedding_with_hash_bucket(
+        [s for s in strs], np.concatenate([weight, weight]), 80)  # whole-string hash, no bound
+    assert not np.array_equal(whole, want)
+    # bucket bound only: the rows past the table would be copied
+    wide = np.concatenate([weight, g.standard_normal((40, 6)).astype(np.float32)])
+    assert not np.array_equal(ora.dnn_embedding_with_hash_bucket(strs, wide, 80), want)
+
+
+def _ragged_fields(seed, nf, batch, rows):
+    g = np.random.Generator(np.random.PCG64(seed))
+    tables = [g.standard_normal((rows[f], 5)).astype(np.float32) for f in range(nf)]
+    lens = g.integers(0, 7, size=nf * batch)
+    lens[:3] = [0, 1, 6]
+    offsets = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    ids = g.integers(-2**63, 2**63 - 1, size=int(offsets[-1]), dtype=np.int64)
+    return tables, ids, offsets
+
+
+def _bags_by_field(tables, num_buckets, ids, offsets, batch, combiner):
+    """Per field f: the pinned bucket ids (decimal text -> Fingerprint64 %
+    buckets), then the pinned CSR embedding bag over field f's slice of the
+    offsets, placed at columns [f*dim, (f+1)*dim) of the concatenated output."""
+    nf = len(tables)
+    dim = tables[0].shape[1]
+    out = np.empty((batch, nf * dim), np.float32)
+    for f in range(nf):
+        off = offsets[f * batch:(f + 1) * batch + 1]
+        lo, hi = int(off[0]), int(off[-1])
+        buckets = ora.hash_bucket_int64(ids[lo:hi], num_buckets[f])
+        out[:, f * dim:(f + 1) * dim] = ora.embedding_bag(tables[f], buckets, off - lo, combiner)
+    return out
+
+
+@pytest.mark.parametrize("combiner", [0, 1])
+@pytest.mark.parametrize("threads", [1, 4])
+def test_hashed_embedding_bags_is_per_field_composition(combiner, threads):
+    """ora_hashed_embedding_bags (the checker of the multi-field hashed bags)
+    equals, bit for bit, the per-field composition of the pinned
+    hash_bucket_int64 and embedding_bag, on ragged bags (empty ones
+    included) over fields with different tables and bucket counts; its
+    bucket output equals the pinned bucket ids."""
+    nf, batch = 4, 37
+    nb = [101, 57, 1000, 3]
+    tables, ids, offsets = _ragged_fields(40 + combiner, nf, batch, [101, 60, 1000, 3])
+    got, buckets = ora.hashed_embedding_bags(tables, nb, ids, offsets, batch, combiner,
+                                             threads=threads, with_buckets=True)
+    np.testing.assert_array_equal(got, _bags_by_field(tables, nb, ids, offsets, batch, combiner))
+    want_b = np.concatenate([ora.hash_bucket_int64(
+        ids[offsets[f * batch]:offsets[(f + 1) * batch]], nb[f]) for f in range(nf)])
+    np.testing.assert_array_equal(buckets, want_b)
+
+
+def test_hashed_embedding_bags_check_catches_field_mixups():
+    """The composition check fails for a field order swapped, a bucket count
+    taken from the wrong field, or a mean where a sum is due (mistakes
+    planted in the oracle's inputs, on the CPU)."""
+    nf, batch = 3, 20
+    nb = [101, 57, 1000]
+    tables, ids, offsets = _ragged_fields(50, nf, batch, [101, 60, 1000])
+    want = _bags_by_field(tables, nb, ids, offsets, batch, 0)
+    swapped = [tables[1], tables[0], tables[2]]
+    assert not np.array_equal(
+        ora.hashed_embedding_bags(swapped, [57, 101, 1000], ids, offsets, batch, 0), want)
+    assert not np.array_equal(
+        ora.hashed_embedding_bags(tables, [101, 101, 1000], ids, offsets, batch, 0), want)
+    assert not np.array_equal(
+        ora.hashed_embedding_bags(tables, nb, ids, offsets, batch, 1), want)
+
+
 # ------------------------------------------------------------ GEMM via OpenBLAS
 def test_openblas_is_0_3_29():
     assert "0.3.29" in ora.blas_config()
