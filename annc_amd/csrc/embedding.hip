@@ -340,12 +340,19 @@ __global__ __launch_bounds__(kThreads) void cs_hist_kernel(const int64_t* __rest
   for (int s = threadIdx.x; s < batch; s += kThreads) cs_lds[s] = 0;
   __syncthreads();
   const int64_t b0 = (int64_t)blockIdx.x * kCsBlock;
-  for (int t = threadIdx.x; t < kCsBlock; t += kThreads) {
-    const int64_t i = b0 + t;
-    if (i < n) {
-      const int64_t s = seg[i * stride];
-      if (s >= 0 && s < batch) atomicAdd(&cs_lds[s], 1u);
-    }
+  // every id of the thread is loaded (positions clamped to n - 1) before the
+  // first count, so the loads travel together
+  constexpr int kPer = kCsBlock / kThreads;
+  int64_t sv[kPer];
+#pragma unroll
+  for (int u = 0; u < kPer; ++u) {
+    const int64_t i = b0 + threadIdx.x + u * kThreads;
+    sv[u] = seg[(i < n ? i : n - 1) * stride];
+  }
+#pragma unroll
+  for (int u = 0; u < kPer; ++u) {
+    const int64_t i = b0 + threadIdx.x + u * kThreads;
+    if (i < n && sv[u] >= 0 && sv[u] < batch) atomicAdd(&cs_lds[sv[u]], 1u);
   }
   __syncthreads();
   uint32_t* row = H + (int64_t)blockIdx.x * batch;
@@ -369,14 +376,16 @@ __global__ __launch_bounds__(1024) void cs_prefix_kernel(const uint32_t* __restr
   const bool ok = s < batch;
   const int per = (nblk + 15) / 16;
   const int b_lo = min(nblk, c * per), b_hi = min(nblk, b_lo + per);
+  // loads are unconditional (block and segment clamped into range) and
+  // masked afterwards, so the U loads of a step travel together
+  const int sc = ok ? s : batch - 1;
   uint32_t sum = 0;
   for (int b = b_lo; b < b_hi; b += U) {
     uint32_t v[U];
 #pragma unroll
-    for (int u = 0; u < U; ++u)
-      v[u] = (ok && b + u < b_hi) ? H[(int64_t)(b + u) * batch + s] : 0u;
+    for (int u = 0; u < U; ++u) v[u] = H[(int64_t)min(b + u, b_hi - 1) * batch + sc];
 #pragma unroll
-    for (int u = 0; u < U; ++u) sum += v[u];
+    for (int u = 0; u < U; ++u) sum += (ok && b + u < b_hi) ? v[u] : 0u;
   }
   part[c][j] = sum;
   __syncthreads();
@@ -387,11 +396,11 @@ __global__ __launch_bounds__(1024) void cs_prefix_kernel(const uint32_t* __restr
   for (int b = b_lo; b < b_hi; b += U) {
     uint32_t v[U];
 #pragma unroll
-    for (int u = 0; u < U; ++u) v[u] = b + u < b_hi ? H[(int64_t)(b + u) * batch + s] : 0u;
+    for (int u = 0; u < U; ++u) v[u] = H[(int64_t)min(b + u, b_hi - 1) * batch + s];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       if (b + u < b_hi) P[(int64_t)(b + u) * batch + s] = run;
-      run += v[u];
+      run += b + u < b_hi ? v[u] : 0u;
     }
   }
 }
@@ -439,13 +448,15 @@ __global__ __launch_bounds__(kThreads) void cs_scatter_kernel(const int64_t* __r
                                                              int32_t* __restrict__ perm) {
   extern __shared__ uint32_t cs_lds[];  // next slot of each segment
   const uint32_t* pre = P + (int64_t)blockIdx.x * batch;
-  constexpr int kInit = 16;  // cursor loads in flight per thread
+  // cursor loads in flight per thread; unconditional (segment clamped to
+  // batch - 1), so they are issued together and waited for once
+  constexpr int kInit = 16;
   for (int s0 = threadIdx.x; s0 < batch; s0 += kThreads * kInit) {
     uint32_t v[kInit];
 #pragma unroll
     for (int u = 0; u < kInit; ++u) {
-      const int s = s0 + u * kThreads;
-      v[u] = s < batch ? static_cast<uint32_t>(offsets[s]) + pre[s] : 0u;
+      const int s = min(s0 + u * kThreads, batch - 1);
+      v[u] = static_cast<uint32_t>(offsets[s]) + pre[s];
     }
 #pragma unroll
     for (int u = 0; u < kInit; ++u) {
@@ -762,15 +773,48 @@ int segment_scan(hipStream_t s, const int64_t* seg, int64_t stride, int64_t n, i
   return ANNC_OK;
 }
 
-int segment_reduce(hipStream_t s, const float* data, int64_t rows, int64_t dim,
-                   const void* indices, int indices_is_64, const int64_t* seg, int64_t stride,
-                   int64_t n, int combiner, int64_t batch, float* out, int sorted_hint) {
-  if (batch <= 0) return ANNC_OK;
-  int* status = stream_status(s);
-  if (!status) return set_error(ANNC_RESOURCE_EXHAUSTED, "status allocation failed");
+namespace {
+size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+}  // namespace
+
+int segment_reduce_plan(int64_t n, int64_t batch, int sorted_hint, hipStream_t s, SegPlan* plan) {
   ANNC_REQUIRE(n < (1ll << 31), "too many indices");
   ANNC_REQUIRE(batch < (1ll << 32), "too many segments");
+  *plan = SegPlan{};
+  const size_t off_bytes = align256(sizeof(int64_t) * (size_t)(batch + 1));
+  if (sorted_hint == 1) {
+    plan->path = SegPlan::kSorted;
+    plan->bytes = off_bytes;
+    return ANNC_OK;
+  }
+  const int64_t nblk = ceil_div(n, kCsBlock);
+  if (batch <= kCsMaxSegments && nblk * batch <= (int64_t(1) << 24)) {
+    plan->path = SegPlan::kCounting;
+    const size_t hb = align256(sizeof(uint32_t) * (size_t)std::max<int64_t>(nblk * batch, 1));
+    const size_t tb = align256(sizeof(uint32_t) * (size_t)batch);
+    const size_t pb = align256(sizeof(int32_t) * (size_t)std::max<int64_t>(n, 1));
+    plan->bytes = 2 * hb + tb + off_bytes + pb;
+    return ANNC_OK;
+  }
+  plan->path = SegPlan::kRadix;
+  int end_bit = 1;
+  while (end_bit < 32 && (1ull << end_bit) <= (uint64_t)batch) ++end_bit;  // batch fits too
+  size_t temp_bytes = 0;
+  ANNC_HIP_TRY(hipcub::DeviceRadixSort::SortPairs(nullptr, temp_bytes, (const uint32_t*)nullptr,
+                                                  (uint32_t*)nullptr, (const int32_t*)nullptr,
+                                                  (int32_t*)nullptr, (int)n, 0, end_bit, s));
+  const size_t nk = align256(sizeof(uint32_t) * (size_t)std::max<int64_t>(n, 1));
+  plan->end_bit = end_bit;
+  plan->temp_bytes = temp_bytes;
+  plan->bytes = 4 * nk + off_bytes + align256(temp_bytes);
+  return ANNC_OK;
+}
 
+int segment_reduce_run(hipStream_t s, const float* data, int64_t rows, int64_t dim,
+                       const void* indices, int indices_is_64, const int64_t* seg, int64_t stride,
+                       int64_t n, int combiner, int64_t batch, float* out, const SegPlan& plan,
+                       void* workspace, int* status) {
+  if (batch <= 0) return ANNC_OK;
   BagArgs a{};
   a.table = data;
   a.rows = rows;
@@ -782,12 +826,11 @@ int segment_reduce(hipStream_t s, const float* data, int64_t rows, int64_t dim,
   a.out = out;
   a.ldo = dim;
   a.status = status;
+  char* ws = static_cast<char*>(workspace);
+  const size_t off_bytes = align256(sizeof(int64_t) * (size_t)(batch + 1));
 
-  const size_t off_bytes = sizeof(int64_t) * (size_t)(batch + 1);
-  auto align = [](size_t x) { return (x + 255) & ~size_t(255); };
-  if (sorted_hint == 1) {
-    int64_t* offsets = static_cast<int64_t*>(stream_workspace(s, off_bytes));
-    if (!offsets) return set_error(ANNC_RESOURCE_EXHAUSTED, "workspace allocation failed");
+  if (plan.path == SegPlan::kSorted) {
+    int64_t* offsets = reinterpret_cast<int64_t*>(ws);
     hipLaunchKernelGGL(seg_bounds_kernel<int64_t>, dim3((unsigned)ceil_div(n + 1, kThreads)),
                        dim3(kThreads), 0, s, seg, stride, n, batch, offsets);
     ANNC_HIP_TRY(hipGetLastError());
@@ -796,19 +839,16 @@ int segment_reduce(hipStream_t s, const float* data, int64_t rows, int64_t dim,
     return launch_bag(a, s);
   }
 
-  // General order, up to kCsMaxSegments segments: stable counting sort.
-  const int64_t nblk = ceil_div(n, kCsBlock);
-  if (batch <= kCsMaxSegments && nblk * batch <= (int64_t(1) << 24)) {
-    const size_t hb = align(sizeof(uint32_t) * (size_t)std::max<int64_t>(nblk * batch, 1));
-    const size_t tb = align(sizeof(uint32_t) * (size_t)batch);
-    const size_t pb = align(sizeof(int32_t) * (size_t)std::max<int64_t>(n, 1));
-    char* ws = static_cast<char*>(stream_workspace(s, 2 * hb + tb + align(off_bytes) + pb));
-    if (!ws) return set_error(ANNC_RESOURCE_EXHAUSTED, "workspace allocation failed");
+  if (plan.path == SegPlan::kCounting) {
+    // stable counting sort by segment (up to kCsMaxSegments segments)
+    const int64_t nblk = ceil_div(n, kCsBlock);
+    const size_t hb = align256(sizeof(uint32_t) * (size_t)std::max<int64_t>(nblk * batch, 1));
+    const size_t tb = align256(sizeof(uint32_t) * (size_t)batch);
     uint32_t* H = reinterpret_cast<uint32_t*>(ws);
     uint32_t* P = reinterpret_cast<uint32_t*>(ws + hb);
     uint32_t* total = reinterpret_cast<uint32_t*>(ws + 2 * hb);
     int64_t* offsets = reinterpret_cast<int64_t*>(ws + 2 * hb + tb);
-    int32_t* perm = reinterpret_cast<int32_t*>(ws + 2 * hb + tb + align(off_bytes));
+    int32_t* perm = reinterpret_cast<int32_t*>(ws + 2 * hb + tb + off_bytes);
     const int nb = static_cast<int>(batch);
     const size_t lds = sizeof(uint32_t) * (size_t)batch;
     if (n > 0) {
@@ -832,29 +872,20 @@ int segment_reduce(hipStream_t s, const float* data, int64_t rows, int64_t dim,
   }
 
   // More segments: stable radix sort of (segment id, position), then CSR.
-  int end_bit = 1;
-  while (end_bit < 32 && (1ull << end_bit) <= (uint64_t)batch) ++end_bit;  // batch fits too
-  size_t temp_bytes = 0;
-  ANNC_HIP_TRY(hipcub::DeviceRadixSort::SortPairs(nullptr, temp_bytes, (const uint32_t*)nullptr,
-                                                  (uint32_t*)nullptr, (const int32_t*)nullptr,
-                                                  (int32_t*)nullptr, (int)n, 0, end_bit, s));
-  const size_t nk = align(sizeof(uint32_t) * (size_t)std::max<int64_t>(n, 1));
-  const size_t nv = align(sizeof(int32_t) * (size_t)std::max<int64_t>(n, 1));
-  const size_t total = 2 * nk + 2 * nv + align(off_bytes) + align(temp_bytes);
-  char* ws = static_cast<char*>(stream_workspace(s, total));
-  if (!ws) return set_error(ANNC_RESOURCE_EXHAUSTED, "workspace allocation failed");
+  const size_t nk = align256(sizeof(uint32_t) * (size_t)std::max<int64_t>(n, 1));
   uint32_t* keys_in = reinterpret_cast<uint32_t*>(ws);
   uint32_t* keys_out = reinterpret_cast<uint32_t*>(ws + nk);
   int32_t* vals_in = reinterpret_cast<int32_t*>(ws + 2 * nk);
-  int32_t* vals_out = reinterpret_cast<int32_t*>(ws + 2 * nk + nv);
-  int64_t* offsets = reinterpret_cast<int64_t*>(ws + 2 * nk + 2 * nv);
-  void* temp = ws + 2 * nk + 2 * nv + align(off_bytes);
+  int32_t* vals_out = reinterpret_cast<int32_t*>(ws + 3 * nk);
+  int64_t* offsets = reinterpret_cast<int64_t*>(ws + 4 * nk);
+  void* temp = ws + 4 * nk + off_bytes;
+  size_t temp_bytes = plan.temp_bytes;
   if (n > 0) {
     hipLaunchKernelGGL(make_keys_kernel, dim3((unsigned)ceil_div(n, kThreads)), dim3(kThreads), 0,
                        s, seg, stride, n, batch, keys_in, vals_in);
     ANNC_HIP_TRY(hipGetLastError());
     ANNC_HIP_TRY(hipcub::DeviceRadixSort::SortPairs(temp, temp_bytes, keys_in, keys_out, vals_in,
-                                                    vals_out, (int)n, 0, end_bit, s));
+                                                    vals_out, (int)n, 0, plan.end_bit, s));
   }
   hipLaunchKernelGGL(seg_bounds_kernel<uint32_t>, dim3((unsigned)ceil_div(n + 1, kThreads)),
                      dim3(kThreads), 0, s, keys_out, (int64_t)1, n, batch, offsets);
@@ -862,6 +893,21 @@ int segment_reduce(hipStream_t s, const float* data, int64_t rows, int64_t dim,
   a.offsets = offsets;
   a.perm = vals_out;
   return launch_bag(a, s);
+}
+
+int segment_reduce(hipStream_t s, const float* data, int64_t rows, int64_t dim,
+                   const void* indices, int indices_is_64, const int64_t* seg, int64_t stride,
+                   int64_t n, int combiner, int64_t batch, float* out, int sorted_hint) {
+  if (batch <= 0) return ANNC_OK;
+  int* status = stream_status(s);
+  if (!status) return set_error(ANNC_RESOURCE_EXHAUSTED, "status allocation failed");
+  SegPlan plan;
+  int rc = segment_reduce_plan(n, batch, sorted_hint, s, &plan);
+  if (rc != ANNC_OK) return rc;
+  void* ws = stream_workspace(s, plan.bytes);
+  if (!ws) return set_error(ANNC_RESOURCE_EXHAUSTED, "workspace allocation failed");
+  return segment_reduce_run(s, data, rows, dim, indices, indices_is_64, seg, stride, n, combiner,
+                            batch, out, plan, ws, status);
 }
 
 namespace {

@@ -30,11 +30,29 @@ int launch_bag(const BagArgs& a, hipStream_t s);
 int segment_scan(hipStream_t s, const int64_t* seg, int64_t stride, int64_t n, int64_t* min_out,
                  int64_t* max_out, bool* sorted);
 
-// out[batch, dim] = segment reduction of data rows; segment ids must lie in
-// [0, batch).  sorted_hint = 1 when the ids are known to be non-decreasing.
+// out[batch, dim] = segment reduction of data rows; positions whose segment
+// id lies outside [0, batch) are skipped.  sorted_hint = 1 when the ids are
+// known to be non-decreasing.  Workspace from the stream, status word of
+// the stream.
 int segment_reduce(hipStream_t s, const float* data, int64_t rows, int64_t dim,
                    const void* indices, int indices_is_64, const int64_t* seg, int64_t stride,
                    int64_t n, int combiner, int64_t batch, float* out, int sorted_hint);
+
+// The path a segment reduction takes and the device workspace it needs.
+struct SegPlan {
+  enum Path { kSorted, kCounting, kRadix } path = kSorted;
+  size_t bytes = 0;       // workspace bytes
+  size_t temp_bytes = 0;  // radix sort temporary storage (kRadix)
+  int end_bit = 0;        // radix sort key bits (kRadix)
+};
+int segment_reduce_plan(int64_t n, int64_t batch, int sorted_hint, hipStream_t s, SegPlan* plan);
+// Runs `plan` with caller-provided workspace (plan.bytes, 256-byte aligned)
+// and status word (bit 0 is set for a row id outside the data).  Allocates
+// nothing.
+int segment_reduce_run(hipStream_t s, const float* data, int64_t rows, int64_t dim,
+                       const void* indices, int indices_is_64, const int64_t* seg, int64_t stride,
+                       int64_t n, int combiner, int64_t batch, float* out, const SegPlan& plan,
+                       void* workspace, int* status);
 
 // dst[i] = src[i] for i < n (int32 -> int64).
 int widen_i32(hipStream_t s, const int32_t* src, int64_t n, int64_t* dst);
