@@ -79,6 +79,9 @@ _PROTOTYPES = {
                                       _c_void_p, _i64, _i32, _c_void_p, _i64]),
     "annc_hip_segment_reduce": (_i32, [_c_void_p, _c_void_p, _i64, _i64, _c_void_p, _i32,
                                        _c_void_p, _i64, _i64, _i32, _i64, _c_void_p, _i32]),
+    "annc_hip_segment_reduce_noalloc": (_i32, [_c_void_p, _c_void_p, _i64, _i64, _c_void_p,
+                                               _i32, _c_void_p, _i64, _i64, _i32, _i64,
+                                               _c_void_p, _i32, _c_void_p]),
     "annc_hip_sparse_embedding2": (_i32, [_c_void_p, _c_void_p, _i64, _i64, _c_void_p, _i32,
                                           _i64, _i64, _c_void_p]),
     "annc_hip_pooling": (_i32, [_c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64,

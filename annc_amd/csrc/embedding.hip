@@ -20,6 +20,8 @@
 #include <hipcub/hipcub.hpp>
 
 #include <algorithm>
+#include <map>
+#include <mutex>
 #include <utility>
 
 #include "common.h"
@@ -1038,6 +1040,39 @@ int nonzero_compact(hipStream_t s, const float* dense, int64_t count, int64_t di
 
 }  // namespace annc
 
+// ---------------------------------------------------------------------------
+// Device scratch of the allocation-free segment reduction
+// (annc_hip_segment_reduce_noalloc): one copy per GPU, held until the process
+// ends.  The first kNoAllocStatusBytes hold the status word kernels write
+// when the caller passes none; the rest is the workspace.
+// ---------------------------------------------------------------------------
+constexpr size_t kNoAllocScratchBytes = size_t(16) << 20;
+constexpr size_t kNoAllocStatusBytes = 256;
+static __device__ __align__(256) char scratch[kNoAllocScratchBytes];
+
+namespace annc {
+namespace {
+std::mutex g_scratch_mu;
+std::map<int, char*> g_scratch_ptr;  // device -> address of that device's copy
+
+// Address of `scratch` on the current device (looked up once per device;
+// the host-side name is not a device address).
+int noalloc_scratch(char** out) {
+  int dev = 0;
+  ANNC_HIP_TRY(hipGetDevice(&dev));
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  auto it = g_scratch_ptr.find(dev);
+  if (it == g_scratch_ptr.end()) {
+    char* ptr = nullptr;
+    ANNC_HIP_TRY(hipGetSymbolAddress(reinterpret_cast<void**>(&ptr), HIP_SYMBOL(scratch)));
+    it = g_scratch_ptr.emplace(dev, ptr).first;
+  }
+  *out = it->second;
+  return ANNC_OK;
+}
+}  // namespace
+}  // namespace annc
+
 extern "C" {
 
 int annc_hip_embedding_bag(void* stream, const float* table, int64_t rows, int64_t dim,
@@ -1084,6 +1119,37 @@ int annc_hip_segment_reduce(void* stream, const float* data, int64_t rows, int64
   ANNC_REQUIRE(seg_sorted == 0 || seg_sorted == 1, "seg_sorted must be 0 or 1");
   int rc = segment_reduce(static_cast<hipStream_t>(stream), data, rows, dim, indices,
                           indices_is_64, seg_ids, seg_stride, n, combiner, batch, out, seg_sorted);
+  return rc == ANNC_OK ? set_error(ANNC_OK, "") : rc;
+}
+
+int annc_hip_segment_reduce_noalloc(void* stream, const float* data, int64_t rows, int64_t dim,
+                                    const void* indices, int indices_is_64,
+                                    const int64_t* seg_ids, int64_t seg_stride, int64_t n,
+                                    int combiner, int64_t batch, float* out, int seg_sorted,
+                                    int32_t* status) {
+  using namespace annc;
+  ANNC_REQUIRE(rows >= 0 && dim >= 1 && n >= 0 && batch >= 0 && seg_stride >= 1,
+               "bad dimensions");
+  ANNC_REQUIRE(combiner == ANNC_COMBINER_SUM || combiner == ANNC_COMBINER_MEAN,
+               "combiner must be 0 or 1");
+  if (batch == 0) return set_error(ANNC_OK, "");
+  ANNC_REQUIRE(data && out && (n == 0 || (indices && seg_ids)), "null pointer");
+  ANNC_REQUIRE(seg_sorted == 0 || seg_sorted == 1, "seg_sorted must be 0 or 1");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  SegPlan plan;
+  int rc = segment_reduce_plan(n, batch, seg_sorted, s, &plan);
+  if (rc != ANNC_OK) return rc;
+  constexpr size_t kMax = kNoAllocScratchBytes - kNoAllocStatusBytes;
+  ANNC_REQUIRE(plan.bytes <= kMax,
+               "segment reduction of %lld positions into %lld segments needs %zu bytes of "
+               "workspace, above the %zu bytes of the allocation-free entry's scratch",
+               (long long)n, (long long)batch, plan.bytes, kMax);
+  char* base = nullptr;
+  rc = noalloc_scratch(&base);
+  if (rc != ANNC_OK) return rc;
+  int* st = status ? reinterpret_cast<int*>(status) : reinterpret_cast<int*>(base);
+  rc = segment_reduce_run(s, data, rows, dim, indices, indices_is_64, seg_ids, seg_stride, n,
+                          combiner, batch, out, plan, base + kNoAllocStatusBytes, st);
   return rc == ANNC_OK ? set_error(ANNC_OK, "") : rc;
 }
 

@@ -224,6 +224,25 @@ int annc_hip_segment_reduce(void* stream, const float* data, int64_t rows, int64
                             int64_t seg_stride, int64_t n, int combiner, int64_t batch,
                             float* out, int seg_sorted);
 
+/* No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, serving loops, harnesses that forbid
+ * hipMalloc): annc_hip_segment_reduce with the same arguments and results,
+ * plus `status` (device int32, optional): bit 0 is OR-ed in when a row id
+ * lies outside the data (the caller clears it; NULL discards the flag).
+ * It calls no hipMalloc/hipFree: its workspace is a 16 MiB device array of
+ * the library, one per GPU, held until the process ends.  Inputs that need
+ * more workspace than that are rejected with ANNC_INVALID_ARGUMENT (sorted
+ * ids: up to about 2 M segments; any order: the stable counting sort needs
+ * 8 * ceil(n/1024) * batch + 4 * n bytes and more, up to 16384 segments; the
+ * radix sort beyond that about 16 * n bytes).  Every call on a GPU uses that
+ * GPU's one array, so calls that overlap on one GPU (two streams, two
+ * threads) race and must be serialised by the caller. */
+int annc_hip_segment_reduce_noalloc(void* stream, const float* data, int64_t rows, int64_t dim,
+                                    const void* indices, int indices_is_64,
+                                    const int64_t* seg_ids, int64_t seg_stride, int64_t n,
+                                    int combiner, int64_t batch, float* out, int seg_sorted,
+                                    int32_t* status);
+
 /* sparse_embedding2 kLoop fusion (graph_opt.cc:8-41 with the bound checks of
  * bisheng-cpu/embedding_simplify.cc:62-81):
  * out[i,:] = table[valid ? ids[i] : fallback_row, :] * (float)valid,
