@@ -11,14 +11,18 @@ reported beside it.
 GEMM + bias + ReLU): 2*M*N*K flops per launch over its average duration,
 timed with HIP events on the stream the launches run on.
 
-`components` reports the other configurations (fused __matmul_add_relu,
-embedding bag GB/s, hashed multi-field bags GB/s, end-to-end wide&deep
-samples/s) and, under `other_rows`, the path's remaining operators on those
-inputs (sparse_embedding2 + __pooling in XLA's padded form, segment reduce,
-KPFusedGather, __batch_matmul, bucket ids); `cpu_baseline` times the
-oracle's OpenBLAS path on the host.
+`components` reports every other configuration and operator of the path,
+one entry per case of CASES (kernel time from HIP events over back-to-back
+launches in HIP graphs, the rate on algorithmic bytes or flops, and the
+rocprofv3 kernel average and PMC traffic of the committed summary in
+profiles/<profile>.md), the cold-cache variants of configs[2] and configs[3]
+(rotating table copies), and configs[4] end to end as samples/s.
+`cpu_baseline` times the oracle's CPU path for every configuration (OpenBLAS
+0.3.29 sgemm for the GEMMs, the reference's sequential loops for the bags),
+at 1 thread and at all cores.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-components] [--no-cpu]
+       python bench.py --kernel CASE [--launches N] [--graph]   (profiling mode)
 """
 from __future__ import annotations
 
@@ -36,14 +40,25 @@ sys.path.insert(0, ROOT)
 METRIC = "embedding-bag GB/s, fused-matmul TFLOPS, e2e rec-model samples/s @ batch 4096"
 HBM_PEAK_GBS = 8000.0
 FP32_MFMA_PEAK_TFLOPS = 157.3
+# cold-cache variants: enough table copies that the rows one rotation cycle
+# touches exceed the 256 MB MALL plus the 8 x 4 MB L2 several times over
+COLD_TABLE_COPIES = 96   # configs[2]: ~6.7 MB of distinct rows per launch -> 640 MB a cycle
+COLD_TABLE_SETS = 16     # configs[3]: ~82 MB of 128-byte lines per launch -> 1.3 GB a cycle
 
 
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def graph_time_ms(make_fn, launches: int, replays: int):
-    """Average ms per launch of fn, launched `launches` times per HIP graph."""
+def graph_time_ms(make_fn, launches: int, replays: int, settle_s: float = 0.025,
+                  info: dict | None = None):
+    """Average ms per launch of fn, launched `launches` times per HIP graph.
+
+    The graph is replayed untimed for `settle_s` first: after the idle gap
+    of the capture the GPU's clocks take a few ms of load to come back (the
+    first replays of a 37 us GEMM measured 43, 41, 39 us, then 36.8), and
+    the timed replays should see the steady state.  `info` receives the
+    number of untimed replays."""
     import torch
     from annc_amd.rec_graph import CapturedGraph
 
@@ -54,8 +69,16 @@ def graph_time_ms(make_fn, launches: int, replays: int):
         return out
 
     g = CapturedGraph(many)
-    g.replay()
-    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    settle = 0
+    while True:
+        g.replay()
+        settle += 1
+        torch.cuda.synchronize()
+        if time.perf_counter() - t0 >= settle_s:
+            break
+    if info is not None:
+        info["settle_replays"] = settle
     s = torch.cuda.current_stream()
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
@@ -88,32 +111,315 @@ def time_steps(step, steps: int, warmup: int):
     return e0.elapsed_time(e1) / steps, wall / steps
 
 
-def read_traffic(profile: str):
-    """HBM bytes per launch (calibrated FETCH_SIZE + WRITE_SIZE) from the
-    committed rocprofv3 --pmc summary profiles/<profile>.md, if present."""
+def read_profile(profile: str) -> dict:
+    """Figures of the committed rocprofv3 summary profiles/<profile>.md:
+    `rocprof_avg_ns` (kernel time per case launch under --kernel-trace) and
+    `traffic_bytes_per_launch` (calibrated FETCH_SIZE + WRITE_SIZE)."""
     path = os.path.join(ROOT, "profiles", f"{profile}.md")
+    out = {}
     if not os.path.exists(path):
-        return None
-    m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", open(path).read())
-    return float(m.group(1)) if m else None
+        return out
+    text = open(path).read()
+    for key in ("rocprof_avg_ns", "traffic_bytes_per_launch"):
+        m = re.search(rf"^{key}:\s*([0-9.eE+]+)", text, re.M)
+        if m:
+            out[key] = float(m.group(1))
+    return out
+
+
+# ---------------------------------------------------------------- cases
+class Inputs:
+    """Benchmark inputs, generated once per process (seed 0)."""
+
+    def __init__(self):
+        self._cache = {}
+
+    def get(self, name):
+        if name not in self._cache:
+            from annc_amd import workloads
+            self._cache[name] = getattr(workloads, name)(seed=0)
+        return self._cache[name]
+
+
+class Case:
+    """One operator on one workload: fn(i) enqueues launch i on torch's
+    current stream.  `bound` is "hbm" (rate on `work` bytes) or "mfma" (rate
+    on `work` flops)."""
+
+    def __init__(self, name, fn, work, bound, workload, profile, launches=50, **extra):
+        self.name, self.fn, self.work, self.bound = name, fn, work, bound
+        self.workload, self.profile, self.launches, self.extra = workload, profile, launches, extra
+
+    def rate(self, ms):
+        if self.bound == "samples":
+            return {"samples_per_s": round(self.work / (ms * 1e-3), 1)}
+        if self.bound == "hbm":
+            gbs = self.work / (ms * 1e-3) / 1e9
+            return {"GBps": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
+        tf = self.work / (ms * 1e-3) / 1e12
+        return {"tflops": round(tf, 2), "mfma_frac": round(tf / FP32_MFMA_PEAK_TFLOPS, 4)}
+
+
+def _bag_bytes(nnz, bags, dim, idx_bytes=8):
+    return idx_bytes * nnz + 8 * (bags + 1) + 4 * dim * nnz + 4 * dim * bags
+
+
+def make_case(name: str, device, inp: Inputs) -> Case:
+    import numpy as np
+    import torch
+    from annc_amd import EPI_RELU, EPI_SIGMOID, workloads
+    from annc_amd import device as dev
+
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(device)  # noqa: E731
+    if name in ("gemm_l1", "gemm_l2", "gemm_l3"):
+        w = inp.get("config2")
+        li = int(name[-1]) - 1
+        x = t(w.x)
+        if li >= 1:   # layer inputs of the right shape: ReLU of a slice of x
+            x = torch.relu(x[:, :w.weights[li].shape[0]]).contiguous()
+        wt = dev.pack_weight(t(w.weights[li]))
+        bias = t(w.biases[li])
+        out = torch.empty((x.shape[0], wt.n), dtype=torch.float32, device=device)
+        act = EPI_SIGMOID if li == 2 else EPI_RELU
+        m, n, k = x.shape[0], wt.n, wt.k
+        prof = {0: "gemm_layer1_4096x512x1024", 1: "gemm_layer2_4096x256x512",
+                2: "gemv_layer3_4096x1x256"}[li]
+        if li == 2:   # the scoring GEMV streams A once: HBM-bound
+            return Case(name, lambda i: dev.gemm(x, wt, bias=bias, epilogue=act, out=out),
+                        4 * (m * k + k + m), "hbm",
+                        f"configs[1] layer 3: [{m}x{k}] . [{k}x1] + bias, sigmoid", prof)
+        return Case(name, lambda i: dev.gemm(x, wt, bias=bias, epilogue=act, out=out),
+                    2.0 * m * n * k, "mfma",
+                    f"configs[1] layer {li + 1}: [{m}x{k}] . packed [{k}x{n}] + bias, ReLU", prof)
+    if name == "tower":
+        from annc_amd.rec_graph import MLPTower
+        w = inp.get("config2")
+        tower = MLPTower(w.weights, w.biases, device=device, packed=True)
+        x = t(w.x)
+        return Case(name, lambda i: tower(x), float(tower.flops(x.shape[0])), "mfma",
+                    "configs[1] step: the 3-layer tower forward (3 kernels)", "tower_config2_step")
+    if name == "widedeep":
+        from annc_amd.rec_graph import WideDeepConfig, WideDeepGraph
+        w = inp.get("config5")
+        h = w.hashed
+        graph = WideDeepGraph(WideDeepConfig(), [torch.from_numpy(x) for x in h.tables],
+                              w.weights, w.biases, device=device)
+        ids, offs = t(h.ids), t(h.offsets)
+        dense = graph.dense_view(h.batch)
+        dense.copy_(t(w.dense))
+        return Case(name, lambda i: graph(ids, offs, dense), float(h.batch), "samples",
+                    "configs[4] step: hashed bags into the concat buffer, 3 GEMMs + bias + ReLU, "
+                    "GEMV + sigmoid (5 kernels)", "widedeep_config5_step", launches=20,
+                    gemm_flops=graph.flops(h.batch))
+    if name == "gemm_small":
+        w = inp.get("config1")
+        a, b, e = t(w.a), t(w.b), t(w.e)
+        out = torch.empty((512, 256), dtype=torch.float32, device=device)
+        return Case(name, lambda i: dev.gemm(a, b, addend=e, epilogue=EPI_RELU, out=out),
+                    2.0 * 512 * 256 * 256, "mfma",
+                    "configs[0] __matmul_add_relu 512x256x256, row-major B, materialised addend",
+                    "gemm_small_config1_512x256x256", launches=100)
+    if name == "gemm_e2e_l1":
+        w = inp.get("config5")
+        k0 = w.weights[0].shape[0]
+        ld = (k0 + 3) // 4 * 4
+        buf = torch.zeros((w.hashed.batch, ld), dtype=torch.float32, device=device)
+        g = workloads.rng(7)
+        buf[:, :k0] = t(g.standard_normal((w.hashed.batch, k0)).astype(np.float32))
+        x = buf[:, :k0]
+        wt = dev.pack_weight(t(w.weights[0]))
+        bias = t(w.biases[0])
+        out = torch.empty((x.shape[0], wt.n), dtype=torch.float32, device=device)
+        return Case(name, lambda i: dev.gemm(x, wt, bias=bias, epilogue=EPI_RELU, out=out),
+                    2.0 * x.shape[0] * wt.n * wt.k, "mfma",
+                    f"configs[4] layer 1: concat [{x.shape[0]}x{k0}] (row stride {ld}) . packed "
+                    f"[{k0}x{wt.n}] + bias, ReLU", "gemm_widedeep_layer1_4096x1024x845")
+    if name == "batch_matmul":
+        g = workloads.rng(5)
+        bm, m, k, n = 32, 512, 256, 256
+        a = t(g.standard_normal((bm, m, k)).astype(np.float32))
+        b = t((g.standard_normal((bm, k, n)) / 16).astype(np.float32))
+        out = torch.empty((bm, m, n), dtype=torch.float32, device=device)
+        return Case(name, lambda i: dev.gemm(a, b, out=out), 2.0 * bm * m * n * k, "mfma",
+                    "__batch_matmul, 32 x [512x256] . [256x256] fp32, row-major B",
+                    "gemm_batch_matmul_32x512x256x256")
+    if name in ("bag_sum", "bag_mean", "bag_sum_cold"):
+        w = inp.get("config3")
+        table = t(w.table)
+        ids, offs = t(w.ids), t(w.offsets)
+        nnz, bags, dim = int(w.offsets[-1]), w.offsets.size - 1, w.table.shape[1]
+        out = torch.empty((bags, dim), dtype=torch.float32, device=device)
+        comb = 1 if name == "bag_mean" else 0
+        wl = ("configs[2] embedding bag: table 1e6x64 fp32, 4096 bags, Poisson(20) lengths, "
+              f"Zipf(1.05) int64 ids, CSR, {'mean' if comb else 'sum'}")
+        if name == "bag_sum_cold":
+            copies = [table] + [table.clone() for _ in range(COLD_TABLE_COPIES - 1)]
+            return Case(name, lambda i: dev.embedding_bag(copies[i % len(copies)], ids, offs, 0,
+                                                          out=out),
+                        _bag_bytes(nnz, bags, dim), "hbm",
+                        wl + f"; launch i reads table copy i % {COLD_TABLE_COPIES} "
+                             f"({COLD_TABLE_COPIES} x 256 MB), so every launch starts cold",
+                        "bag_kernel_config3_sum_cold", launches=2 * COLD_TABLE_COPIES,
+                        table_copies=COLD_TABLE_COPIES)
+        uniq = int(np.unique(w.ids).size)
+        return Case(name, lambda i: dev.embedding_bag(table, ids, offs, comb, out=out),
+                    _bag_bytes(nnz, bags, dim), "hbm", wl,
+                    f"bag_kernel_config3_{'mean' if comb else 'sum'}", launches=200,
+                    nnz=nnz, unique_rows=uniq,
+                    unique_row_bytes=8 * nnz + 8 * (bags + 1) + 4 * dim * uniq + 4 * dim * bags)
+    if name in ("hashed", "hashed_cold", "hashed_nohash"):
+        w = inp.get("config4")
+        ids, offs = t(w.ids), t(w.offsets)
+        nf = len(w.tables)
+        out = torch.empty((w.batch, nf * w.dim), dtype=torch.float32, device=device)
+        nnz = int(w.offsets[-1])
+        alg = _bag_bytes(nnz, nf * w.batch, w.dim)   # out [8192 x 416] = one dim-row per bag
+        nb = [w.num_buckets] * nf
+        wl = ("configs[3] 26 fields x batch 8192, int64 ids -> decimal -> Fingerprint64 % 1e5 "
+              "-> gather [1e5x16] -> mean, out [8192x416]")
+        if name == "hashed_nohash":
+            # gather ceiling: the same 639K row reads through the plain CSR bag
+            # kernel, with the bucket rows computed beforehand (no hashing) in
+            # one concatenated [26e5 x 16] table
+            big = t(np.concatenate(w.tables))
+            rows = dev.hash_bucket_int64(ids, w.num_buckets)
+            field = torch.repeat_interleave(
+                torch.arange(nf, device=device, dtype=torch.int64),
+                (offs[w.batch::w.batch] - offs[:-1:w.batch]))
+            grow = (rows + field * w.num_buckets).contiguous()
+            out2 = torch.empty((nf * w.batch, w.dim), dtype=torch.float32, device=device)
+            return Case(name, lambda i: dev.embedding_bag(big, grow, offs, 1, out=out2),
+                        alg, "hbm",
+                        "configs[3]'s 639K row reads with precomputed bucket rows (no hash): "
+                        "CSR bag kernel over the 26 tables concatenated, mean, out [26*8192x16]",
+                        "bag_kernel_config4_prehashed_rows")
+        tables = [t(x) for x in w.tables]
+        if name == "hashed_cold":
+            sets = [tables] + [[x.clone() for x in tables] for _ in range(COLD_TABLE_SETS - 1)]
+            return Case(name, lambda i: dev.hashed_embedding_bags(sets[i % len(sets)], nb, ids,
+                                                                  offs, w.batch, 1, out=out),
+                        alg, "hbm",
+                        wl + f"; launch i reads table set i % {COLD_TABLE_SETS} "
+                             f"({COLD_TABLE_SETS} x 26 x 6.4 MB), so every launch starts cold",
+                        "hashed_bags_config4_cold", launches=2 * COLD_TABLE_SETS,
+                        table_sets=COLD_TABLE_SETS)
+        return Case(name, lambda i: dev.hashed_embedding_bags(tables, nb, ids, offs, w.batch, 1,
+                                                              out=out),
+                    alg, "hbm", wl, "hashed_bags_config4", nnz=nnz)
+    if name == "hashed_dim32":
+        w = inp.get("config5").hashed
+        ids, offs = t(w.ids), t(w.offsets)
+        nf = len(w.tables)
+        tables = [t(x) for x in w.tables]
+        k0 = nf * w.dim + 13
+        buf = torch.zeros((w.batch, (k0 + 3) // 4 * 4), dtype=torch.float32, device=device)
+        out = buf[:, :nf * w.dim]
+        nnz = int(w.offsets[-1])
+        alg = 8 * nnz + 8 * (nf * w.batch + 1) + 4 * w.dim * nnz + 4 * w.batch * nf * w.dim
+        nb = [w.num_buckets] * nf
+        return Case(name, lambda i: dev.hashed_embedding_bags(tables, nb, ids, offs, w.batch, 1,
+                                                              out=out),
+                    alg, "hbm",
+                    "configs[4] hashed fields: 26 x batch 4096, Zipf ids, bags 1-5, tables "
+                    "[1e5x32], mean, written into the [4096x848] concat buffer",
+                    "hashed_bags_lds_config5_dim32", nnz=nnz)
+    if name in ("sparse_embedding2", "pooling"):
+        w = inp.get("config3")
+        bags, dim = w.offsets.size - 1, w.table.shape[1]
+        nnz = int(w.offsets[-1])
+        lens = np.diff(w.offsets)
+        width = int(lens.max())
+        pad = np.full((bags, width), -1, dtype=np.int64)
+        pad[np.arange(width)[None, :] < lens[:, None]] = w.ids
+        pad_d = t(pad)
+        table = t(w.table)
+        gathered = torch.empty((bags * width, dim), dtype=torch.float32, device=device)
+        wl = f"configs[2] ids padded to [{bags}, {width}] (-1 = masked), dim {dim}"
+        if name == "sparse_embedding2":
+            return Case(name, lambda i: dev.sparse_embedding2(table, pad_d, 0, out=gathered),
+                        8 * bags * width + 4 * dim * nnz + 4 * dim * bags * width, "hbm",
+                        wl + ": masked gather to [B*L, dim]", "sparse_embedding2_config3_padded")
+        dev.sparse_embedding2(table, pad_d, 0, out=gathered)
+        g3 = gathered.view(bags, width, dim)
+        # __pooling reads the gathered rows of positions with id > 0 only
+        return Case(name, lambda i: dev.pooling(pad_d, g3, (0, 0, 0), (bags, width, dim)),
+                    8 * bags * width + 4 * dim * nnz + 4 * dim * bags, "hbm",
+                    wl + ": masked mean over the gathered [B, L, dim]", "pooling_config3_padded")
+    if name in ("segment_reduce_sorted", "segment_reduce_any"):
+        w = inp.get("config3")
+        bags, dim = w.offsets.size - 1, w.table.shape[1]
+        nnz = int(w.offsets[-1])
+        table, ids = t(w.table), t(w.ids)
+        seg = t(np.repeat(np.arange(bags, dtype=np.int64), np.diff(w.offsets)))
+        srt = name.endswith("sorted")
+        return Case(name, lambda i: dev.segment_reduce(table, ids, seg, bags, 1, sorted_ids=srt),
+                    16 * nnz + 4 * dim * nnz + 4 * dim * bags, "hbm",
+                    "configs[2] as KPFusedSparseSegmentReduce inputs (indices, segment ids), mean, "
+                    + ("ids promised sorted" if srt else
+                       "no order assumed (stable counting sort by segment)"),
+                    f"segment_reduce_config3_{'sorted' if srt else 'any_order'}", launches=100)
+    if name == "hash_bucket":
+        h = inp.get("config4")
+        hid = t(h.ids)
+        return Case(name, lambda i: dev.hash_bucket_int64(hid, h.num_buckets),
+                    16 * h.ids.size, "hbm",
+                    f"configs[3] ids ({h.ids.size}) -> decimal -> Fingerprint64 % 1e5, int64 in "
+                    "and out (compute-bound: rate for reference only)", "hash_bucket_int64_config4",
+                    ids=int(h.ids.size))
+    if name == "copy":
+        src = torch.ones(64 << 20, dtype=torch.float32, device=device)
+        dst = torch.empty_like(src)
+        return Case(name, lambda i: dst.copy_(src), 2 * src.numel() * 4, "hbm",
+                    "torch copy of a 256 MiB float32 buffer (PMC calibration)",
+                    "pmc_copy_calibration", launches=10)
+    raise ValueError(f"unknown case {name!r}; choose from {CASES}")
+
+
+CASES = ("tower", "widedeep", "gemm_l1", "gemm_l2", "gemm_l3", "gemm_small", "gemm_e2e_l1", "batch_matmul",
+         "bag_sum", "bag_mean", "bag_sum_cold", "hashed", "hashed_cold", "hashed_nohash",
+         "hashed_dim32", "sparse_embedding2", "pooling", "segment_reduce_sorted",
+         "segment_reduce_any", "hash_bucket", "copy")
+# the cases reported under `components` (gemm_l1 is the roofline, copy the calibration)
+COMPONENT_CASES = ("gemm_small", "gemm_l2", "gemm_l3", "gemm_e2e_l1", "batch_matmul",
+                   "bag_sum", "bag_mean", "bag_sum_cold", "hashed", "hashed_cold",
+                   "hashed_nohash", "hashed_dim32", "sparse_embedding2", "pooling",
+                   "segment_reduce_sorted", "segment_reduce_any", "hash_bucket")
+
+
+def bench_case(c: Case, replays: int = 5) -> dict:
+    ms = graph_time_ms(c.fn, launches=c.launches, replays=replays)
+    res = {"workload": c.workload, "bound": c.bound,
+           ("algorithmic_bytes" if c.bound == "hbm" else "flops"): c.work,
+           "kernel_us": round(ms * 1e3, 3)}
+    res.update(c.rate(ms))
+    prof = read_profile(c.profile)
+    res["profile"] = f"profiles/{c.profile}.md"
+    if "rocprof_avg_ns" in prof:
+        r = c.rate(prof["rocprof_avg_ns"] * 1e-6)
+        res["rocprof_us"] = round(prof["rocprof_avg_ns"] * 1e-3, 3)
+        res.update({k + "_rocprof": v for k, v in r.items()})
+    if "traffic_bytes_per_launch" in prof:
+        res["traffic_bytes"] = prof["traffic_bytes_per_launch"]
+    res.update(c.extra)
+    log(f"{c.name}: {ms * 1e3:.2f} us, " + ", ".join(f"{k} {v}" for k, v in c.rate(ms).items()))
+    return res
 
 
 # ---------------------------------------------------------------- headline
-def bench_tower(args, device):
-    import numpy as np
+def bench_tower(args, device, inp: Inputs):
     import torch
-    from annc_amd import workloads, EPI_RELU
+    from annc_amd import EPI_RELU
     from annc_amd import device as dev
     from annc_amd.rec_graph import CapturedGraph, MLPTower
 
-    w = workloads.config2(seed=0)
+    w = inp.get("config2")
     tower = MLPTower(w.weights, w.biases, device=device, packed=True)
     x = torch.from_numpy(w.x).to(device)
     batch = x.shape[0]
     flops = tower.flops(batch)
     # One step = the 3-layer forward launched on one stream (3 kernels).  A
-    # HIP-graph replay per step is timed too: each graph launch adds a ~4 us
-    # boundary on the box, more than the host needs to enqueue 3 kernels.
+    # HIP-graph replay per step is timed too: each graph launch adds a few us
+    # of boundary on the box, more than the host needs to enqueue 3 kernels.
     ms, wall = time_steps(lambda: tower(x), args.steps, args.warmup)
     log(f"tower: {ms * 1e3:.1f} us/step ({wall * 1e6:.1f} us wall)")
     graph = CapturedGraph(tower, x)
@@ -129,6 +435,7 @@ def bench_tower(args, device):
     n = l1.weight.n
     k1_flops = 2.0 * m * n * k
     achieved = k1_flops / (k1_ms * 1e-3) / 1e12
+    prof = read_profile("gemm_layer1_4096x512x1024")
     roofline = {
         "kernel": "gemm_packed_pipe_kernel<4,2,1,1,4,2,1,true,false,false> (layer 1: 4096x512x1024 packed B + bias + ReLU)",
         "bound": "mfma",
@@ -136,37 +443,28 @@ def bench_tower(args, device):
         "peak": FP32_MFMA_PEAK_TFLOPS,
         "unit": "TFLOP/s",
         "frac": round(achieved / FP32_MFMA_PEAK_TFLOPS, 4),
-        "traffic": read_traffic("gemm_layer1_4096x512x1024"),
+        "traffic": prof.get("traffic_bytes_per_launch"),
         "avg_launch_us": round(k1_ms * 1e3, 3),
+        "rocprof_avg_us": (round(prof["rocprof_avg_ns"] * 1e-3, 3)
+                           if "rocprof_avg_ns" in prof else None),
         "flops_per_launch": k1_flops,
     }
     log(f"layer1 gemm: {k1_ms * 1e3:.2f} us, {achieved:.1f} TFLOP/s")
-    per_layer = []
-    h = x
-    for i, layer in enumerate(tower.layers):
-        o = tower.buffers(batch)[i]
-        ms_i = graph_time_ms(lambda j, h=h, layer=layer, o=o: dev.gemm(
-            h, layer.weight, bias=layer.bias, epilogue=layer.activation, out=o),
-            launches=50, replays=4)
-        kk, nn = layer.weight.k, layer.weight.n
-        per_layer.append({"m": batch, "n": nn, "k": kk, "us": round(ms_i * 1e3, 2),
-                          "tflops": round(2.0 * batch * nn * kk / (ms_i * 1e-3) / 1e12, 2)})
-        h = o
     value = flops / (ms * 1e-3) / 1e12
     return {"value": value, "ms": ms, "flops": flops, "batch": batch, "roofline": roofline,
-            "per_layer": per_layer, "inputs": w,
             "graph": {"us_per_step": round(graph_ms * 1e3, 2),
                       "tflops": round(flops / (graph_ms * 1e-3) / 1e12, 2)}}
 
 
 # ---------------------------------------------------------------- components
-def bench_config1(device):
+def bench_config1_call(device, inp: Inputs):
+    """configs[0] through the XLA custom-call ABI (synchronous call on
+    device-resident operands): median wall time of single calls."""
     import torch
-    from annc_amd import workloads, xla
-    w = workloads.config1(seed=0)
+    from annc_amd import xla
+    w = inp.get("config1")
     d = [torch.from_numpy(a).to(device) for a in (w.z, w.e, w.a, w.b)]
     out = torch.empty((512, 256), dtype=torch.float32, device=device)
-    # device-resident operands through the XLA custom-call ABI (synchronous)
     for _ in range(5):
         xla.matmul_add_relu(*d, out)
     # median of single synchronous calls: a rare host-side stall (tens of ms)
@@ -176,142 +474,17 @@ def bench_config1(device):
         t0 = time.perf_counter()
         xla.matmul_add_relu(*d, out)
         per_call.append(time.perf_counter() - t0)
-    sync_us = statistics.median(per_call) * 1e6
-    from annc_amd import device as dev, EPI_RELU
-    a, e, b = d[2], d[1], d[3]
-    k_ms = graph_time_ms(lambda i: dev.gemm(a, b, addend=e, epilogue=EPI_RELU, out=out),
-                         launches=100, replays=5)
-    flops = 2.0 * 512 * 256 * 256
-    return {"workload": "configs[0] __matmul_add_relu 512x256x256 fp32",
-            "kernel_us": round(k_ms * 1e3, 3),
-            "kernel_tflops": round(flops / (k_ms * 1e-3) / 1e12, 3),
-            "custom_call_sync_us_median": round(sync_us, 1),
-            "note": "launch-bound: 67.1 MFLOP is 0.43 us at peak"}
+    return {"workload": "configs[0] __matmul_add_relu custom call, device operands, synchronous",
+            "custom_call_sync_us_median": round(statistics.median(per_call) * 1e6, 1)}
 
 
-def bench_config3(device):
-    import numpy as np
+def bench_unique_gather(device, inp: Inputs):
+    """KPFusedGather engine on configs[2]'s ids: the unique count is read
+    back, so each call ends with a synchronisation (wall time)."""
     import torch
-    from annc_amd import workloads
     from annc_amd import device as dev
-    w = workloads.config3(seed=0)
-    table = torch.from_numpy(w.table).to(device)
-    ids = torch.from_numpy(w.ids).to(device)
-    offs = torch.from_numpy(w.offsets).to(device)
-    nnz, bags, dim = int(w.offsets[-1]), w.offsets.size - 1, w.table.shape[1]
-    alg_bytes = 8 * nnz + 8 * (bags + 1) + 4 * dim * nnz + 4 * dim * bags
-    uniq = int(np.unique(w.ids).size)
-    uniq_bytes = 8 * nnz + 8 * (bags + 1) + 4 * dim * uniq + 4 * dim * bags
-    out = torch.empty((bags, dim), dtype=torch.float32, device=device)
-    res = {"workload": "configs[2] embedding bag: table 1e6x64 fp32, 4096 bags, Poisson(20) "
-                       "lengths, Zipf(1.05) int64 ids, CSR",
-           "nnz": nnz, "unique_rows": uniq, "algorithmic_bytes": alg_bytes,
-           "unique_row_bytes": uniq_bytes}
-    for name, comb in (("sum", 0), ("mean", 1)):
-        k_ms = graph_time_ms(lambda i: dev.embedding_bag(table, ids, offs, comb, out=out),
-                             launches=200, replays=5)
-        gbs = alg_bytes / (k_ms * 1e-3) / 1e9
-        res[name] = {"kernel_us": round(k_ms * 1e3, 3), "GBps": round(gbs, 1),
-                     "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
-                     "unique_GBps": round(uniq_bytes / (k_ms * 1e-3) / 1e9, 1)}
-        log(f"bag {name}: {k_ms * 1e3:.2f} us, {gbs:.0f} GB/s")
-    # cache-defeating variant: rotate 3 table copies (768 MB > 256 MB MALL)
-    copies = [table] + [table.clone() for _ in range(2)]
-    k_ms = graph_time_ms(lambda i: dev.embedding_bag(copies[i % 3], ids, offs, 0, out=out),
-                         launches=201, replays=5)
-    res["sum_rotating_3_tables"] = {"kernel_us": round(k_ms * 1e3, 3),
-                                    "GBps": round(alg_bytes / (k_ms * 1e-3) / 1e9, 1)}
-    dev.stream_status()
-    del copies
-    return res, w
-
-
-def bench_config4(device):
-    import torch
-    from annc_amd import workloads
-    from annc_amd import device as dev
-    w = workloads.config4(seed=0)
-    tables = [torch.from_numpy(t).to(device) for t in w.tables]
-    ids = torch.from_numpy(w.ids).to(device)
-    offs = torch.from_numpy(w.offsets).to(device)
-    nf = len(tables)
-    out = torch.empty((w.batch, nf * w.dim), dtype=torch.float32, device=device)
-    nnz = int(w.offsets[-1])
-    alg_bytes = 8 * nnz + 8 * (nf * w.batch + 1) + 4 * w.dim * nnz + 4 * w.batch * nf * w.dim
-    nb = [w.num_buckets] * nf
-    k_ms = graph_time_ms(lambda i: dev.hashed_embedding_bags(tables, nb, ids, offs, w.batch, 1,
-                                                             out=out),
-                         launches=50, replays=5)
-    gbs = alg_bytes / (k_ms * 1e-3) / 1e9
-    log(f"hashed bags: {k_ms * 1e3:.2f} us, {gbs:.0f} GB/s")
-    return {"workload": "configs[3] 26 fields x batch 8192, int64 ids -> decimal -> "
-                        "Fingerprint64 % 1e5 -> gather [1e5x16] -> mean, out [8192x416]",
-            "nnz": nnz, "algorithmic_bytes": alg_bytes, "kernel_us": round(k_ms * 1e3, 3),
-            "GBps": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
-            "ids_per_s": round(nnz / (k_ms * 1e-3), 1)}
-
-
-def bench_other_rows(device, bag_inputs):
-    """The path's other operators, on the configs' inputs in the form each
-    operator takes them (no benchmark config names them): the XLA form of
-    configs[2] (sparse_embedding2 masked gather over padded [B, L] ids, then
-    __pooling), the TF segment-reduce form of configs[2], the KPFusedGather
-    engine on configs[2]'s ids, __batch_matmul at 32 x configs[0]'s shape,
-    and configs[3]'s bucket ids alone."""
-    import numpy as np
-    import torch
-    from annc_amd import workloads
-    from annc_amd import device as dev
-    res = {}
-    w = bag_inputs
-    bags, dim = w.offsets.size - 1, w.table.shape[1]
-    nnz = int(w.offsets[-1])
-    lens = np.diff(w.offsets)
-    table = torch.from_numpy(w.table).to(device)
-    ids = torch.from_numpy(w.ids).to(device)
-
-    # XLA form: ids padded to [B, L] with -1 (masked), gathered [B, L, dim], pooled
-    width = int(lens.max())
-    pad = np.full((bags, width), -1, dtype=np.int64)
-    pos = np.arange(width)[None, :] < lens[:, None]
-    pad[pos] = w.ids
-    pad_d = torch.from_numpy(pad).to(device)
-    gathered = torch.empty((bags * width, dim), dtype=torch.float32, device=device)
-    se_ms = graph_time_ms(lambda i: dev.sparse_embedding2(table, pad_d, 0, out=gathered),
-                          launches=50, replays=5)
-    g3 = gathered.view(bags, width, dim)
-    pool_ms = graph_time_ms(lambda i: dev.pooling(pad_d, g3, (0, 0, 0), (bags, width, dim)),
-                            launches=50, replays=5)
-    se_bytes = 8 * bags * width + 4 * dim * nnz + 4 * dim * bags * width
-    # __pooling reads the gathered rows of positions with id > 0 only
-    pool_bytes = 8 * bags * width + 4 * dim * nnz + 4 * dim * bags
-    for name, ms, nbytes in (("sparse_embedding2", se_ms, se_bytes),
-                             ("pooling", pool_ms, pool_bytes)):
-        gbs = nbytes / (ms * 1e-3) / 1e9
-        res[f"{name}_config3_padded"] = {
-            "workload": f"configs[2] ids padded to [{bags}, {width}] (-1 = masked), dim {dim}",
-            "algorithmic_bytes": nbytes, "kernel_us": round(ms * 1e3, 3), "GBps": round(gbs, 1),
-            "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
-        log(f"{name} (padded configs[2]): {ms * 1e3:.2f} us, {gbs:.0f} GB/s")
-
-    # KPFusedSparseSegmentReduce form: indices + per-position segment ids
-    seg = torch.from_numpy(np.repeat(np.arange(bags, dtype=np.int64), lens)).to(device)
-    sr_bytes = 16 * nnz + 4 * dim * nnz + 4 * dim * bags
-    for name, sorted_ids in (("sorted_ids", True), ("any_order", False)):
-        sr_ms = graph_time_ms(lambda i: dev.segment_reduce(table, ids, seg, bags, 1,
-                                                           sorted_ids=sorted_ids),
-                              launches=100, replays=5)
-        gbs = sr_bytes / (sr_ms * 1e-3) / 1e9
-        res[f"segment_reduce_config3_mean_{name}"] = {
-            "workload": "configs[2] as KPFusedSparseSegmentReduce inputs (indices, segment "
-                        "ids), " + ("ids promised sorted" if sorted_ids else
-                                    "no order assumed (stable counting sort by segment)"),
-            "algorithmic_bytes": sr_bytes, "kernel_us": round(sr_ms * 1e3, 3),
-            "GBps": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
-        log(f"segment reduce ({name}): {sr_ms * 1e3:.2f} us, {gbs:.0f} GB/s")
-
-    # KPFusedGather engine: sort-based unique + gather; the unique count is
-    # read back, so each call ends with a synchronisation (wall time)
+    w = inp.get("config3")
+    table, ids = torch.from_numpy(w.table).to(device), torch.from_numpy(w.ids).to(device)
     for _ in range(3):
         dev.unique_gather(table, ids)
     ts = []
@@ -319,46 +492,17 @@ def bench_other_rows(device, bag_inputs):
         t0 = time.perf_counter()
         u, _, _ = dev.unique_gather(table, ids)
         ts.append(time.perf_counter() - t0)
-    res["unique_gather_config3"] = {
-        "workload": f"configs[2] ids ({nnz} keys, {int(u.numel())} unique) -> unique, "
-                    "inverse index, gathered rows",
-        "wall_us_median": round(statistics.median(ts) * 1e6, 1),
-        "keys_per_s": round(nnz / statistics.median(ts), 1)}
-
-    # __batch_matmul: 32 independent configs[0]-shaped products, row-major B
-    g = workloads.rng(5)
-    bm, m, k, n = 32, 512, 256, 256
-    a = torch.from_numpy(g.standard_normal((bm, m, k)).astype(np.float32)).to(device)
-    b = torch.from_numpy((g.standard_normal((bm, k, n)) / 16).astype(np.float32)).to(device)
-    c = torch.empty((bm, m, n), dtype=torch.float32, device=device)
-    bm_ms = graph_time_ms(lambda i: dev.gemm(a, b, out=c), launches=50, replays=5)
-    tf = 2.0 * bm * m * n * k / (bm_ms * 1e-3) / 1e12
-    res["batch_matmul_32x512x256x256"] = {
-        "workload": "__batch_matmul, 32 x [512x256] . [256x256] fp32, row-major B",
-        "kernel_us": round(bm_ms * 1e3, 3), "tflops": round(tf, 2),
-        "mfma_frac": round(tf / FP32_MFMA_PEAK_TFLOPS, 4)}
-    log(f"batch matmul: {bm_ms * 1e3:.2f} us, {tf:.1f} TFLOP/s")
-
-    # bucket ids alone (decimal text -> Fingerprint64 -> % 1e5) on configs[3]'s ids
-    h = workloads.config4(seed=0)
-    hid = torch.from_numpy(h.ids).to(device)
-    hb_ms = graph_time_ms(lambda i: dev.hash_bucket_int64(hid, h.num_buckets),
-                          launches=50, replays=5)
-    res["hash_bucket_int64_config4"] = {
-        "workload": f"configs[3] ids ({h.ids.size}) -> bucket ids, int64 in and out",
-        "kernel_us": round(hb_ms * 1e3, 3),
-        "ids_per_s": round(h.ids.size / (hb_ms * 1e-3), 1),
-        "GBps": round(16 * h.ids.size / (hb_ms * 1e-3) / 1e9, 1)}
-    log(f"hash bucket ids: {hb_ms * 1e3:.2f} us")
-    dev.stream_status()
-    return res
+    nnz = int(w.offsets[-1])
+    return {"workload": f"configs[2] ids ({nnz} keys, {int(u.numel())} unique) -> unique, "
+                        "inverse index, gathered rows",
+            "wall_us_median": round(statistics.median(ts) * 1e6, 1),
+            "keys_per_s": round(nnz / statistics.median(ts), 1)}
 
 
-def bench_config5(device, steps: int):
+def bench_config5(device, inp: Inputs, steps: int):
     import torch
-    from annc_amd import workloads
     from annc_amd.rec_graph import CapturedGraph, WideDeepConfig, WideDeepGraph
-    w = workloads.config5(seed=0)
+    w = inp.get("config5")
     h = w.hashed
     graph = WideDeepGraph(WideDeepConfig(), [torch.from_numpy(t) for t in h.tables], w.weights,
                           w.biases, device=device)
@@ -371,9 +515,8 @@ def bench_config5(device, steps: int):
     dense.copy_(torch.from_numpy(w.dense).to(device))
     # One step = the whole graph (hashed bags into the concat buffer, 4 GEMMs),
     # timed both as one HIP-graph replay and as its kernels launched on one
-    # stream;
-    # which is faster varies from box to box (±6%), so the step is the faster
-    # of the two and both are reported.
+    # stream; which is faster varies from box to box, so the step is the
+    # faster of the two and both are reported.
     replay = CapturedGraph(graph, ids, offs, dense)
     graph_ms, _ = time_steps(replay.replay, steps, 5)
     eager_ms, _ = time_steps(lambda: graph(ids, offs, dense), steps, 5)
@@ -411,125 +554,136 @@ def cpu_model() -> str:
     return "unknown"
 
 
-def cpu_baseline(inputs, bag_inputs):
-    """Oracle (OpenBLAS 0.3.29 sgemm + loops) on the host: the whole config-2
-    tower at batch 4096, median of 5 after one warm-up, 1 thread and all cores."""
+def cpu_median_s(fn, reps: int = 5) -> float:
+    """Median wall seconds of `reps` calls after one warm-up call."""
+    fn()
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return statistics.median(ts)
+
+
+def cpu_baseline(inp: Inputs):
+    """The oracle's CPU path (the reference's: OpenBLAS 0.3.29 sgemm, the
+    sequential per-bag loops, FarmHash per id) for every configuration, at 1
+    thread (the reference convention) and at all cores of the affinity mask;
+    median of 5 after a warm-up.  `value` is configs[1], the headline."""
     import numpy as np
     from oracle import ora
 
-    x, ws, bs = inputs.x, inputs.weights, inputs.biases
-    flops = 2.0 * x.shape[0] * sum(w.shape[0] * w.shape[1] for w in ws)
-    res = {}
-    for threads in (1, cpu_cores()):
-        ora.set_threads(threads)
-        ora.mlp_tower(x, ws, bs)
-        ts = []
-        for _ in range(5):
-            t0 = time.perf_counter()
-            ora.mlp_tower(x, ws, bs)
-            ts.append(time.perf_counter() - t0)
-        res[threads] = flops / statistics.median(ts) / 1e12
     cores = cpu_cores()
-    out = {"value": round(res[cores], 4), "unit": "TFLOP/s", "cores": cores, "kind": "port",
-           "sample": "full configs[1] tower (batch 4096, 5.37 GFLOP) x5 reps, median; "
-                     "OpenBLAS 0.3.29 sgemm + bias/ReLU/sigmoid loops",
-           "single_thread_value": round(res[1], 4), "blas": ora.blas_config(),
-           "cpu_model": cpu_model(), "affinity_cpus": len(os.sched_getaffinity(0))}
-    if bag_inputs is not None:
-        w = bag_inputs
-        bags, dim = w.offsets.size - 1, w.table.shape[1]
-        nnz = int(w.offsets[-1])
-        alg = 8 * nnz + 8 * (bags + 1) + 4 * dim * nnz + 4 * dim * bags
-        bag = {}
-        # OpenBLAS's worker threads spin for a while after the tower's last
-        # sgemm; one BLAS thread and a pause keep them off the cores the bag
-        # loop uses.  The box's CPU share can be smaller than its affinity
-        # mask, so several thread counts are timed and the best is reported.
-        ora.set_threads(1)
-        time.sleep(1.0)
-        for threads in sorted({1, 4, 8, cores}):
-            ora.embedding_bag(w.table, w.ids, w.offsets, 0, threads=threads)
-            ts = []
-            for _ in range(5):
-                t0 = time.perf_counter()
-                ora.embedding_bag(w.table, w.ids, w.offsets, 0, threads=threads)
-                ts.append(time.perf_counter() - t0)
-            bag[f"threads_{threads}_GBps"] = round(alg / statistics.median(ts) / 1e9, 2)
-        best = max((v, k) for k, v in bag.items())
-        bag["best"] = {"GBps": best[0], "threads": int(best[1].split("_")[1])}
-        out["embedding_bag_config3_sum"] = bag
-    return out
+    threads = sorted({1, cores})
+    res = {}
+
+    def entry(fn, work, scale, unit, sample, blas):
+        out = {"unit": unit, "sample": sample}
+        for t in threads:
+            if blas:
+                ora.set_threads(t)
+            else:
+                # OpenBLAS's workers spin for a while after an sgemm; one BLAS
+                # thread and a pause keep them off the cores the loops use
+                ora.set_threads(1)
+                time.sleep(0.5)
+            sec = cpu_median_s(lambda: fn(t))
+            out[f"threads_{t}"] = round(work / sec / scale, 4)
+            out[f"threads_{t}_ms"] = round(sec * 1e3, 3)
+        return out
+
+    c1 = inp.get("config1")
+    res["config1_matmul_add_relu"] = entry(
+        lambda t: ora.matmul_add_relu(c1.e, c1.a, c1.b), 2.0 * 512 * 256 * 256, 1e12, "TFLOP/s",
+        "configs[0] 512x256x256: memcpy of the materialised addend, sgemm beta=1, ReLU loop "
+        "(gemm_rewriter.cc:249-281)", True)
+    c2 = inp.get("config2")
+    flops2 = 2.0 * c2.x.shape[0] * sum(w.shape[0] * w.shape[1] for w in c2.weights)
+    res["config2_tower"] = entry(
+        lambda t: ora.mlp_tower(c2.x, c2.weights, c2.biases), flops2, 1e12, "TFLOP/s",
+        "full configs[1] tower (batch 4096, 5.37 GFLOP): sgemm + bias/ReLU/sigmoid loops", True)
+    c3 = inp.get("config3")
+    bags3, dim3 = c3.offsets.size - 1, c3.table.shape[1]
+    bytes3 = _bag_bytes(int(c3.offsets[-1]), bags3, dim3)
+    for comb, cname in ((0, "sum"), (1, "mean")):
+        res[f"config3_bag_{cname}"] = entry(
+            lambda t, comb=comb: ora.embedding_bag(c3.table, c3.ids, c3.offsets, comb, threads=t),
+            bytes3, 1e9, "GB/s (algorithmic bytes)",
+            f"full configs[2] bag ({cname}): per-bag sequential row adds "
+            "(embedding_fused_sparse_segment_reduce.cc:92-131), OpenMP over bags", False)
+    c4 = inp.get("config4")
+    nf4 = len(c4.tables)
+    nnz4 = int(c4.offsets[-1])
+    bytes4 = 8 * nnz4 + 8 * (nf4 * c4.batch + 1) + 4 * c4.dim * nnz4 + 4 * c4.batch * nf4 * c4.dim
+    res["config4_hashed_bags"] = entry(
+        lambda t: ora.hashed_embedding_bags(c4.tables, c4.num_buckets, c4.ids, c4.offsets,
+                                            c4.batch, 1, threads=t),
+        bytes4, 1e9, "GB/s (algorithmic bytes)",
+        f"full configs[3] ({nnz4} ids): decimal text, Fingerprint64 % 1e5 per id "
+        "(fused_embedding_with_hash_bucket.cc:61-77), mean per bag in id order, OpenMP over bags",
+        False)
+    res["config4_hashed_bags"]["ids_per_s_threads_1"] = round(
+        nnz4 / (res["config4_hashed_bags"]["threads_1_ms"] * 1e-3), 1)
+    c5 = inp.get("config5")
+    h5 = c5.hashed
+    nf5 = len(h5.tables)
+    e5 = [np.ascontiguousarray(np.broadcast_to(b, (h5.batch, b.size))) for b in c5.biases[:-1]]
+
+    def graph5(t):
+        emb = ora.hashed_embedding_bags(h5.tables, h5.num_buckets, h5.ids, h5.offsets, h5.batch,
+                                        1, threads=t)
+        h = np.concatenate([emb, c5.dense], axis=1)      # XLA concat fusion
+        for w, e in zip(c5.weights[:-1], e5):            # __matmul_add_relu (E materialised)
+            h = ora.matmul_add_relu(e, h, w)
+        return ora.dense_layer(h, c5.weights[-1], c5.biases[-1], 2)   # XLA dot + sigmoid
+
+    res["config5_wide_deep"] = entry(
+        graph5, h5.batch, 1.0, "samples/s",
+        f"full configs[4] graph, batch {h5.batch}: {nf5} hashed bags (dim {h5.dim}, mean), concat "
+        "with the 13 dense features, 3 x __matmul_add_relu (memcpy E, sgemm beta=1, ReLU), "
+        "256->1 dot + sigmoid", True)
+    ora.set_threads(1)
+    top = res["config2_tower"]
+    return {"value": top[f"threads_{cores}"], "unit": "TFLOP/s", "cores": cores, "kind": "port",
+            "sample": "full configs[1] tower (batch 4096, 5.37 GFLOP) x5 reps, median; OpenBLAS "
+                      "0.3.29 sgemm + bias/ReLU/sigmoid loops",
+            "single_thread_value": top["threads_1"], "blas": ora.blas_config(),
+            "cpu_model": cpu_model(), "affinity_cpus": len(os.sched_getaffinity(0)),
+            "configs": res}
 
 
-KERNELS = ("gemm_l1", "gemm_l2", "batch_matmul", "bag_sum", "bag_mean", "hashed", "copy")
-
-
-def profile_kernel(name: str, launches: int, device) -> dict:
-    """Launch one hot-path kernel `launches` times back to back, eagerly, for
-    rocprofv3 (--kernel-trace --stats, or --pmc FETCH_SIZE / WRITE_SIZE).
+# ---------------------------------------------------------------- profiling mode
+def profile_case(name: str, launches: int, graph: bool, device) -> dict:
+    """Launch one case `launches` times back to back, for rocprofv3
+    (--kernel-trace --stats, or --pmc FETCH_SIZE / WRITE_SIZE).  Eager by
+    default; with `graph`, as the components time it: one HIP graph of
+    `launches` launches, replayed 5 times, whose HIP-event average per launch
+    is printed beside the launch count.
 
     `copy` is the calibration kernel for the PMC byte counters: torch's copy
     of a 256 MiB float32 buffer, which reads and writes exactly 256 MiB."""
     import torch
-    from annc_amd import EPI_RELU, workloads
-    from annc_amd import device as dev
-
-    info: dict = {"kernel": name, "launches": launches}
-    if name in ("gemm_l1", "gemm_l2"):
-        w = workloads.config2(seed=0)
-        li = 0 if name == "gemm_l1" else 1
-        x = torch.from_numpy(w.x).to(device)
-        if li == 1:
-            x = torch.relu(x[:, :512]).contiguous()
-        wt = dev.pack_weight(torch.from_numpy(w.weights[li]).to(device))
-        bias = torch.from_numpy(w.biases[li]).to(device)
-        out = torch.empty((x.shape[0], wt.n), dtype=torch.float32, device=device)
-        fn = lambda: dev.gemm(x, wt, bias=bias, epilogue=EPI_RELU, out=out)  # noqa: E731
-        info.update(m=x.shape[0], n=wt.n, k=wt.k, flops_per_launch=2 * x.shape[0] * wt.n * wt.k)
-    elif name == "batch_matmul":
-        # the components' __batch_matmul case: 32 x configs[0]'s shape, row-major B
-        import numpy as np
-        g = workloads.rng(5)
-        bm, m, k, n = 32, 512, 256, 256
-        a = torch.from_numpy(g.standard_normal((bm, m, k)).astype(np.float32)).to(device)
-        b = torch.from_numpy((g.standard_normal((bm, k, n)) / 16).astype(np.float32)).to(device)
-        out = torch.empty((bm, m, n), dtype=torch.float32, device=device)
-        fn = lambda: dev.gemm(a, b, out=out)  # noqa: E731
-        info.update(batch=bm, m=m, n=n, k=k, flops_per_launch=2 * bm * m * n * k,
-                    algorithmic_bytes=4 * bm * (m * k + k * n + m * n))
-    elif name in ("bag_sum", "bag_mean"):
-        w = workloads.config3(seed=0)
-        table = torch.from_numpy(w.table).to(device)
-        ids = torch.from_numpy(w.ids).to(device)
-        offs = torch.from_numpy(w.offsets).to(device)
-        nnz, bags, dim = int(w.offsets[-1]), w.offsets.size - 1, w.table.shape[1]
-        out = torch.empty((bags, dim), dtype=torch.float32, device=device)
-        comb = 0 if name == "bag_sum" else 1
-        fn = lambda: dev.embedding_bag(table, ids, offs, comb, out=out)  # noqa: E731
-        info.update(algorithmic_bytes=8 * nnz + 8 * (bags + 1) + 4 * dim * nnz + 4 * dim * bags)
-    elif name == "hashed":
-        w = workloads.config4(seed=0)
-        tables = [torch.from_numpy(t).to(device) for t in w.tables]
-        ids = torch.from_numpy(w.ids).to(device)
-        offs = torch.from_numpy(w.offsets).to(device)
-        nf = len(tables)
-        out = torch.empty((w.batch, nf * w.dim), dtype=torch.float32, device=device)
-        nb = [w.num_buckets] * nf
-        fn = lambda: dev.hashed_embedding_bags(tables, nb, ids, offs, w.batch, 1,  # noqa: E731
-                                               out=out)
-        nnz = int(w.offsets[-1])
-        info.update(algorithmic_bytes=8 * nnz + 8 * (nf * w.batch + 1) + 4 * w.dim * nnz
-                    + 4 * w.batch * nf * w.dim)
-    elif name == "copy":
-        src = torch.ones(64 << 20, dtype=torch.float32, device=device)
-        dst = torch.empty_like(src)
-        fn = lambda: dst.copy_(src)  # noqa: E731
-        info.update(bytes_read=src.numel() * 4, bytes_written=dst.numel() * 4)
-    else:
-        raise ValueError(f"unknown kernel {name!r}; choose from {KERNELS}")
+    c = make_case(name, device, Inputs())
+    info = {"case": name, "workload": c.workload, "bound": c.bound, "work_per_launch": c.work,
+            "profile": c.profile}
     torch.cuda.synchronize()
-    for i in range(launches):
-        fn()
+    if graph:
+        replays = 5
+        launches = launches or c.launches
+        g = {}
+        ms = graph_time_ms(c.fn, launches=launches, replays=replays, info=g)
+        # the capture's 2 eager warm-ups, the untimed settling replays, then
+        # the timed ones: the last replays * launches in the trace
+        info.update(mode="graph", settle_replays=g["settle_replays"],
+                    timed_launches=launches * replays,
+                    launches_total=launches * (2 + g["settle_replays"] + replays),
+                    event_us_per_launch=round(ms * 1e3, 3))
+    else:
+        launches = launches or 20
+        c.fn(0)
+        for i in range(launches):
+            c.fn(i + 1)
+        info.update(mode="eager", launches_total=launches + 1)
     torch.cuda.synchronize()
     return info
 
@@ -538,12 +692,17 @@ def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=500)
-    ap.add_argument("--warmup", type=int, default=50)
+    # untimed steps: after start-up the clocks need a few ms of load to settle
+    ap.add_argument("--warmup", type=int, default=500)
     ap.add_argument("--no-components", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--kernel", choices=KERNELS, default=None,
-                    help="profiling mode: launch only this kernel --launches times")
-    ap.add_argument("--launches", type=int, default=20)
+    ap.add_argument("--kernel", choices=CASES, default=None,
+                    help="profiling mode: launch only this case --launches times")
+    ap.add_argument("--launches", type=int, default=None,
+                    help="profiling mode: launches (default: the case's own count with "
+                         "--graph, else 20)")
+    ap.add_argument("--graph", action="store_true",
+                    help="profiling mode: launch through a replayed HIP graph")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build targets one GPU; --gpus must be 1 (GEMMs "
@@ -557,23 +716,21 @@ def main() -> int:
     device = torch.device("cuda:0")
     torch.cuda.set_device(device)
     if args.kernel:
-        print(json.dumps(profile_kernel(args.kernel, args.launches, device)), flush=True)
+        print(json.dumps(profile_case(args.kernel, args.launches, args.graph, device)), flush=True)
         return 0
 
-    tower = bench_tower(args, device)
-    components = {}
-    bag_inputs = None
+    inp = Inputs()
+    tower = bench_tower(args, device, inp)
+    components = {"tower_graph_replay_config2": tower["graph"]}
     if not args.no_components:
-        components["matmul_add_relu_config1"] = bench_config1(device)
-        components["embedding_bag_config3"], bag_inputs = bench_config3(device)
-        components["hashed_bags_config4"] = bench_config4(device)
-        components["wide_deep_e2e_config5"] = bench_config5(device, steps=100)
+        for name in COMPONENT_CASES:
+            components[name] = bench_case(make_case(name, device, inp))
+            torch.cuda.empty_cache()
+        components["matmul_add_relu_config1_custom_call"] = bench_config1_call(device, inp)
+        components["unique_gather_config3"] = bench_unique_gather(device, inp)
+        components["wide_deep_e2e_config5"] = bench_config5(device, inp, steps=100)
         torch.cuda.empty_cache()
-        components["other_rows"] = bench_other_rows(device, bag_inputs)
-        torch.cuda.empty_cache()
-    components["tower_layers_config2"] = tower["per_layer"]
-    components["tower_graph_replay_config2"] = tower["graph"]
-    cpu = None if args.no_cpu else cpu_baseline(tower["inputs"], bag_inputs)
+    cpu = None if args.no_cpu else cpu_baseline(inp)
 
     line = {
         "metric": METRIC,
