@@ -108,24 +108,44 @@ __device__ __forceinline__ uint32_t group_bcast(uint32_t v) {
 }
 
 
-// One bag per group of G lanes (64/G bags share a wave).  The bag is walked
-// in rounds of kGroupRound positions: the round's ids are fetched (clamped
-// into the bag, so every load is valid and no per-position exec mask is
-// needed; lanes fetch distinct ids and broadcast them inside the group),
-// then all of the round's row chunks, and only then are the first
-// `cnt` rows added in index order.  A bag of n ids costs ceil(n/32) id->row
-// round trips.
-template <typename IdxT, int G, int VEC, bool MEAN, bool PERM, bool BUF>
-__global__ __launch_bounds__(kThreads) void bag_kernel(
-    const float* __restrict__ table, int64_t rows, int64_t dim, const IdxT* __restrict__ ids,
-    const int32_t* __restrict__ perm, const int64_t* __restrict__ offsets, int64_t num_bags,
-    float* __restrict__ out, int64_t ldo, int* __restrict__ status) {
+// Row ids of bag positions from global memory: ids[at] or, through a
+// permutation, ids[perm[at]] (every slot loaded: the clamped positions are
+// valid; permuted positions first, then the ids they name, so each level is
+// waited for once).
+template <typename IdxT, bool PERM>
+struct GlobalIds {
+  const IdxT* ids;
+  const int32_t* perm;
+  template <int K>
+  __device__ __forceinline__ void operator()(int64_t (&at)[K], const bool (&loaded)[K],
+                                             int64_t (&idv)[K]) const {
+    if constexpr (PERM) {
+#pragma unroll
+      for (int t = 0; t < K; ++t) at[t] = perm[at[t]];
+#pragma unroll
+      for (int t = 0; t < K; ++t) idv[t] = static_cast<int64_t>(ids[at[t]]);
+    } else {
+#pragma unroll
+      for (int t = 0; t < K; ++t) idv[t] = loaded[t] ? static_cast<int64_t>(ids[at[t]]) : 0;
+    }
+  }
+};
+
+// One bag, reduced by this lane's aligned group of G lanes (every lane of
+// the group calls it with the same bag; groups of a wave may hold different
+// bags).  The bag is walked in rounds of kGroupRound positions: the round's
+// ids are fetched (clamped into the bag, so every load is valid and no
+// per-position exec mask is needed; lanes fetch distinct ids and broadcast
+// them inside the group), then all of the round's row chunks, and only then
+// are the first `cnt` rows added in index order.  A bag of n ids costs
+// ceil(n/32) id->row round trips.  Returns true if an id was outside the
+// table.
+template <int G, int VEC, bool MEAN, bool BUF, typename Fetch>
+__device__ __forceinline__ bool bag_group(const float* __restrict__ table, int64_t rows,
+                                          int64_t dim, int64_t beg, int64_t end,
+                                          const Fetch& fetch, float* __restrict__ out_row) {
   typedef typename VecT<VEC>::type V;
   const int g = threadIdx.x & (G - 1);
-  const int64_t bag = ((int64_t)blockIdx.x * kThreads + threadIdx.x) / G;
-  if (bag >= num_bags) return;
-  const int64_t beg = offsets[bag];
-  const int64_t end = offsets[bag + 1];
   bool bad = false;
   // Every lane of the group runs the same chunk and round loops (the row
   // broadcasts read all G lanes); lanes past `dim` read the zero vector.
@@ -164,17 +184,7 @@ __global__ __launch_bounds__(kThreads) void bag_kernel(
         loaded[t] = t == 0 || __ballot(cnt > G * t) != 0;
         at[t] = j0 + min(g + G * t, cnt - 1);
       }
-      if constexpr (PERM) {
-        // every slot (clamped positions are valid): permuted positions first,
-        // then the ids they name, so each level is waited for once
-#pragma unroll
-        for (int t = 0; t < kPer; ++t) at[t] = perm[at[t]];
-#pragma unroll
-        for (int t = 0; t < kPer; ++t) idv[t] = static_cast<int64_t>(ids[at[t]]);
-      } else {
-#pragma unroll
-        for (int t = 0; t < kPer; ++t) idv[t] = loaded[t] ? static_cast<int64_t>(ids[at[t]]) : 0;
-      }
+      fetch(at, loaded, idv);
       uint32_t mine[kPer];
 #pragma unroll
       for (int t = 0; t < kPer; ++t) {
@@ -218,8 +228,21 @@ __global__ __launch_bounds__(kThreads) void bag_kernel(
       const int32_t n = static_cast<int32_t>(end - beg);
       if (n > 0) acc *= 1.0f / static_cast<float>(n);
     }
-    if (active) store_row<VEC>(out + bag * ldo + c, acc);
+    if (active) store_row<VEC>(out_row + c, acc);
   }
+  return bad;
+}
+
+// One bag per group of G lanes (64/G bags share a wave).
+template <typename IdxT, int G, int VEC, bool MEAN, bool PERM, bool BUF>
+__global__ __launch_bounds__(kThreads) void bag_kernel(
+    const float* __restrict__ table, int64_t rows, int64_t dim, const IdxT* __restrict__ ids,
+    const int32_t* __restrict__ perm, const int64_t* __restrict__ offsets, int64_t num_bags,
+    float* __restrict__ out, int64_t ldo, int* __restrict__ status) {
+  const int64_t bag = ((int64_t)blockIdx.x * kThreads + threadIdx.x) / G;
+  if (bag >= num_bags) return;
+  const bool bad = bag_group<G, VEC, MEAN, BUF>(table, rows, dim, offsets[bag], offsets[bag + 1],
+                                                GlobalIds<IdxT, PERM>{ids, perm}, out + bag * ldo);
   if (bad) atomicOr(status, 1);
 }
 
@@ -500,6 +523,440 @@ __global__ __launch_bounds__(kThreads) void cs_scatter_kernel(const int64_t* __r
       perm[base + rank] = static_cast<int32_t>(i);
       if (rank + 1 == cnt) cs_lds[s] = base + cnt;
     }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Two-level stable sort of positions by segment (at most kCsMaxSegments
+// segments and kTlMaxBlocks blocks of positions), in two launches before
+// the bag kernel:
+//   1. seg_block_sort: each block of kTlBlock positions is sorted by segment
+//      range (bucket = segment / S; ids outside [0, batch) go to bucket
+//      kTlBuckets), stably: equal buckets keep their position order.  It
+//      writes the sorted positions, their segments, and bstart[block][b],
+//      the first sorted index of bucket b (b = 0..kTlBuckets).
+//   2. seg_range: workgroup g owns the S segments of bucket g and takes the
+//      slice [bstart[a][g], bstart[a][g+1]) of every block a.  Blocks in
+//      order, each slice in position order: the concatenation is in position
+//      order.  The sum of bstart[a][g] over the blocks counts the kept
+//      positions of the buckets before g, which is where the range starts in
+//      perm, so no workgroup waits for another.  It ranks its positions by
+//      segment in LDS (ballot match over log2(S) bits, 64 entries per wave
+//      step, as cs_scatter) and writes perm and its segments' offsets.
+// ---------------------------------------------------------------------------
+constexpr int kTlThreads = 256;
+constexpr int kTlWaves = kTlThreads / 64;
+constexpr int kTlItems = 4;
+constexpr int kTlBlock = kTlThreads * kTlItems;  // positions per block
+constexpr int kTlBuckets = 256;                   // segment ranges
+constexpr int kTlBucketBits = 9;                  // bucket kTlBuckets: dropped ids
+constexpr int kTlMaxBlocks = 4096;                // up to 4 Mi positions
+constexpr int kTlPer = kTlMaxBlocks / kTlThreads; // blocks per thread in step 2
+constexpr int kTlCap = 8192;                      // step 2's list (LDS)
+constexpr int kTlMaxS = 64;                       // segments per range
+constexpr int kTlMaxSBits = 6;
+static_assert(kCsMaxSegments <= int64_t(kTlBuckets) * kTlMaxS, "segment ranges");
+
+// ROWS: the row id of every sorted position (indices[p], or 0xffffffff for
+// an id outside [0, rows)) instead of the position, for the fused reduction
+// of step 2.
+template <typename IdxT, bool ROWS>
+__global__ __launch_bounds__(kTlThreads) void seg_block_sort_kernel(
+    const int64_t* __restrict__ seg, int64_t stride, int64_t n, int batch, int S,
+    const IdxT* __restrict__ indices, int64_t rows, uint32_t* __restrict__ sorted_pos,
+    uint16_t* __restrict__ sorted_seg, uint32_t* __restrict__ sorted_row,
+    uint32_t* __restrict__ bstart) {
+  // Positions are striped (item i of thread t is position b0 + i*256 + t),
+  // so the wave steps (i, wave) taken in order visit positions in order.
+  // Each step ranks its lanes per bucket by a ballot match over the bucket
+  // bits; cnt[i][wave][b] holds the step's bucket counts.  An entry's slot
+  // is then start[b] + (b's entries in the steps before) + its rank.
+  constexpr int kSteps = kTlItems * kTlWaves;
+  __shared__ uint16_t cnt[kSteps][kTlBuckets + 1];
+  __shared__ uint32_t start[kTlBuckets + 1];
+  __shared__ uint32_t wsum[kTlWaves];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const uint64_t lt = (uint64_t(1) << lane) - 1;
+  const int64_t b0 = (int64_t)blockIdx.x * kTlBlock;
+  // unconditional loads (position clamped to n - 1), so they travel together
+  int64_t v[kTlItems], iv[kTlItems];
+#pragma unroll
+  for (int i = 0; i < kTlItems; ++i) {
+    const int64_t p = b0 + i * kTlThreads + t;
+    v[i] = seg[(p < n ? p : n - 1) * stride];
+    if constexpr (ROWS) iv[i] = static_cast<int64_t>(indices[p < n ? p : n - 1]);
+  }
+  uint16_t* cflat = &cnt[0][0];
+  for (int k = t; k < kSteps * (kTlBuckets + 1); k += kTlThreads) cflat[k] = 0;
+  uint32_t key[kTlItems], rank[kTlItems];
+#pragma unroll
+  for (int i = 0; i < kTlItems; ++i) {
+    const int64_t p = b0 + i * kTlThreads + t;
+    const bool ok = p < n && v[i] >= 0 && v[i] < batch;
+    key[i] = ok ? static_cast<uint32_t>(v[i]) / static_cast<uint32_t>(S) : kTlBuckets;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < kTlItems; ++i) {
+    uint64_t same = ~uint64_t(0);
+#pragma unroll
+    for (int bit = 0; bit < kTlBucketBits; ++bit) {
+      const bool on = (key[i] >> bit) & 1u;
+      const uint64_t bb = __ballot(on);
+      same &= on ? bb : ~bb;
+    }
+    rank[i] = static_cast<uint32_t>(__popcll(same & lt));
+    if (rank[i] == 0) cnt[i * kTlWaves + wave][key[i]] = static_cast<uint16_t>(__popcll(same));
+  }
+  __syncthreads();
+  // per bucket: counts before each step (in place), total, and the bucket
+  // starts by a block scan of the totals (thread t: bucket t; the last
+  // thread also takes the dropped bucket kTlBuckets)
+  auto prefix_steps = [&](int b) {
+    uint32_t c[kSteps];  // all loads first, so they travel together
+#pragma unroll
+    for (int k = 0; k < kSteps; ++k) c[k] = cnt[k][b];
+    uint32_t run = 0;
+#pragma unroll
+    for (int k = 0; k < kSteps; ++k) {
+      cnt[k][b] = static_cast<uint16_t>(run);
+      run += c[k];
+    }
+    return run;
+  };
+  const uint32_t tot = prefix_steps(t);
+  if (t == kTlThreads - 1) prefix_steps(kTlBuckets);
+  uint32_t inc = tot;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const uint32_t x = __shfl_up(inc, off, 64);
+    if (lane >= off) inc += x;
+  }
+  if (lane == 63) wsum[wave] = inc;
+  __syncthreads();
+  uint32_t before = inc - tot;
+  for (int w = 0; w < wave; ++w) before += wsum[w];
+  start[t] = before;
+  if (t == kTlThreads - 1) start[kTlBuckets] = before + tot;  // first dropped entry
+  __syncthreads();
+  uint32_t* bs = bstart + (int64_t)blockIdx.x * (kTlBuckets + 1);
+  bs[t] = start[t];
+  if (t == kTlThreads - 1) bs[kTlBuckets] = start[kTlBuckets];
+#pragma unroll
+  for (int i = 0; i < kTlItems; ++i) {
+    const uint32_t slot = start[key[i]] + cnt[i * kTlWaves + wave][key[i]] + rank[i];
+    if constexpr (!ROWS) sorted_pos[b0 + slot] = static_cast<uint32_t>(b0 + i * kTlThreads + t);
+    sorted_seg[b0 + slot] = key[i] < kTlBuckets ? static_cast<uint16_t>(v[i]) : uint16_t(0);
+    if constexpr (ROWS)
+      sorted_row[b0 + slot] = static_cast<uint64_t>(iv[i]) < static_cast<uint64_t>(rows)
+                                  ? static_cast<uint32_t>(iv[i]) : 0xffffffffu;
+  }
+}
+
+// Row ids of bag positions from a global list of row ids (uint32; ids
+// outside the table are 0xffffffff).
+struct GlobalRows {
+  const int32_t* rows;
+  template <int K>
+  __device__ __forceinline__ void operator()(int64_t (&at)[K], const bool (&)[K],
+                                             int64_t (&idv)[K]) const {
+#pragma unroll
+    for (int t = 0; t < K; ++t) idv[t] = static_cast<int64_t>(static_cast<uint32_t>(rows[at[t]]));
+  }
+};
+
+// Row ids of bag positions from LDS (the fused reduction's ranked list).
+struct LdsIds {
+  const uint32_t* rows;
+  template <int K>
+  __device__ __forceinline__ void operator()(int64_t (&at)[K], const bool (&)[K],
+                                             int64_t (&idv)[K]) const {
+#pragma unroll
+    for (int t = 0; t < K; ++t) idv[t] = static_cast<int64_t>(rows[at[t]]);
+  }
+};
+
+// FUSED: instead of perm and offsets for the bag kernel, the workgroup
+// reduces its segments itself (bag_group, G lanes per segment, 16-byte row
+// chunks, table below 2 GiB) into out[batch, dim].  Its list then holds row
+// ids (from step 1), so the rows are one round trip away.  A range with
+// more entries than the list holds ranks them into perm (row ids, in its
+// own slots) and reduces through it.
+template <int G, bool MEAN, bool FUSED>
+__global__ __launch_bounds__(kTlThreads) void seg_range_kernel(
+    const uint32_t* __restrict__ sorted_val, const uint16_t* __restrict__ sorted_seg,
+    const uint32_t* __restrict__ bstart, int nblk, int batch, int S, int sbits,
+    int64_t* __restrict__ offsets, int32_t* __restrict__ perm, const float* __restrict__ data,
+    int64_t rows, int64_t dim, float* __restrict__ out, int* __restrict__ status) {
+  __shared__ uint32_t src[kTlMaxBlocks];        // sorted index of the range's first entry in block a
+  __shared__ uint32_t excl[kTlMaxBlocks + 1];   // the range's entries in the blocks before a
+  __shared__ uint32_t list_pos[kTlCap];         // the range's positions (FUSED: row ids), in order
+  __shared__ uint8_t list_seg[kTlCap];          // ... and their segments less the range's first
+  __shared__ uint32_t lrow[FUSED ? kTlCap : 1]; // FUSED: row ids ranked by segment
+  __shared__ uint32_t sstart[kTlMaxS + 1];      // segment starts in the ranked list
+  __shared__ uint16_t bmap[kTlCap];             // block of each list entry (gather)
+  __shared__ uint32_t wcnt[kTlWaves][kTlMaxS];  // entries per wave slice and segment
+  __shared__ uint32_t wpref[kTlWaves][kTlMaxS]; // next perm slot per wave slice and segment
+  __shared__ uint32_t cursor[kTlMaxS];          // next perm slot per segment
+  __shared__ uint32_t wsum[kTlWaves], wbelow[kTlWaves];
+  __shared__ uint32_t total_s, base_all_s;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint64_t lt = (uint64_t(1) << lane) - 1;
+  const int g = blockIdx.x;
+  const uint32_t lo = static_cast<uint32_t>(g) * S;
+  const uint32_t ns = static_cast<uint32_t>(min(S, batch - static_cast<int>(lo)));
+
+  // 1. the range's slice of every block: thread tid takes blocks
+  //    [tid*per, tid*per + per); loads unconditional (block clamped)
+  const int per = (nblk + kTlThreads - 1) / kTlThreads;
+  uint32_t s0[kTlPer], cnt[kTlPer];
+#pragma unroll
+  for (int u = 0; u < kTlPer; ++u) {
+    if (u < per) {
+      const int a = min(tid * per + u, nblk - 1);
+      const uint32_t* bs = bstart + (int64_t)a * (kTlBuckets + 1) + g;
+      s0[u] = bs[0];
+      cnt[u] = bs[1];
+    }
+  }
+  uint32_t below = 0, mine = 0;
+#pragma unroll
+  for (int u = 0; u < kTlPer; ++u) {
+    if (u < per) {
+      const bool ok = tid * per + u < nblk;
+      cnt[u] = ok ? cnt[u] - s0[u] : 0u;
+      below += ok ? s0[u] : 0u;
+      mine += cnt[u];
+    }
+  }
+  // block scan of the per-thread entry counts; block sum of `below`
+  uint32_t inc = mine;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const uint32_t x = __shfl_up(inc, off, 64);
+    if (lane >= off) inc += x;
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) below += __shfl_xor(below, off, 64);
+  if (lane == 63) wsum[wave] = inc;
+  if (lane == 0) wbelow[wave] = below;
+  __syncthreads();
+  uint32_t run = inc - mine;
+  for (int w = 0; w < wave; ++w) run += wsum[w];
+#pragma unroll
+  for (int u = 0; u < kTlPer; ++u) {
+    if (u < per) {
+      const int a = tid * per + u;
+      if (a < nblk) {
+        src[a] = static_cast<uint32_t>(a) * kTlBlock + s0[u];
+        excl[a] = run;
+        run += cnt[u];
+      }
+    }
+  }
+  if (tid == kTlThreads - 1) {
+    excl[nblk] = run;  // the last thread's running sum is the total
+    total_s = run;
+    uint32_t b = 0;
+    for (int w = 0; w < kTlWaves; ++w) b += wbelow[w];
+    base_all_s = b;
+  }
+  __syncthreads();
+  const uint32_t total = total_s;
+
+  // entries [c0, c0 + len) into the list (from `vals`: positions or row
+  // ids): each thread marks its blocks' entries in bmap, then every thread
+  // takes four entries (balanced, however the entries fall on the blocks),
+  // all four loads in flight
+  auto gather = [&](const uint32_t* __restrict__ vals, uint32_t c0, uint32_t len) {
+#pragma unroll
+    for (int u = 0; u < kTlPer; ++u) {
+      if (u < per) {
+        const int a = tid * per + u;
+        if (a < nblk) {
+          const uint32_t e0 = excl[a];
+          const uint32_t hi_i = min(e0 + cnt[u], c0 + len);
+          for (uint32_t i = max(e0, c0); i < hi_i; ++i) bmap[i - c0] = static_cast<uint16_t>(a);
+        }
+      }
+    }
+    __syncthreads();
+    for (uint32_t i0 = 0; i0 < len; i0 += 4 * kTlThreads) {
+      uint32_t e[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint32_t i = min(i0 + q * kTlThreads + tid, len - 1);
+        const int a = bmap[i];
+        e[q] = src[a] + (c0 + i - excl[a]);
+      }
+      uint32_t p[4];
+      uint16_t sg[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        p[q] = vals[e[q]];
+        sg[q] = sorted_seg[e[q]];
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint32_t i = i0 + q * kTlThreads + tid;
+        if (i < len) {
+          list_pos[i] = p[q];
+          list_seg[i] = static_cast<uint8_t>(sg[q] - lo);
+        }
+      }
+    }
+  };
+  // lanes of this wave step holding the same segment
+  auto match = [&](uint32_t seg_local, bool valid) {
+    uint64_t same = __ballot(valid);
+#pragma unroll
+    for (int b = 0; b < kTlMaxSBits; ++b) {
+      if (b < sbits) {
+        const bool on = (seg_local >> b) & 1u;
+        const uint64_t bb = __ballot(on);
+        same &= on ? bb : ~bb;
+      }
+    }
+    return same;
+  };
+  auto slice = [&](uint32_t len, uint32_t* beg, uint32_t* end) {
+    const uint32_t per_w = (len + kTlWaves - 1) / kTlWaves;
+    *beg = wave * per_w;
+    *end = min(len, *beg + per_w);
+  };
+  // wcnt[wave][s] += entries of segment s in this wave's slice of the list
+  auto count_pass = [&](uint32_t len) {
+    uint32_t beg, end;
+    slice(len, &beg, &end);
+    for (uint32_t k0 = beg; k0 < end; k0 += 64) {
+      const uint32_t k = k0 + lane;
+      const bool valid = k < end;
+      const uint32_t s = valid ? list_seg[k] : 0u;
+      const uint64_t same = match(s, valid);
+      const uint32_t c = static_cast<uint32_t>(__popcll(same));
+      if (valid && static_cast<uint32_t>(__popcll(same & lt)) + 1 == c) wcnt[wave][s] += c;
+    }
+  };
+  // wpref[w][s] = cursor[s] + the entries of s in the slices before w;
+  // returns the cursor after this list (for the last slice's threads)
+  auto prefix_pass = [&]() {
+    uint32_t r = 0;
+    if (static_cast<uint32_t>(lane) < ns) {
+      r = cursor[lane];
+      for (int q = 0; q < wave; ++q) r += wcnt[q][lane];
+      wpref[wave][lane] = r;
+      r += wcnt[wave][lane];
+    }
+    return r;
+  };
+  // to_lds: the list's row ids into lrow (slots less the range's start);
+  // else its values (positions, or FUSED: row ids) into perm
+  auto write_pass = [&](uint32_t len, bool to_lds) {
+    uint32_t beg, end;
+    slice(len, &beg, &end);
+    const uint32_t base_all = base_all_s;
+    for (uint32_t k0 = beg; k0 < end; k0 += 64) {
+      const uint32_t k = k0 + lane;
+      const bool valid = k < end;
+      const uint32_t s = valid ? list_seg[k] : 0u;
+      const uint64_t same = match(s, valid);
+      if (valid) {
+        const uint32_t rank = static_cast<uint32_t>(__popcll(same & lt));
+        const uint32_t c = static_cast<uint32_t>(__popcll(same));
+        const uint32_t slot = wpref[wave][s] + rank;
+        if (FUSED && to_lds)
+          lrow[slot - base_all] = list_pos[k];
+        else
+          perm[slot] = static_cast<int32_t>(list_pos[k]);
+        if (rank + 1 == c) wpref[wave][s] += c;
+      }
+    }
+  };
+  // segment counts (summed over the wave slices) -> offsets and cursors
+  auto seg_offsets = [&]() {
+    uint32_t c = 0;
+    if (static_cast<uint32_t>(lane) < ns)
+      for (int q = 0; q < kTlWaves; ++q) c += wcnt[q][lane];
+    uint32_t sc = c;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const uint32_t x = __shfl_up(sc, off, 64);
+      if (lane >= off) sc += x;
+    }
+    const uint32_t base_all = base_all_s;
+    const uint32_t start = base_all + sc - c;
+    if (static_cast<uint32_t>(lane) < ns) {
+      cursor[lane] = start;
+      sstart[lane] = sc - c;
+      if (!FUSED) offsets[lo + lane] = start;
+    }
+    if (lane == 63) {
+      sstart[ns] = sc;
+      if (!FUSED && lo + ns == static_cast<uint32_t>(batch)) offsets[batch] = base_all + sc;
+    }
+  };
+  // FUSED: every segment of the range, G lanes each, from row ids fetched
+  // by `ids` at list indices base + sstart[s] .. base + sstart[s + 1]
+  auto reduce = [&](auto ids, uint32_t base) {
+    if constexpr (FUSED) {
+      constexpr int kGroups = kTlThreads / G;
+      bool bad = false;
+      for (uint32_t s = tid / G; s < ns; s += kGroups)
+        bad |= bag_group<G, 4, MEAN, true>(data, rows, dim, base + sstart[s], base + sstart[s + 1],
+                                           ids, out + static_cast<int64_t>(lo + s) * dim);
+      if (bad) atomicOr(status, 1);
+    }
+  };
+  uint32_t* wflat = &wcnt[0][0];
+
+  if (total <= static_cast<uint32_t>(kTlCap)) {
+    // the usual case: one list; its count pass also gives the segment sizes
+    wflat[tid] = 0;
+    gather(sorted_val, 0, total);
+    __syncthreads();
+    count_pass(total);
+    __syncthreads();
+    if (wave == 0) seg_offsets();
+    __syncthreads();
+    prefix_pass();
+    __syncthreads();
+    write_pass(total, true);
+    if constexpr (FUSED) {
+      __syncthreads();
+      reduce(LdsIds{lrow}, 0u);
+    }
+    return;
+  }
+  // more entries than the list holds: chunks in order; a counting sweep
+  // gives the segment sizes, a writing sweep carries the cursors
+  wflat[tid] = 0;
+  for (int sweep = 0; sweep < 2; ++sweep) {
+    if (sweep == 1) {
+      __syncthreads();
+      if (wave == 0) seg_offsets();
+    }
+    for (uint32_t c0 = 0; c0 < total; c0 += kTlCap) {
+      const uint32_t len = min(total - c0, static_cast<uint32_t>(kTlCap));
+      __syncthreads();  // the previous chunk's readers of the list and wcnt are done
+      if (sweep == 1) wflat[tid] = 0;
+      gather(sorted_val, c0, len);
+      __syncthreads();
+      count_pass(len);
+      if (sweep == 1) {
+        __syncthreads();
+        const uint32_t next = prefix_pass();
+        __syncthreads();
+        if (wave == kTlWaves - 1 && static_cast<uint32_t>(lane) < ns) cursor[lane] = next;
+        write_pass(len, false);
+      }
+    }
+  }
+  if constexpr (FUSED) {
+    // this workgroup's perm entries are read back by other lanes of it
+    __threadfence();
+    __syncthreads();
+    reduce(GlobalRows{perm}, base_all_s);
   }
 }
 
@@ -789,6 +1246,16 @@ int segment_reduce_plan(int64_t n, int64_t batch, int sorted_hint, hipStream_t s
     plan->bytes = off_bytes;
     return ANNC_OK;
   }
+  const int64_t tblk = std::max<int64_t>(1, ceil_div(n, kTlBlock));
+  if (batch <= kCsMaxSegments && tblk <= kTlMaxBlocks) {
+    plan->path = SegPlan::kTwoLevel;
+    const size_t m = (size_t)(tblk * kTlBlock);
+    // sorted positions (or row ids), segments, bucket starts, offsets, perm
+    plan->bytes = align256(sizeof(uint32_t) * m) + align256(sizeof(uint16_t) * m) +
+                  align256(sizeof(uint32_t) * (size_t)(tblk * (kTlBuckets + 1))) + off_bytes +
+                  align256(sizeof(int32_t) * (size_t)std::max<int64_t>(n, 1));
+    return ANNC_OK;
+  }
   const int64_t nblk = ceil_div(n, kCsBlock);
   if (batch <= kCsMaxSegments && nblk * batch <= (int64_t(1) << 24)) {
     plan->path = SegPlan::kCounting;
@@ -839,6 +1306,74 @@ int segment_reduce_run(hipStream_t s, const float* data, int64_t rows, int64_t d
     a.offsets = offsets;
     a.perm = nullptr;
     return launch_bag(a, s);
+  }
+
+  if (plan.path == SegPlan::kTwoLevel) {
+    // block sort by segment range, then one workgroup per range, which
+    // reduces its segments itself (fused) or writes perm for the bag kernel
+    const int64_t tblk = std::max<int64_t>(1, ceil_div(n, kTlBlock));
+    const size_t m = (size_t)(tblk * kTlBlock);
+    uint32_t* sorted_pos = reinterpret_cast<uint32_t*>(ws);
+    ws += align256(sizeof(uint32_t) * m);
+    uint16_t* sorted_seg = reinterpret_cast<uint16_t*>(ws);
+    ws += align256(sizeof(uint16_t) * m);
+    uint32_t* bstart = reinterpret_cast<uint32_t*>(ws);
+    ws += align256(sizeof(uint32_t) * (size_t)(tblk * (kTlBuckets + 1)));
+    int64_t* offsets = reinterpret_cast<int64_t*>(ws);
+    int32_t* perm = reinterpret_cast<int32_t*>(ws + off_bytes);
+    // S segments per range: at most kTlBuckets ranges, S <= kTlMaxS
+    const int S = static_cast<int>(std::max<int64_t>(1, ceil_div(batch, kTlBuckets)));
+    int sbits = 0;
+    while ((1 << sbits) < S) ++sbits;
+    const int nb = n > 0 ? static_cast<int>(tblk) : 0;
+    const dim3 rgrid((unsigned)ceil_div(batch, S));
+    // fused: 16-byte row chunks and a table below 2 GiB (buffer loads)
+    auto aligned16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+    const bool fuse = n > 0 && dim % 4 == 0 && aligned16(data) && aligned16(out) &&
+                      rows * dim * static_cast<int64_t>(sizeof(float)) < (int64_t(1) << 31);
+    if (!fuse) {
+      if (n > 0) {
+        hipLaunchKernelGGL((seg_block_sort_kernel<int64_t, false>), dim3((unsigned)tblk),
+                           dim3(kTlThreads), 0, s, seg, stride, n, static_cast<int>(batch), S,
+                           static_cast<const int64_t*>(nullptr), rows, sorted_pos, sorted_seg,
+                           static_cast<uint32_t*>(nullptr), bstart);
+        ANNC_HIP_TRY(hipGetLastError());
+      }
+      hipLaunchKernelGGL((seg_range_kernel<4, false, false>), rgrid, dim3(kTlThreads), 0, s,
+                         sorted_pos, sorted_seg, bstart, nb, static_cast<int>(batch), S, sbits,
+                         offsets, perm, static_cast<const float*>(nullptr), rows, dim,
+                         static_cast<float*>(nullptr), status);
+      ANNC_HIP_TRY(hipGetLastError());
+      a.offsets = offsets;
+      a.perm = perm;
+      return launch_bag(a, s);
+    }
+    auto run_fused = [&](auto idx_tag) -> int {
+      using IdxT = decltype(idx_tag);
+      const IdxT* idx = static_cast<const IdxT*>(indices);
+      // sorted_pos holds the row ids (ROWS)
+      hipLaunchKernelGGL((seg_block_sort_kernel<IdxT, true>), dim3((unsigned)tblk),
+                         dim3(kTlThreads), 0, s, seg, stride, n, static_cast<int>(batch), S, idx,
+                         rows, static_cast<uint32_t*>(nullptr), sorted_seg, sorted_pos, bstart);
+      ANNC_HIP_TRY(hipGetLastError());
+      const int64_t lanes = dim / 4;
+      const bool mean = combiner == ANNC_COMBINER_MEAN;
+      auto go = [&](auto g_tag) -> int {
+        constexpr int G = decltype(g_tag)::value;
+        auto k = mean ? seg_range_kernel<G, true, true> : seg_range_kernel<G, false, true>;
+        hipLaunchKernelGGL(k, rgrid, dim3(kTlThreads), 0, s, sorted_pos, sorted_seg, bstart, nb,
+                           static_cast<int>(batch), S, sbits, offsets, perm, data, rows, dim, out,
+                           status);
+        ANNC_HIP_TRY(hipGetLastError());
+        return ANNC_OK;
+      };
+      if (lanes <= 4) return go(std::integral_constant<int, 4>{});
+      if (lanes <= 8) return go(std::integral_constant<int, 8>{});
+      if (lanes <= 16) return go(std::integral_constant<int, 16>{});
+      if (lanes <= 32) return go(std::integral_constant<int, 32>{});
+      return go(std::integral_constant<int, 64>{});
+    };
+    return indices_is_64 ? run_fused(int64_t{}) : run_fused(int32_t{});
   }
 
   if (plan.path == SegPlan::kCounting) {

@@ -40,7 +40,7 @@ int segment_reduce(hipStream_t s, const float* data, int64_t rows, int64_t dim,
 
 // The path a segment reduction takes and the device workspace it needs.
 struct SegPlan {
-  enum Path { kSorted, kCounting, kRadix } path = kSorted;
+  enum Path { kSorted, kTwoLevel, kCounting, kRadix } path = kSorted;
   size_t bytes = 0;       // workspace bytes
   size_t temp_bytes = 0;  // radix sort temporary storage (kRadix)
   int end_bit = 0;        // radix sort key bits (kRadix)

@@ -349,14 +349,18 @@ def make_case(name: str, device, inp: Inputs) -> Case:
         w = inp.get("config3")
         bags, dim = w.offsets.size - 1, w.table.shape[1]
         nnz = int(w.offsets[-1])
-        table, ids = t(w.table), t(w.ids)
-        seg = t(np.repeat(np.arange(bags, dtype=np.int64), np.diff(w.offsets)))
+        seg_np = np.repeat(np.arange(bags, dtype=np.int64), np.diff(w.offsets))
+        ids_np = w.ids
         srt = name.endswith("sorted")
+        if not srt:   # the positions in a random order (seeded): unsorted segment ids
+            order = workloads.rng(11).permutation(nnz)
+            seg_np, ids_np = seg_np[order], ids_np[order]
+        table, ids, seg = t(w.table), t(ids_np), t(seg_np)
         return Case(name, lambda i: dev.segment_reduce(table, ids, seg, bags, 1, sorted_ids=srt),
                     16 * nnz + 4 * dim * nnz + 4 * dim * bags, "hbm",
                     "configs[2] as KPFusedSparseSegmentReduce inputs (indices, segment ids), mean, "
-                    + ("ids promised sorted" if srt else
-                       "no order assumed (stable counting sort by segment)"),
+                    + ("segment ids sorted and promised so" if srt else
+                       "positions shuffled (seeded), no order assumed: stable sort by segment"),
                     f"segment_reduce_config3_{'sorted' if srt else 'any_order'}", launches=100)
     if name == "hash_bucket":
         h = inp.get("config4")

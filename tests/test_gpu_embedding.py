@@ -122,12 +122,18 @@ def test_tf_segment_reduce_empty_indices():
 SEG_ORDER_CASES = [
     ("reversed", 3000, 50000),
     ("one segment over 5 blocks of 1024 positions", 1, 5000),
-    ("largest counting-sort batch", 16384, 70000),
+    ("largest sort batch: 64 segments per filter workgroup", 16384, 70000),
     ("radix-sort batch", 16385, 70000),
     ("mostly empty segments", 10000, 100),
     ("ids outside [0, batch) dropped", 1000, 30000),
     ("ids outside [0, batch) dropped, radix sort", 20000, 30000),
     ("sorted", 4096, 81857),
+    ("two-level sort, 128 blocks", 4096, 131072),
+    ("two-level sort, last block partial", 4096, 131073),
+    ("counting sort: past the two-level sort's 4 Mi positions", 64, 4 * 2**20 + 1),
+    ("counting sort, ids outside [0, batch) dropped", 2000, 4 * 2**20 + 3000),
+    ("three segments: more entries per range than its list holds", 3, 100000),
+    ("skewed: every other position in one segment", 4096, 120000),
 ]
 
 
@@ -135,8 +141,9 @@ SEG_ORDER_CASES = [
 @pytest.mark.parametrize("combiner", [0, 1])
 def test_device_segment_reduce_orders(what, batch, n, combiner):
     """Every segment's rows are summed in position order whatever the order
-    of the segment ids (stable counting sort up to 16384 segments, radix
-    sort beyond): bit-exact against the sequential loop."""
+    of the segment ids (up to 16384 segments: the two-level sort up to 4 Mi
+    positions, the stable counting sort beyond; radix sort for more
+    segments): bit-exact against the sequential loop."""
     note(f"device segment reduce: {what} (batch {batch}, n {n}, combiner {combiner})")
     g = workloads.rng(batch + n)
     data = g.standard_normal((2000, 8)).astype(np.float32)
@@ -144,10 +151,12 @@ def test_device_segment_reduce_orders(what, batch, n, combiner):
     seg = g.integers(0, batch, size=n).astype(np.int64)
     if what.startswith("reversed"):
         seg = np.sort(seg)[::-1].copy()
+    elif what.startswith("skewed"):
+        seg[::2] = 17
     elif what.startswith("sorted"):
         seg.sort()
     keep = np.ones(n, bool)
-    if what.startswith("ids outside"):
+    if what.startswith("ids outside") or "dropped" in what:
         bad = g.choice(n, size=n // 10, replace=False)
         seg[bad] = g.choice([-1, -7, batch, batch + 5, 2**40], size=bad.size)
         keep[bad] = False
