@@ -370,6 +370,20 @@ def make_case(name: str, device, inp: Inputs) -> Case:
                     f"configs[3] ids ({h.ids.size}) -> decimal -> Fingerprint64 % 1e5, int64 in "
                     "and out (compute-bound: rate for reference only)", "hash_bucket_int64_config4",
                     ids=int(h.ids.size))
+    if name == "bag_stream":
+        # streaming-read reference: the bag kernel over a 1 GiB table whose
+        # rows are read once, in order (ids 0..R-1, bags of 128 positions)
+        rows_n, dim, per = 4 << 20, 64, 128
+        table = torch.zeros((rows_n, dim), dtype=torch.float32, device=device)
+        ids = torch.arange(rows_n, dtype=torch.int64, device=device)
+        offs = torch.arange(0, rows_n + 1, per, dtype=torch.int64, device=device)
+        bags = rows_n // per
+        out = torch.empty((bags, dim), dtype=torch.float32, device=device)
+        return Case(name, lambda i: dev.embedding_bag(table, ids, offs, 0, out=out),
+                    _bag_bytes(rows_n, bags, dim), "hbm",
+                    "bag kernel, sequential rows: table [4Mi x 64] (1 GiB) read once in order, "
+                    "bags of 128 ids (streaming-read reference)", "bag_kernel_stream_reference",
+                    launches=10)
     if name == "copy":
         src = torch.ones(64 << 20, dtype=torch.float32, device=device)
         dst = torch.empty_like(src)
@@ -382,7 +396,7 @@ def make_case(name: str, device, inp: Inputs) -> Case:
 CASES = ("tower", "widedeep", "gemm_l1", "gemm_l2", "gemm_l3", "gemm_small", "gemm_e2e_l1", "batch_matmul",
          "bag_sum", "bag_mean", "bag_sum_cold", "hashed", "hashed_cold", "hashed_nohash",
          "hashed_dim32", "sparse_embedding2", "pooling", "segment_reduce_sorted",
-         "segment_reduce_any", "hash_bucket", "copy")
+         "segment_reduce_any", "hash_bucket", "copy", "bag_stream")
 # the cases reported under `components` (gemm_l1 is the roofline, copy the calibration)
 COMPONENT_CASES = ("gemm_small", "gemm_l2", "gemm_l3", "gemm_e2e_l1", "batch_matmul",
                    "bag_sum", "bag_mean", "bag_sum_cold", "hashed", "hashed_cold",
