@@ -370,6 +370,16 @@ def make_case(name: str, device, inp: Inputs) -> Case:
                     f"configs[3] ids ({h.ids.size}) -> decimal -> Fingerprint64 % 1e5, int64 in "
                     "and out (compute-bound: rate for reference only)", "hash_bucket_int64_config4",
                     ids=int(h.ids.size))
+    if name == "torch_mm_l1":
+        # reference point: torch.mm (hipBLASLt) on layer 1's shape, row-major
+        # B, no bias or activation
+        w = inp.get("config2")
+        x, wt = t(w.x), t(w.weights[0])
+        out = torch.empty((x.shape[0], wt.shape[1]), dtype=torch.float32, device=device)
+        return Case(name, lambda i: torch.mm(x, wt, out=out),
+                    2.0 * x.shape[0] * wt.shape[0] * wt.shape[1], "mfma",
+                    "torch.mm (hipBLASLt) fp32 [4096x1024] . [1024x512], for reference",
+                    "hipblaslt_layer1_4096x512x1024")
     if name == "bag_stream":
         # streaming-read reference: the bag kernel over a 1 GiB table whose
         # rows are read once, in order (ids 0..R-1, bags of 128 positions)
@@ -396,7 +406,7 @@ def make_case(name: str, device, inp: Inputs) -> Case:
 CASES = ("tower", "widedeep", "gemm_l1", "gemm_l2", "gemm_l3", "gemm_small", "gemm_e2e_l1", "batch_matmul",
          "bag_sum", "bag_mean", "bag_sum_cold", "hashed", "hashed_cold", "hashed_nohash",
          "hashed_dim32", "sparse_embedding2", "pooling", "segment_reduce_sorted",
-         "segment_reduce_any", "hash_bucket", "copy", "bag_stream")
+         "segment_reduce_any", "hash_bucket", "copy", "bag_stream", "torch_mm_l1")
 # the cases reported under `components` (gemm_l1 is the roofline, copy the calibration)
 COMPONENT_CASES = ("gemm_small", "gemm_l2", "gemm_l3", "gemm_e2e_l1", "batch_matmul",
                    "bag_sum", "bag_mean", "bag_sum_cold", "hashed", "hashed_cold",
@@ -515,6 +525,52 @@ def bench_unique_gather(device, inp: Inputs):
                         "inverse index, gathered rows",
             "wall_us_median": round(statistics.median(ts) * 1e6, 1),
             "keys_per_s": round(nnz / statistics.median(ts), 1)}
+
+
+def bench_nonzero(device, inp: Inputs):
+    """KPFusedSparseSegmentReduceNonzero on configs[2] in TF form (positions
+    shuffled, segment ids in column 1 of slice_input), device tensors, mean:
+    median wall time of the two-phase op (phase 1 counts the nonzeros and
+    reads the count back; phase 2 runs the pipeline again and writes them),
+    and of phase 1 alone."""
+    import ctypes
+    import numpy as np
+    import torch
+    from annc_amd import _lib, tf_ops, workloads
+    w = inp.get("config3")
+    bags = w.offsets.size - 1
+    nnz = int(w.offsets[-1])
+    order = workloads.rng(11).permutation(nnz)
+    seg = np.repeat(np.arange(bags, dtype=np.int64), np.diff(w.offsets))[order]
+    slice_input = torch.from_numpy(np.stack([np.zeros(nnz, np.int64), seg], axis=1)).to(device)
+    data = torch.from_numpy(w.table).to(device)
+    idx = torch.from_numpy(w.ids[order].copy()).to(device)
+    begin = np.array([0, 1], np.int32)
+    for _ in range(3):
+        tf_ops.kp_fused_sparse_segment_reduce_nonzero(data, idx, slice_input, begin, 1)
+    ts = []
+    for _ in range(20):
+        t0 = time.perf_counter()
+        _, _, vals = tf_ops.kp_fused_sparse_segment_reduce_nonzero(data, idx, slice_input, begin, 1)
+        ts.append(time.perf_counter() - t0)
+    lib = _lib.lib()
+    ddims = np.asarray(data.shape, np.int64)
+    sdims = np.asarray(slice_input.shape, np.int64)
+    shape = np.zeros(2, np.int32)
+    cnt = np.zeros(1, np.int64)
+    args = (data.data_ptr(), 2, ddims.ctypes.data, idx.data_ptr(), 1, nnz, slice_input.data_ptr(),
+            2, sdims.ctypes.data, begin.ctypes.data, 2, 1, shape.ctypes.data, cnt.ctypes.data)
+    t1 = []
+    for _ in range(20):
+        t0 = time.perf_counter()
+        _lib.check(lib.annc_kp_fused_sparse_segment_reduce_nonzero(*args, None, None))
+        t1.append(time.perf_counter() - t0)
+    return {"workload": f"configs[2] as KPFusedSparseSegmentReduceNonzero inputs ({nnz} positions "
+                        f"shuffled, {bags} segments, dim 64, mean), device tensors; "
+                        f"{int(vals.numel())} nonzero values listed",
+            "two_phase_wall_us_median": round(statistics.median(ts) * 1e6, 1),
+            "phase1_wall_us_median": round(statistics.median(t1) * 1e6, 1),
+            "note": "each phase synchronises (count read-back); phase 2 reruns the reduction"}
 
 
 def bench_config5(device, inp: Inputs, steps: int):
@@ -746,6 +802,7 @@ def main() -> int:
             torch.cuda.empty_cache()
         components["matmul_add_relu_config1_custom_call"] = bench_config1_call(device, inp)
         components["unique_gather_config3"] = bench_unique_gather(device, inp)
+        components["segment_reduce_nonzero_config3"] = bench_nonzero(device, inp)
         components["wide_deep_e2e_config5"] = bench_config5(device, inp, steps=100)
         torch.cuda.empty_cache()
     cpu = None if args.no_cpu else cpu_baseline(inp)
