@@ -291,8 +291,13 @@ int launch_bag_idx(const BagArgs& a, hipStream_t s) {
 // ---------------------------------------------------------------------------
 // Segment-id preprocessing for unsorted segment reduction.
 // ---------------------------------------------------------------------------
-__global__ void seg_scan_kernel(const int64_t* __restrict__ seg, int64_t stride, int64_t n,
-                                long long* __restrict__ minmax, int* __restrict__ unsorted) {
+// Partial min, max and "some id is smaller than the one before it" of
+// seg[i*stride] over each block's grid-stride share, one record per block
+// (no atomics: the host combines the blocks' records).
+__global__ __launch_bounds__(kThreads) void seg_scan_kernel(const int64_t* __restrict__ seg,
+                                                           int64_t stride, int64_t n,
+                                                           long long* __restrict__ part) {
+  __shared__ long long red[3][kThreads / 64];
   long long lo = LLONG_MAX, hi = LLONG_MIN;
   int unsort = 0;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
@@ -309,17 +314,23 @@ __global__ void seg_scan_kernel(const int64_t* __restrict__ seg, int64_t stride,
     hi = h2 > hi ? h2 : hi;
     unsort |= __shfl_xor(unsort, off, 64);
   }
+  const int w = threadIdx.x >> 6;
   if ((threadIdx.x & 63) == 0) {
-    atomicMin(&minmax[0], lo);
-    atomicMax(&minmax[1], hi);
-    if (unsort) atomicOr(unsorted, 1);
+    red[0][w] = lo;
+    red[1][w] = hi;
+    red[2][w] = unsort;
   }
-}
-
-__global__ void init_scan_kernel(long long* minmax, int* unsorted) {
-  minmax[0] = LLONG_MAX;
-  minmax[1] = LLONG_MIN;
-  *unsorted = 0;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int q = 1; q < kThreads / 64; ++q) {
+      lo = red[0][q] < lo ? red[0][q] : lo;
+      hi = red[1][q] > hi ? red[1][q] : hi;
+      unsort |= static_cast<int>(red[2][q]);
+    }
+    part[3 * blockIdx.x] = lo;
+    part[3 * blockIdx.x + 1] = hi;
+    part[3 * blockIdx.x + 2] = unsort;
+  }
 }
 
 // offsets[s] = first position whose segment id is >= s, for s in [0, batch],
@@ -1212,23 +1223,27 @@ int launch_bag(const BagArgs& a, hipStream_t s) {
 
 int segment_scan(hipStream_t s, const int64_t* seg, int64_t stride, int64_t n, int64_t* min_out,
                  int64_t* max_out, bool* sorted) {
-  void* ws = stream_workspace(s, 64);
+  *min_out = LLONG_MAX;
+  *max_out = LLONG_MIN;
+  *sorted = true;
+  if (n <= 0) return ANNC_OK;
+  // up to 256 blocks of 4 waves; their records are combined here
+  constexpr int kMaxBlocks = 256;
+  const int blocks = (int)std::min<int64_t>(kMaxBlocks, ceil_div(n, 4 * kThreads));
+  void* ws = stream_workspace(s, sizeof(long long) * 3 * kMaxBlocks);
   if (!ws) return set_error(ANNC_RESOURCE_EXHAUSTED, "workspace allocation failed");
-  long long* minmax = static_cast<long long*>(ws);
-  int* unsorted = reinterpret_cast<int*>(minmax + 2);
-  hipLaunchKernelGGL(init_scan_kernel, dim3(1), dim3(1), 0, s, minmax, unsorted);
-  if (n > 0) {
-    const int blocks = (int)std::min<int64_t>(1024, ceil_div(n, kThreads));
-    hipLaunchKernelGGL(seg_scan_kernel, dim3(blocks), dim3(kThreads), 0, s, seg, stride, n,
-                       minmax, unsorted);
-  }
+  long long* part = static_cast<long long*>(ws);
+  hipLaunchKernelGGL(seg_scan_kernel, dim3(blocks), dim3(kThreads), 0, s, seg, stride, n, part);
   ANNC_HIP_TRY(hipGetLastError());
-  long long host[3];
-  ANNC_HIP_TRY(hipMemcpyAsync(host, ws, sizeof(long long) * 3, hipMemcpyDeviceToHost, s));
+  long long host[3 * kMaxBlocks];
+  ANNC_HIP_TRY(hipMemcpyAsync(host, part, sizeof(long long) * 3 * blocks, hipMemcpyDeviceToHost,
+                              s));
   ANNC_HIP_TRY(hipStreamSynchronize(s));
-  *min_out = host[0];
-  *max_out = host[1];
-  *sorted = reinterpret_cast<int*>(&host[2])[0] == 0;
+  for (int b = 0; b < blocks; ++b) {
+    *min_out = std::min<int64_t>(*min_out, host[3 * b]);
+    *max_out = std::max<int64_t>(*max_out, host[3 * b + 1]);
+    if (host[3 * b + 2]) *sorted = false;
+  }
   return ANNC_OK;
 }
 

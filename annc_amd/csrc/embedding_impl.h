@@ -54,6 +54,14 @@ int segment_reduce_run(hipStream_t s, const float* data, int64_t rows, int64_t d
                        int64_t n, int combiner, int64_t batch, float* out, const SegPlan& plan,
                        void* workspace, int* status);
 
+// Keys in first-occurrence order over a known small range (every key in
+// [kmin, kmin + range)): unique[r] = the r-th distinct key by first position,
+// indices[i] = the number of position i's key, *num_unique (device) = U.
+// A table of `range` ints replaces the hash of annc_hip_unique_gather.
+int first_occurrence_range(hipStream_t s, const int64_t* keys, int64_t stride, int64_t n,
+                           int64_t kmin, int64_t range, int64_t* num_unique, int64_t* unique,
+                           int32_t* indices);
+
 // dst[i] = src[i] for i < n (int32 -> int64).
 int widen_i32(hipStream_t s, const int32_t* src, int64_t n, int64_t* dst);
 

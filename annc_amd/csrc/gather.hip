@@ -25,6 +25,7 @@
 #include <climits>
 
 #include "common.h"
+#include "embedding_impl.h"
 
 namespace annc {
 namespace {
@@ -206,7 +207,84 @@ void launch_ug_gather(hipStream_t s, int g, const float* table, int64_t rows, in
   }
 }
 
+// ---------------------------------------------------------------------------
+// First occurrences over a small key range (keys in [kmin, kmin + range)):
+// first[key - kmin] is indexed directly instead of through the hash table.
+// ---------------------------------------------------------------------------
+__global__ void fo_fill_kernel(int32_t* __restrict__ first, int64_t range) {
+  const int64_t c = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (c < range) first[c] = INT_MAX;
+}
+
+// first[key - kmin] = smallest position of the key; a plain read that already
+// shows a smaller position skips the atomic (frequent keys cost one atomic
+// per few workgroups, not one per occurrence)
+__global__ void fo_min_kernel(const int64_t* __restrict__ keys, int64_t stride, int64_t n,
+                              int64_t kmin, int32_t* __restrict__ first) {
+  const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (i >= n) return;
+  int32_t* f = first + (keys[i * stride] - kmin);
+  if (__hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) > static_cast<int32_t>(i))
+    atomicMin(f, static_cast<int32_t>(i));
+}
+
+__global__ void fo_mark_kernel(const int64_t* __restrict__ keys, int64_t stride, int64_t n,
+                               int64_t kmin, const int32_t* __restrict__ first,
+                               int32_t* __restrict__ first_mark) {
+  const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (i >= n) return;
+  first_mark[i] = first[keys[i * stride] - kmin] == static_cast<int32_t>(i) ? 1 : 0;
+}
+
+// number[i] = inclusive count of first occurrences up to i
+__global__ void fo_output_kernel(const int64_t* __restrict__ keys, int64_t stride, int64_t n,
+                                 int64_t kmin, const int32_t* __restrict__ first,
+                                 const int32_t* __restrict__ number,
+                                 int32_t* __restrict__ indices, int64_t* __restrict__ unique,
+                                 int64_t* __restrict__ num_unique) {
+  const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (i >= n) return;
+  const int64_t key = keys[i * stride];
+  const int32_t f = first[key - kmin];
+  const int32_t r = number[f] - 1;
+  indices[i] = r;
+  if (f == static_cast<int32_t>(i)) unique[r] = key;
+  if (i == n - 1) num_unique[0] = number[n - 1];
+}
+
 }  // namespace
+
+int first_occurrence_range(hipStream_t s, const int64_t* keys, int64_t stride, int64_t n,
+                           int64_t kmin, int64_t range, int64_t* num_unique, int64_t* unique,
+                           int32_t* indices) {
+  ANNC_REQUIRE(n > 0 && n < INT_MAX && range >= 1, "bad first-occurrence size");
+  size_t scan = 0;
+  ANNC_HIP_TRY(hipcub::DeviceScan::InclusiveSum(nullptr, scan, (const int32_t*)nullptr,
+                                                (int32_t*)nullptr, (int)n, s));
+  auto align = [](size_t x) { return (x + 255) & ~size_t(255); };
+  const size_t fb = align(sizeof(int32_t) * (size_t)range);
+  const size_t n4 = align(sizeof(int32_t) * (size_t)n);
+  char* ws = static_cast<char*>(stream_workspace(s, fb + 2 * n4 + align(scan)));
+  if (!ws) return set_error(ANNC_RESOURCE_EXHAUSTED, "workspace allocation failed");
+  int32_t* first = reinterpret_cast<int32_t*>(ws);
+  int32_t* mark = reinterpret_cast<int32_t*>(ws + fb);
+  int32_t* number = reinterpret_cast<int32_t*>(ws + fb + n4);
+  void* tmp = ws + fb + 2 * n4;
+  const dim3 grid((unsigned)ceil_div(n, kThreads));
+  hipLaunchKernelGGL(fo_fill_kernel, dim3((unsigned)ceil_div(range, kThreads)), dim3(kThreads), 0,
+                     s, first, range);
+  ANNC_HIP_TRY(hipGetLastError());
+  hipLaunchKernelGGL(fo_min_kernel, grid, dim3(kThreads), 0, s, keys, stride, n, kmin, first);
+  ANNC_HIP_TRY(hipGetLastError());
+  hipLaunchKernelGGL(fo_mark_kernel, grid, dim3(kThreads), 0, s, keys, stride, n, kmin, first,
+                     mark);
+  ANNC_HIP_TRY(hipGetLastError());
+  ANNC_HIP_TRY(hipcub::DeviceScan::InclusiveSum(tmp, scan, mark, number, (int)n, s));
+  hipLaunchKernelGGL(fo_output_kernel, grid, dim3(kThreads), 0, s, keys, stride, n, kmin, first,
+                     number, indices, unique, num_unique);
+  ANNC_HIP_TRY(hipGetLastError());
+  return ANNC_OK;
+}
 
 int unique_gather(hipStream_t s, const float* table, int64_t rows, int64_t dim,
                   const int64_t* keys, int64_t stride, int64_t n, int64_t* num_unique,

@@ -4,6 +4,7 @@
 // function with the same inputs, attributes and OP_REQUIRES messages; the
 // arithmetic runs on the GPU kernels of embedding.hip / hash.hip.  Operand
 // pointers may be host or device memory; calls are synchronous.
+#include <algorithm>
 #include <cstring>
 #include <vector>
 
@@ -215,8 +216,16 @@ int annc_kp_fused_sparse_segment_reduce_nonzero(
   int64_t* d_slot64 = static_cast<int64_t*>(st.scratch(sizeof(int64_t) * num_indices));
   if (!d_nu || !d_uniq || !d_slot || !d_slot64)
     return set_error(ANNC_RESOURCE_EXHAUSTED, "scratch allocation failed");
-  rc = annc_hip_unique_gather(s, nullptr, 0, 0, d_slice + col, stride, num_indices, d_nu, d_uniq,
-                              d_slot, nullptr);
+  // segment ids spanning a small range (the scan gave min and max) index a
+  // table directly; others go through the hash table of KPFusedGather
+  const uint64_t range = static_cast<uint64_t>(seg_max) - static_cast<uint64_t>(seg_min) + 1;
+  if (range <= static_cast<uint64_t>(std::max<int64_t>(4 * num_indices, int64_t(1) << 16)) &&
+      range <= (uint64_t(1) << 26))
+    rc = first_occurrence_range(s, d_slice + col, stride, num_indices, seg_min,
+                                static_cast<int64_t>(range), d_nu, d_uniq, d_slot);
+  else
+    rc = annc_hip_unique_gather(s, nullptr, 0, 0, d_slice + col, stride, num_indices, d_nu,
+                                d_uniq, d_slot, nullptr);
   if (rc != ANNC_OK) return rc;
   int64_t nseg = 0;
   ANNC_HIP_TRY(hipMemcpyAsync(&nseg, d_nu, sizeof(int64_t), hipMemcpyDeviceToHost, s));
