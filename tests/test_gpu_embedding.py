@@ -297,20 +297,25 @@ def test_tf_segment_reduce_nonzero_random_bit_exact(one_d, combiner, idx64):
     np.testing.assert_array_equal(to_host(val), want[2])
 
 
-@pytest.mark.parametrize("case", ["normal", "negative_ids", "many_segments", "host_5000"])
+@pytest.mark.parametrize("case", ["normal", "negative_ids", "negative_small_range",
+                                  "many_segments", "host_5000"])
 def test_tf_segment_reduce_nonzero_order_sensitive(case):
     """Data from standard_normal, so the summation order shows in the bits:
     negative segment ids (INT64_MIN among them, listed as the reference's
     int32 cast lists them), more than 16384 first-appearance segments (the
     radix-sort path) and host-memory operands at 5000 positions; each equal
-    to the oracle bit for bit."""
+    to the oracle bit for bit.  Segment ids spanning a small range (negative
+    ones included) take the directly indexed first-occurrence table, the
+    others the hash table."""
     note(f"KPFusedSparseSegmentReduceNonzero order-sensitive {case}")
     g = workloads.rng({"normal": 31, "negative_ids": 32, "many_segments": 33,
-                       "host_5000": 34}[case])
+                       "host_5000": 34, "negative_small_range": 36}[case])
     n, rows, dim, nseg = 6000, 400, 9, 900
     if case == "many_segments":
         n, nseg = 40000, 20000
     seg = g.permutation(np.arange(n) % nseg).astype(np.int64)
+    if case == "negative_small_range":
+        seg = seg - nseg // 2
     if case == "negative_ids":
         seg = seg - nseg // 2
         seg[seg == -7] = np.iinfo(np.int64).min
