@@ -61,8 +61,11 @@ __device__ __forceinline__ typename VecT<VEC>::type load_row(const float* p) {
 }
 
 template <int VEC>
+// Output rows are written once and read only by later kernels: non-temporal
+// stores send them to memory without filling this XCD's L2, so the
+// end-of-kernel release has no dirty output lines to write back.
 __device__ __forceinline__ void store_row(float* p, typename VecT<VEC>::type v) {
-  *reinterpret_cast<typename VecT<VEC>::type*>(p) = v;
+  __builtin_nontemporal_store(v, reinterpret_cast<typename VecT<VEC>::type*>(p));
 }
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));

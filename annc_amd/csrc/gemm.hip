@@ -862,7 +862,10 @@ __global__ __launch_bounds__(64 * WM * WN * KS) void gemm_packed_pipe_kernel(Gem
           float v = acc[0][i][j][r];
           if (E) v += E[(int64_t)row * p.lde + col];
           if (p.bias) v += bias_v[j];
-          C[(int64_t)row * p.ldc + col] = apply_epilogue(v, p.epilogue);
+          // non-temporal: C goes to memory without filling this XCD's L2,
+          // so the end-of-kernel release has no dirty C lines to write back
+          __builtin_nontemporal_store(apply_epilogue(v, p.epilogue),
+                                      &C[(int64_t)row * p.ldc + col]);
         }
       }
     }

@@ -344,6 +344,10 @@ struct FieldSet {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 constexpr int kRawBufferFlags = 0x00020000;  // dword3 of a raw buffer descriptor (gfx950)
+// Cache policy of a buffer store (gfx950: bit 1 = nt).  Pooled output rows are
+// written once and read only by later kernels, so they go to memory without
+// filling L2 and the end-of-kernel release has no dirty lines to write back.
+constexpr int kNonTemporal = 2;
 constexpr uint32_t kMaskedOff = 0x80000000u;  // past the range check of any table < 2 GiB
 
 // Fused multi-field hash -> bucket -> gather -> pool, one run of consecutive
@@ -421,7 +425,7 @@ __global__ __launch_bounds__(kThreads) void hashed_bags_wave_kernel(
       const int32_t n = static_cast<int32_t>(end - beg);
       if (n > 0) acc *= 1.0f / static_cast<float>(n);
     }
-    if (active && bag_ok) *reinterpret_cast<f32x4*>(dst + c) = acc;
+    if (active && bag_ok) __builtin_nontemporal_store(acc, reinterpret_cast<f32x4*>(dst + c));
   }
 }
 
@@ -569,7 +573,7 @@ __global__ __launch_bounds__(kThreads) void hashed_bags_pipe_kernel(
     const uint32_t o = active && grp < nb ? static_cast<uint32_t>((grp * ldo + c) * sizeof(float))
                                           : kMaskedOff;
     __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc), orsrc,
-                                           static_cast<int>(o), 0, 0);
+                                           static_cast<int>(o), 0, kNonTemporal);
   };
 
   // A hashed run: row byte offsets of its positions, held by the lanes that
@@ -881,7 +885,8 @@ __global__ __launch_bounds__(kThreads) void hashed_bags_lds_kernel(
       if (n > 0) acc[r] *= 1.0f / static_cast<float>(n);
     }
     if (active && j < nbag)
-      *reinterpret_cast<f32x4*>(out + (b0 + j) * ldo + f * dim + c) = acc[r];
+      __builtin_nontemporal_store(acc[r],
+                                  reinterpret_cast<f32x4*>(out + (b0 + j) * ldo + f * dim + c));
   }
 }
 

@@ -335,10 +335,13 @@ def make_case(name: str, device, inp: Inputs) -> Case:
         table = t(w.table)
         gathered = torch.empty((bags * width, dim), dtype=torch.float32, device=device)
         wl = f"configs[2] ids padded to [{bags}, {width}] (-1 = masked), dim {dim}"
+        uniq = int(np.unique(w.ids).size)
         if name == "sparse_embedding2":
             return Case(name, lambda i: dev.sparse_embedding2(table, pad_d, 0, out=gathered),
                         8 * bags * width + 4 * dim * nnz + 4 * dim * bags * width, "hbm",
-                        wl + ": masked gather to [B*L, dim]", "sparse_embedding2_config3_padded")
+                        wl + ": masked gather to [B*L, dim]", "sparse_embedding2_config3_padded",
+                        nnz=nnz, unique_rows=uniq,
+                        unique_row_bytes=8 * bags * width + 4 * dim * uniq + 4 * dim * bags * width)
         dev.sparse_embedding2(table, pad_d, 0, out=gathered)
         g3 = gathered.view(bags, width, dim)
         # __pooling reads the gathered rows of positions with id > 0 only
@@ -428,6 +431,14 @@ def bench_case(c: Case, replays: int = 5) -> dict:
         res.update({k + "_rocprof": v for k, v in r.items()})
     if "traffic_bytes_per_launch" in prof:
         res["traffic_bytes"] = prof["traffic_bytes_per_launch"]
+        if c.bound == "hbm":
+            # the bytes HBM actually moved (FETCH_SIZE + WRITE_SIZE, calibrated)
+            # over this run's kernel time: with repeated (Zipf) rows served
+            # from L2 / MALL the algorithmic rate can pass the HBM peak, this
+            # one cannot
+            tg = prof["traffic_bytes_per_launch"] / (ms * 1e-3) / 1e9
+            res["traffic_GBps"] = round(tg, 1)
+            res["traffic_hbm_frac"] = round(tg / HBM_PEAK_GBS, 4)
     res.update(c.extra)
     log(f"{c.name}: {ms * 1e3:.2f} us, " + ", ".join(f"{k} {v}" for k, v in c.rate(ms).items()))
     return res
