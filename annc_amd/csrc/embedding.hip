@@ -111,6 +111,34 @@ __device__ __forceinline__ uint32_t group_bcast(uint32_t v) {
 }
 
 
+// x moved by the DPP control CTRL into the rows of ROW_MASK (lanes with no
+// source lane, and rows outside the mask, read 0).
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ uint32_t dpp_move(uint32_t x) {
+  return static_cast<uint32_t>(
+      __builtin_amdgcn_update_dpp(0, static_cast<int>(x), CTRL, ROW_MASK, 0xf, false));
+}
+
+// Inclusive sum over the lanes of a wave64 by DPP moves: rows of 16 by
+// row_shr 1, 2, 4 and 8, then lane 15's row total into rows 1 and 3
+// (row_bcast:15) and lane 31's into rows 2 and 3 (row_bcast:31).  Six VALU
+// moves instead of six LDS permutes; every add is unconditional, as a lane
+// with no source reads 0.
+__device__ __forceinline__ uint32_t wave_incl_sum(uint32_t v) {
+  v += dpp_move<0x111, 0xf>(v);
+  v += dpp_move<0x112, 0xf>(v);
+  v += dpp_move<0x114, 0xf>(v);
+  v += dpp_move<0x118, 0xf>(v);
+  v += dpp_move<0x142, 0xa>(v);
+  v += dpp_move<0x143, 0xc>(v);
+  return v;
+}
+
+// The value of lane 63 (scalar read).
+__device__ __forceinline__ uint32_t lane63(uint32_t v) {
+  return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 63));
+}
+
 // Row ids of bag positions from global memory: ids[at] or, through a
 // permutation, ids[perm[at]] (every slot loaded: the clamped positions are
 // valid; permuted positions first, then the ids they name, so each level is
@@ -573,59 +601,64 @@ static_assert(kCsMaxSegments <= int64_t(kTlBuckets) * kTlMaxS, "segment ranges")
 
 // ROWS: the row id of every sorted position (indices[p], or 0xffffffff for
 // an id outside [0, rows)) instead of the position, for the fused reduction
-// of step 2.
-template <typename IdxT, bool ROWS>
-__global__ __launch_bounds__(kTlThreads) void seg_block_sort_kernel(
+// of step 2.  THREADS x ITEMS positions per block, NB buckets (NB <= THREADS;
+// KEYBITS bits hold the keys 0..NB, NB marking a dropped position);
+// bstart[block][b] has NB + 1 entries per block.
+template <typename IdxT, bool ROWS, int THREADS, int ITEMS, int NB, int KEYBITS>
+__global__ __launch_bounds__(THREADS) void seg_block_sort_kernel(
     const int64_t* __restrict__ seg, int64_t stride, int64_t n, int batch, int S,
     const IdxT* __restrict__ indices, int64_t rows, uint32_t* __restrict__ sorted_pos,
     uint16_t* __restrict__ sorted_seg, uint32_t* __restrict__ sorted_row,
     uint32_t* __restrict__ bstart) {
-  // Positions are striped (item i of thread t is position b0 + i*256 + t),
+  static_assert(NB <= THREADS && (1 << KEYBITS) > NB, "bucket keys");
+  constexpr int kWaves = THREADS / 64;
+  constexpr int kBlock = THREADS * ITEMS;
+  // Positions are striped (item i of thread t is position b0 + i*THREADS + t),
   // so the wave steps (i, wave) taken in order visit positions in order.
-  // Each step ranks its lanes per bucket by a ballot match over the bucket
+  // Each step ranks its lanes per bucket by a ballot match over the key
   // bits; cnt[i][wave][b] holds the step's bucket counts.  An entry's slot
   // is then start[b] + (b's entries in the steps before) + its rank.
-  constexpr int kSteps = kTlItems * kTlWaves;
-  __shared__ uint16_t cnt[kSteps][kTlBuckets + 1];
-  __shared__ uint32_t start[kTlBuckets + 1];
-  __shared__ uint32_t wsum[kTlWaves];
+  constexpr int kSteps = ITEMS * kWaves;
+  __shared__ uint16_t cnt[kSteps][NB + 1];
+  __shared__ uint32_t start[NB + 1];
+  __shared__ uint32_t wsum[kWaves];
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const uint64_t lt = (uint64_t(1) << lane) - 1;
-  const int64_t b0 = (int64_t)blockIdx.x * kTlBlock;
+  const int64_t b0 = (int64_t)blockIdx.x * kBlock;
   // unconditional loads (position clamped to n - 1), so they travel together
-  int64_t v[kTlItems], iv[kTlItems];
+  int64_t v[ITEMS], iv[ITEMS];
 #pragma unroll
-  for (int i = 0; i < kTlItems; ++i) {
-    const int64_t p = b0 + i * kTlThreads + t;
+  for (int i = 0; i < ITEMS; ++i) {
+    const int64_t p = b0 + i * THREADS + t;
     v[i] = seg[(p < n ? p : n - 1) * stride];
     if constexpr (ROWS) iv[i] = static_cast<int64_t>(indices[p < n ? p : n - 1]);
   }
   uint16_t* cflat = &cnt[0][0];
-  for (int k = t; k < kSteps * (kTlBuckets + 1); k += kTlThreads) cflat[k] = 0;
-  uint32_t key[kTlItems], rank[kTlItems];
+  for (int k = t; k < kSteps * (NB + 1); k += THREADS) cflat[k] = 0;
+  uint32_t key[ITEMS], rank[ITEMS];
 #pragma unroll
-  for (int i = 0; i < kTlItems; ++i) {
-    const int64_t p = b0 + i * kTlThreads + t;
+  for (int i = 0; i < ITEMS; ++i) {
+    const int64_t p = b0 + i * THREADS + t;
     const bool ok = p < n && v[i] >= 0 && v[i] < batch;
-    key[i] = ok ? static_cast<uint32_t>(v[i]) / static_cast<uint32_t>(S) : kTlBuckets;
+    key[i] = ok ? static_cast<uint32_t>(v[i]) / static_cast<uint32_t>(S) : NB;
   }
   __syncthreads();
 #pragma unroll
-  for (int i = 0; i < kTlItems; ++i) {
+  for (int i = 0; i < ITEMS; ++i) {
     uint64_t same = ~uint64_t(0);
 #pragma unroll
-    for (int bit = 0; bit < kTlBucketBits; ++bit) {
+    for (int bit = 0; bit < KEYBITS; ++bit) {
       const bool on = (key[i] >> bit) & 1u;
       const uint64_t bb = __ballot(on);
       same &= on ? bb : ~bb;
     }
     rank[i] = static_cast<uint32_t>(__popcll(same & lt));
-    if (rank[i] == 0) cnt[i * kTlWaves + wave][key[i]] = static_cast<uint16_t>(__popcll(same));
+    if (rank[i] == 0) cnt[i * kWaves + wave][key[i]] = static_cast<uint16_t>(__popcll(same));
   }
   __syncthreads();
   // per bucket: counts before each step (in place), total, and the bucket
   // starts by a block scan of the totals (thread t: bucket t; the last
-  // thread also takes the dropped bucket kTlBuckets)
+  // thread also takes the dropped bucket NB)
   auto prefix_steps = [&](int b) {
     uint32_t c[kSteps];  // all loads first, so they travel together
 #pragma unroll
@@ -638,29 +671,25 @@ __global__ __launch_bounds__(kTlThreads) void seg_block_sort_kernel(
     }
     return run;
   };
-  const uint32_t tot = prefix_steps(t);
-  if (t == kTlThreads - 1) prefix_steps(kTlBuckets);
-  uint32_t inc = tot;
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const uint32_t x = __shfl_up(inc, off, 64);
-    if (lane >= off) inc += x;
-  }
+  const uint32_t tot = t < NB ? prefix_steps(t) : 0u;
+  if (t == THREADS - 1) prefix_steps(NB);
+  const uint32_t inc = wave_incl_sum(tot);
   if (lane == 63) wsum[wave] = inc;
   __syncthreads();
   uint32_t before = inc - tot;
-  for (int w = 0; w < wave; ++w) before += wsum[w];
-  start[t] = before;
-  if (t == kTlThreads - 1) start[kTlBuckets] = before + tot;  // first dropped entry
-  __syncthreads();
-  uint32_t* bs = bstart + (int64_t)blockIdx.x * (kTlBuckets + 1);
-  bs[t] = start[t];
-  if (t == kTlThreads - 1) bs[kTlBuckets] = start[kTlBuckets];
 #pragma unroll
-  for (int i = 0; i < kTlItems; ++i) {
-    const uint32_t slot = start[key[i]] + cnt[i * kTlWaves + wave][key[i]] + rank[i];
-    if constexpr (!ROWS) sorted_pos[b0 + slot] = static_cast<uint32_t>(b0 + i * kTlThreads + t);
-    sorted_seg[b0 + slot] = key[i] < kTlBuckets ? static_cast<uint16_t>(v[i]) : uint16_t(0);
+  for (int w = 0; w < kWaves; ++w) before += w < wave ? wsum[w] : 0u;  // loads in flight together
+  if (t < NB) start[t] = before;
+  if (t == THREADS - 1) start[NB] = before + tot;  // first dropped entry
+  __syncthreads();
+  uint32_t* bs = bstart + (int64_t)blockIdx.x * (NB + 1);
+  if (t < NB) bs[t] = start[t];
+  if (t == THREADS - 1) bs[NB] = start[NB];
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i) {
+    const uint32_t slot = start[key[i]] + cnt[i * kWaves + wave][key[i]] + rank[i];
+    if constexpr (!ROWS) sorted_pos[b0 + slot] = static_cast<uint32_t>(b0 + i * THREADS + t);
+    sorted_seg[b0 + slot] = key[i] < NB ? static_cast<uint16_t>(v[i]) : uint16_t(0);
     if constexpr (ROWS)
       sorted_row[b0 + slot] = static_cast<uint64_t>(iv[i]) < static_cast<uint64_t>(rows)
                                   ? static_cast<uint32_t>(iv[i]) : 0xffffffffu;
@@ -974,6 +1003,274 @@ __global__ __launch_bounds__(kTlThreads) void seg_range_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// Fused second step with one wave per segment range (the usual path of the
+// two-level sort when the rows are reduced in place; blocks of 1024
+// positions sorted into NB ranges by seg_block_sort_kernel<.., 1024, 1, NB>).
+// A single wave has no cross-wave barriers, and its stable ranking keeps the
+// per-segment counters in registers: lane s holds segment s's counter, and
+// every wave step of 64 list entries builds, from log2(S) ballots, both the
+// mask of each entry's segment (its rank: the entries of that segment in
+// lower lanes) and the mask of segment `lane` (the counter update).
+//   1. slices: lane l takes blocks [l*per, l*per + per); a wave scan of the
+//      slice lengths gives each block's place in the range's list.
+//   2. gather: the list (row ids and segments, position order) into LDS,
+//      balanced over the lanes however the entries fall on the blocks.
+//   3. count pass, exclusive scan over the segment lanes (segment starts),
+//      write pass: row ids ranked by segment.
+//   4. reduction: G lanes per segment (bag_group), rows in ranked order.
+// A range with more than kRwCap entries is ranked chunk by chunk (a count
+// sweep, then a write sweep carrying the counters) into perm, from which it
+// is reduced.
+// ---------------------------------------------------------------------------
+constexpr int kRwBuckets = 1024;                // segment ranges (one wave each)
+constexpr int kRwKeyBits = 11;                  // keys 0..kRwBuckets
+constexpr int kRwBlock = 1024;                  // positions per block (1024 threads x 1)
+constexpr int kRwMaxBlocks = 1024;              // up to 1 Mi positions
+constexpr int kRwPer = kRwMaxBlocks / 64;       // blocks per lane
+constexpr int kRwCap = 2048;                    // the list (LDS)
+constexpr int kRwMaxS = 64;                     // segments per range (one per lane)
+constexpr int kRwMaxSBits = 6;
+static_assert(kRwBlock == kTlBlock, "both steps share the block layout of the sorted arrays");
+static_assert(kCsMaxSegments <= int64_t(kRwBuckets) * kRwMaxS, "segment ranges");
+
+// Workgroup b's range when consecutive workgroups go to the 8 XCDs in turn:
+// each XCD takes a run of consecutive ranges, whose slices of every block
+// are adjacent in memory.
+__device__ __forceinline__ int xcd_run(int b, int n) {
+  const int per = n / 8, rem = n % 8, x = b % 8, k = b / 8;
+  return (x < rem ? x * (per + 1) : rem * (per + 1) + (x - rem) * per) + k;
+}
+
+template <int G, bool MEAN, int NB>
+__global__ __launch_bounds__(64) void seg_range_wave_kernel(
+    const uint32_t* __restrict__ sorted_row, const uint16_t* __restrict__ sorted_seg,
+    const uint32_t* __restrict__ bstart, int nblk, int batch, int S, int sbits,
+    int32_t* __restrict__ perm, const float* __restrict__ data, int64_t rows, int64_t dim,
+    float* __restrict__ out, int* __restrict__ status) {
+  __shared__ uint32_t src[kRwMaxBlocks];       // sorted index of the range's first entry in block a
+  __shared__ uint32_t excl[kRwMaxBlocks + 1];  // the range's entries in the blocks before a
+  __shared__ uint32_t list_row[kRwCap];        // the range's row ids, in position order
+  __shared__ uint8_t list_seg[kRwCap];         // ... and their segments less the range's first
+  __shared__ uint16_t bmap[kRwCap];            // block of each list entry (gather)
+  __shared__ uint32_t lrow[kRwCap];            // row ids ranked by segment
+  __shared__ uint32_t sstart[kRwMaxS + 1];     // segment starts in the ranked list
+
+  const int lane = threadIdx.x;
+  const uint64_t lt = (uint64_t(1) << lane) - 1;
+  const int g = xcd_run(blockIdx.x, gridDim.x);
+  const uint32_t lo = static_cast<uint32_t>(g) * S;
+  const uint32_t ns = static_cast<uint32_t>(min(S, batch - static_cast<int>(lo)));
+
+  // 1. slices (loads unconditional: block clamped)
+  const int per = (nblk + 63) / 64;
+  uint32_t s0[kRwPer], cnt[kRwPer];
+#pragma unroll
+  for (int u = 0; u < kRwPer; ++u) {
+    if (u < per) {
+      const int a = min(lane * per + u, nblk - 1);
+      const uint32_t* bs = bstart + (int64_t)a * (NB + 1) + g;
+      s0[u] = bs[0];
+      cnt[u] = bs[1];
+    }
+  }
+  uint32_t below = 0, mine = 0;
+#pragma unroll
+  for (int u = 0; u < kRwPer; ++u) {
+    if (u < per) {
+      const bool ok = lane * per + u < nblk;
+      cnt[u] = ok ? cnt[u] - s0[u] : 0u;
+      below += ok ? s0[u] : 0u;
+      mine += cnt[u];
+    }
+  }
+  const uint32_t inc = wave_incl_sum(mine);
+  const uint32_t total = lane63(inc);
+  const uint32_t base_all = lane63(wave_incl_sum(below));  // this range's first slot in perm
+  const uint32_t first = inc - mine;  // this lane's first list entry
+  uint32_t run = first;
+#pragma unroll
+  for (int u = 0; u < kRwPer; ++u) {
+    if (u < per) {
+      const int a = lane * per + u;
+      if (a < nblk) {
+        src[a] = static_cast<uint32_t>(a) * kRwBlock + s0[u];
+        excl[a] = run;
+        run += cnt[u];
+      }
+    }
+  }
+  __syncthreads();
+
+  // 2. list entries [c0, c0 + len) into LDS (row ids and local segments)
+  auto gather = [&](uint32_t c0, uint32_t len) {
+#pragma unroll
+    for (int u = 0; u < kRwPer; ++u) {
+      if (u < per) {
+        const int a = lane * per + u;
+        if (a < nblk) {
+          const uint32_t e0 = excl[a];
+          const uint32_t hi_i = min(e0 + cnt[u], c0 + len);
+          for (uint32_t i = max(e0, c0); i < hi_i; ++i) bmap[i - c0] = static_cast<uint16_t>(a);
+        }
+      }
+    }
+    __syncthreads();
+    for (uint32_t i0 = 0; i0 < len; i0 += 4 * 64) {
+      uint32_t e[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint32_t i = min(i0 + q * 64 + lane, len - 1);
+        const int a = bmap[i];
+        e[q] = src[a] + (c0 + i - excl[a]);
+      }
+      uint32_t r[4];
+      uint16_t sg[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        r[q] = sorted_row[e[q]];
+        sg[q] = sorted_seg[e[q]];
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint32_t i = i0 + q * 64 + lane;
+        if (i < len) {
+          list_row[i] = r[q];
+          list_seg[i] = static_cast<uint8_t>(sg[q] - lo);
+        }
+      }
+    }
+    __syncthreads();
+  };
+  // the step's ballots of the segment bits: masks of segment `s` among the
+  // valid entries
+  struct Step {
+    uint64_t valid, bit[kRwMaxSBits];
+  };
+  auto step_ballots = [&](uint32_t s, bool valid) {
+    Step st;
+    st.valid = __ballot(valid);
+#pragma unroll
+    for (int b = 0; b < kRwMaxSBits; ++b)
+      st.bit[b] = b < sbits ? __ballot(valid && ((s >> b) & 1u)) : 0;
+    return st;
+  };
+  auto seg_mask = [&](const Step& st, uint32_t s) {
+    uint64_t m = st.valid;
+#pragma unroll
+    for (int b = 0; b < kRwMaxSBits; ++b)
+      if (b < sbits) m &= ((s >> b) & 1u) ? st.bit[b] : ~st.bit[b];
+    return m;
+  };
+  // 3a. lane s += the entries of segment s among list entries [0, len)
+  auto count_pass = [&](uint32_t len, uint32_t* c_s) {
+    for (uint32_t k0 = 0; k0 < len; k0 += 64) {
+      const uint32_t k = k0 + lane;
+      const bool valid = k < len;
+      const Step st = step_ballots(valid ? list_seg[k] : 0u, valid);
+      *c_s += static_cast<uint32_t>(__popcll(seg_mask(st, static_cast<uint32_t>(lane))));
+    }
+  };
+  // 3c. each entry to its segment's cursor (lane s holds segment s's) plus
+  // its rank; to_lds: into lrow (slots relative to the range), else perm
+  auto write_pass = [&](uint32_t len, uint32_t* cur_s, bool to_lds) {
+    for (uint32_t k0 = 0; k0 < len; k0 += 64) {
+      const uint32_t k = k0 + lane;
+      const bool valid = k < len;
+      const uint32_t s = valid ? list_seg[k] : 0u;
+      const Step st = step_ballots(s, valid);
+      const uint32_t rank = static_cast<uint32_t>(__popcll(seg_mask(st, s) & lt));
+      const uint32_t base = static_cast<uint32_t>(__shfl(static_cast<int>(*cur_s), static_cast<int>(s), 64));
+      if (valid) {
+        if (to_lds)
+          lrow[base + rank] = list_row[k];
+        else
+          perm[base + rank] = static_cast<int32_t>(list_row[k]);
+      }
+      *cur_s += static_cast<uint32_t>(__popcll(seg_mask(st, static_cast<uint32_t>(lane))));
+    }
+  };
+  // 3b. segment starts (relative to the range) from the counts of lanes < ns
+  // (a lane at or past ns matched the segment its low sbits bits name)
+  auto seg_starts = [&](uint32_t c_s) {
+    if (static_cast<uint32_t>(lane) >= ns) c_s = 0;
+    const uint32_t sc = wave_incl_sum(c_s);
+    if (static_cast<uint32_t>(lane) < ns) sstart[lane] = sc - c_s;
+    if (lane == 63) sstart[ns] = sc;
+    return sc - c_s;
+  };
+  // 4. G lanes per segment; `ids` gives row ids at list index base + j
+  auto reduce = [&](auto ids, uint32_t base) {
+    constexpr int kGroups = 64 / G;
+    bool bad = false;
+    for (uint32_t s = lane / G; s < ns; s += kGroups)
+      bad |= bag_group<G, 4, MEAN, true>(data, rows, dim, base + sstart[s], base + sstart[s + 1],
+                                         ids, out + static_cast<int64_t>(lo + s) * dim);
+    if (bad) atomicOr(status, 1);
+  };
+
+  // the common case: at most two blocks and four entries per lane; each
+  // lane copies its own entries (no block map)
+  auto gather_direct = [&]() {
+    const uint32_t c0 = cnt[0];
+    const uint32_t src0 = static_cast<uint32_t>(min(lane * per, nblk - 1)) * kRwBlock + s0[0];
+    const uint32_t src1 = per > 1 ? static_cast<uint32_t>(min(lane * per + 1, nblk - 1)) * kRwBlock + s0[1]
+                                  : src0;
+    uint32_t e[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t jj = static_cast<uint32_t>(j) < mine ? static_cast<uint32_t>(j) : 0u;
+      e[j] = jj < c0 ? src0 + jj : src1 + (jj - c0);
+    }
+    uint32_t r[4];
+    uint16_t sg[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      r[j] = sorted_row[e[j]];
+      sg[j] = sorted_seg[e[j]];
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (static_cast<uint32_t>(j) < mine) {
+        list_row[first + j] = r[j];
+        list_seg[first + j] = static_cast<uint8_t>(sg[j] - lo);
+      }
+    }
+    __syncthreads();
+  };
+
+  uint32_t c_s = 0;
+  if (total <= static_cast<uint32_t>(kRwCap)) {
+    if (per <= 2 && __ballot(mine > 4) == 0)
+      gather_direct();
+    else
+      gather(0, total);
+    count_pass(total, &c_s);
+    uint32_t cur_s = seg_starts(c_s);
+    write_pass(total, &cur_s, true);
+    __syncthreads();
+    reduce(LdsIds{lrow}, 0u);
+    return;
+  }
+  for (uint32_t c0 = 0; c0 < total; c0 += kRwCap) {
+    const uint32_t len = min(total - c0, static_cast<uint32_t>(kRwCap));
+    gather(c0, len);
+    count_pass(len, &c_s);
+    __syncthreads();  // the list is read again by the next chunk's gather
+  }
+  uint32_t cur_s = base_all + seg_starts(c_s);
+  for (uint32_t c0 = 0; c0 < total; c0 += kRwCap) {
+    const uint32_t len = min(total - c0, static_cast<uint32_t>(kRwCap));
+    gather(c0, len);
+    write_pass(len, &cur_s, false);
+    __syncthreads();
+  }
+  // this wave's perm entries are read back by its other lanes
+  __threadfence();
+  __syncthreads();
+  reduce(GlobalRows{perm}, base_all);
+}
+
 // Sort keys: the segment id, or `batch` for ids outside [0, batch), which
 // then sort after every kept position.
 __global__ void make_keys_kernel(const int64_t* __restrict__ seg, int64_t stride, int64_t n,
@@ -1268,9 +1565,12 @@ int segment_reduce_plan(int64_t n, int64_t batch, int sorted_hint, hipStream_t s
   if (batch <= kCsMaxSegments && tblk <= kTlMaxBlocks) {
     plan->path = SegPlan::kTwoLevel;
     const size_t m = (size_t)(tblk * kTlBlock);
-    // sorted positions (or row ids), segments, bucket starts, offsets, perm
+    // sorted positions (or row ids), segments, bucket starts (kRwBuckets
+    // ranges for the one-wave step, which takes up to kRwMaxBlocks blocks),
+    // offsets, perm
+    const int64_t nb = tblk <= kRwMaxBlocks ? kRwBuckets : kTlBuckets;
     plan->bytes = align256(sizeof(uint32_t) * m) + align256(sizeof(uint16_t) * m) +
-                  align256(sizeof(uint32_t) * (size_t)(tblk * (kTlBuckets + 1))) + off_bytes +
+                  align256(sizeof(uint32_t) * (size_t)(tblk * (nb + 1))) + off_bytes +
                   align256(sizeof(int32_t) * (size_t)std::max<int64_t>(n, 1));
     return ANNC_OK;
   }
@@ -1336,7 +1636,8 @@ int segment_reduce_run(hipStream_t s, const float* data, int64_t rows, int64_t d
     uint16_t* sorted_seg = reinterpret_cast<uint16_t*>(ws);
     ws += align256(sizeof(uint16_t) * m);
     uint32_t* bstart = reinterpret_cast<uint32_t*>(ws);
-    ws += align256(sizeof(uint32_t) * (size_t)(tblk * (kTlBuckets + 1)));
+    const int64_t nb_alloc = tblk <= kRwMaxBlocks ? kRwBuckets : kTlBuckets;
+    ws += align256(sizeof(uint32_t) * (size_t)(tblk * (nb_alloc + 1)));
     int64_t* offsets = reinterpret_cast<int64_t*>(ws);
     int32_t* perm = reinterpret_cast<int32_t*>(ws + off_bytes);
     // S segments per range: at most kTlBuckets ranges, S <= kTlMaxS
@@ -1351,7 +1652,8 @@ int segment_reduce_run(hipStream_t s, const float* data, int64_t rows, int64_t d
                       rows * dim * static_cast<int64_t>(sizeof(float)) < (int64_t(1) << 31);
     if (!fuse) {
       if (n > 0) {
-        hipLaunchKernelGGL((seg_block_sort_kernel<int64_t, false>), dim3((unsigned)tblk),
+        hipLaunchKernelGGL((seg_block_sort_kernel<int64_t, false, kTlThreads, kTlItems, kTlBuckets,
+                                                kTlBucketBits>), dim3((unsigned)tblk),
                            dim3(kTlThreads), 0, s, seg, stride, n, static_cast<int>(batch), S,
                            static_cast<const int64_t*>(nullptr), rows, sorted_pos, sorted_seg,
                            static_cast<uint32_t*>(nullptr), bstart);
@@ -1366,22 +1668,43 @@ int segment_reduce_run(hipStream_t s, const float* data, int64_t rows, int64_t d
       a.perm = perm;
       return launch_bag(a, s);
     }
+    // one wave per range (kRwBuckets ranges) up to kRwMaxBlocks blocks
+    const bool wave = tblk <= kRwMaxBlocks;
+    const int Sw = static_cast<int>(std::max<int64_t>(1, ceil_div(batch, kRwBuckets)));
+    int sbits_w = 0;
+    while ((1 << sbits_w) < Sw) ++sbits_w;
     auto run_fused = [&](auto idx_tag) -> int {
       using IdxT = decltype(idx_tag);
       const IdxT* idx = static_cast<const IdxT*>(indices);
       // sorted_pos holds the row ids (ROWS)
-      hipLaunchKernelGGL((seg_block_sort_kernel<IdxT, true>), dim3((unsigned)tblk),
-                         dim3(kTlThreads), 0, s, seg, stride, n, static_cast<int>(batch), S, idx,
-                         rows, static_cast<uint32_t*>(nullptr), sorted_seg, sorted_pos, bstart);
+      if (wave)
+        hipLaunchKernelGGL((seg_block_sort_kernel<IdxT, true, kRwBlock, 1, kRwBuckets, kRwKeyBits>),
+                           dim3((unsigned)tblk), dim3(kRwBlock), 0, s, seg, stride, n,
+                           static_cast<int>(batch), Sw, idx, rows, static_cast<uint32_t*>(nullptr),
+                           sorted_seg, sorted_pos, bstart);
+      else
+        hipLaunchKernelGGL((seg_block_sort_kernel<IdxT, true, kTlThreads, kTlItems, kTlBuckets,
+                                                  kTlBucketBits>),
+                           dim3((unsigned)tblk), dim3(kTlThreads), 0, s, seg, stride, n,
+                           static_cast<int>(batch), S, idx, rows, static_cast<uint32_t*>(nullptr),
+                           sorted_seg, sorted_pos, bstart);
       ANNC_HIP_TRY(hipGetLastError());
       const int64_t lanes = dim / 4;
       const bool mean = combiner == ANNC_COMBINER_MEAN;
       auto go = [&](auto g_tag) -> int {
         constexpr int G = decltype(g_tag)::value;
-        auto k = mean ? seg_range_kernel<G, true, true> : seg_range_kernel<G, false, true>;
-        hipLaunchKernelGGL(k, rgrid, dim3(kTlThreads), 0, s, sorted_pos, sorted_seg, bstart, nb,
-                           static_cast<int>(batch), S, sbits, offsets, perm, data, rows, dim, out,
-                           status);
+        if (wave) {
+          auto k = mean ? seg_range_wave_kernel<G, true, kRwBuckets>
+                        : seg_range_wave_kernel<G, false, kRwBuckets>;
+          hipLaunchKernelGGL(k, dim3((unsigned)ceil_div(batch, Sw)), dim3(64), 0, s, sorted_pos,
+                             sorted_seg, bstart, nb, static_cast<int>(batch), Sw, sbits_w, perm,
+                             data, rows, dim, out, status);
+        } else {
+          auto k = mean ? seg_range_kernel<G, true, true> : seg_range_kernel<G, false, true>;
+          hipLaunchKernelGGL(k, rgrid, dim3(kTlThreads), 0, s, sorted_pos, sorted_seg, bstart, nb,
+                             static_cast<int>(batch), S, sbits, offsets, perm, data, rows, dim, out,
+                             status);
+        }
         ANNC_HIP_TRY(hipGetLastError());
         return ANNC_OK;
       };

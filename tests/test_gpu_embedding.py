@@ -130,6 +130,8 @@ SEG_ORDER_CASES = [
     ("sorted", 4096, 81857),
     ("two-level sort, 128 blocks", 4096, 131072),
     ("two-level sort, last block partial", 4096, 131073),
+    ("two-level sort, 5000 segments: 5 per one-wave range, 3 key bits", 5000, 90000),
+    ("two-level sort past the one-wave ranges' 1 Mi positions", 4096, 1_200_000),
     ("counting sort: past the two-level sort's 4 Mi positions", 64, 4 * 2**20 + 1),
     ("counting sort, ids outside [0, batch) dropped", 2000, 4 * 2**20 + 3000),
     ("three segments: more entries per range than its list holds", 3, 100000),
