@@ -1009,7 +1009,7 @@ __global__ __launch_bounds__(kTlThreads) void seg_range_kernel(
 // positions sorted into NB ranges by seg_block_sort_kernel<.., 1024, 1, NB>).
 // A single wave has no cross-wave barriers, and its stable ranking keeps the
 // per-segment counters in registers: lane s holds segment s's counter, and
-// every wave step of 64 list entries builds, from log2(S) ballots, both the
+// every wave step of 64 list entries builds, from four ballots, both the
 // mask of each entry's segment (its rank: the entries of that segment in
 // lower lanes) and the mask of segment `lane` (the counter update).
 //   1. slices: lane l takes blocks [l*per, l*per + per); a wave scan of the
@@ -1029,8 +1029,8 @@ constexpr int kRwBlock = 1024;                  // positions per block (1024 thr
 constexpr int kRwMaxBlocks = 1024;              // up to 1 Mi positions
 constexpr int kRwPer = kRwMaxBlocks / 64;       // blocks per lane
 constexpr int kRwCap = 2048;                    // the list (LDS)
-constexpr int kRwMaxS = 64;                     // segments per range (one per lane)
-constexpr int kRwMaxSBits = 6;
+constexpr int kRwMaxS = 16;                     // segments per range (one per lane)
+constexpr int kRwSBits = 4;                     // bits of a segment's place in its range
 static_assert(kRwBlock == kTlBlock, "both steps share the block layout of the sorted arrays");
 static_assert(kCsMaxSegments <= int64_t(kRwBuckets) * kRwMaxS, "segment ranges");
 
@@ -1045,8 +1045,7 @@ __device__ __forceinline__ int xcd_run(int b, int n) {
 template <int G, bool MEAN, int NB>
 __global__ __launch_bounds__(64) void seg_range_wave_kernel(
     const uint32_t* __restrict__ sorted_row, const uint16_t* __restrict__ sorted_seg,
-    const uint32_t* __restrict__ bstart, int nblk, int batch, int S, int sbits,
-    int32_t* __restrict__ perm, const float* __restrict__ data, int64_t rows, int64_t dim,
+    const uint32_t* __restrict__ bstart, int nblk, int batch, int S, int32_t* __restrict__ perm, const float* __restrict__ data, int64_t rows, int64_t dim,
     float* __restrict__ out, int* __restrict__ status) {
   __shared__ uint32_t src[kRwMaxBlocks];       // sorted index of the range's first entry in block a
   __shared__ uint32_t excl[kRwMaxBlocks + 1];  // the range's entries in the blocks before a
@@ -1144,22 +1143,22 @@ __global__ __launch_bounds__(64) void seg_range_wave_kernel(
   };
   // the step's ballots of the segment bits: masks of segment `s` among the
   // valid entries
+  // (all kRwSBits bits: a range's segments past S have no entries, so
+  // their masks are empty)
   struct Step {
-    uint64_t valid, bit[kRwMaxSBits];
+    uint64_t valid, bit[kRwSBits];
   };
   auto step_ballots = [&](uint32_t s, bool valid) {
     Step st;
     st.valid = __ballot(valid);
 #pragma unroll
-    for (int b = 0; b < kRwMaxSBits; ++b)
-      st.bit[b] = b < sbits ? __ballot(valid && ((s >> b) & 1u)) : 0;
+    for (int b = 0; b < kRwSBits; ++b) st.bit[b] = __ballot(valid && ((s >> b) & 1u));
     return st;
   };
   auto seg_mask = [&](const Step& st, uint32_t s) {
     uint64_t m = st.valid;
 #pragma unroll
-    for (int b = 0; b < kRwMaxSBits; ++b)
-      if (b < sbits) m &= ((s >> b) & 1u) ? st.bit[b] : ~st.bit[b];
+    for (int b = 0; b < kRwSBits; ++b) m &= ((s >> b) & 1u) ? st.bit[b] : ~st.bit[b];
     return m;
   };
   // 3a. lane s += the entries of segment s among list entries [0, len)
@@ -1191,7 +1190,7 @@ __global__ __launch_bounds__(64) void seg_range_wave_kernel(
     }
   };
   // 3b. segment starts (relative to the range) from the counts of lanes < ns
-  // (a lane at or past ns matched the segment its low sbits bits name)
+  // (a lane at or past ns matched the segment its low kRwSBits bits name)
   auto seg_starts = [&](uint32_t c_s) {
     if (static_cast<uint32_t>(lane) >= ns) c_s = 0;
     const uint32_t sc = wave_incl_sum(c_s);
@@ -1671,8 +1670,6 @@ int segment_reduce_run(hipStream_t s, const float* data, int64_t rows, int64_t d
     // one wave per range (kRwBuckets ranges) up to kRwMaxBlocks blocks
     const bool wave = tblk <= kRwMaxBlocks;
     const int Sw = static_cast<int>(std::max<int64_t>(1, ceil_div(batch, kRwBuckets)));
-    int sbits_w = 0;
-    while ((1 << sbits_w) < Sw) ++sbits_w;
     auto run_fused = [&](auto idx_tag) -> int {
       using IdxT = decltype(idx_tag);
       const IdxT* idx = static_cast<const IdxT*>(indices);
@@ -1697,7 +1694,7 @@ int segment_reduce_run(hipStream_t s, const float* data, int64_t rows, int64_t d
           auto k = mean ? seg_range_wave_kernel<G, true, kRwBuckets>
                         : seg_range_wave_kernel<G, false, kRwBuckets>;
           hipLaunchKernelGGL(k, dim3((unsigned)ceil_div(batch, Sw)), dim3(64), 0, s, sorted_pos,
-                             sorted_seg, bstart, nb, static_cast<int>(batch), Sw, sbits_w, perm,
+                             sorted_seg, bstart, nb, static_cast<int>(batch), Sw, perm,
                              data, rows, dim, out, status);
         } else {
           auto k = mean ? seg_range_kernel<G, true, true> : seg_range_kernel<G, false, true>;
