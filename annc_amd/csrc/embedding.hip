@@ -573,10 +573,11 @@ __global__ __launch_bounds__(kThreads) void cs_scatter_kernel(const int64_t* __r
 // segments and kTlMaxBlocks blocks of positions), in two launches before
 // the bag kernel:
 //   1. seg_block_sort: each block of kTlBlock positions is sorted by segment
-//      range (bucket = segment / S; ids outside [0, batch) go to bucket
-//      kTlBuckets), stably: equal buckets keep their position order.  It
-//      writes the sorted positions, their segments, and bstart[block][b],
-//      the first sorted index of bucket b (b = 0..kTlBuckets).
+//      range (bucket = segment / S; ids outside [0, batch) get the key
+//      kTlBuckets and are left out), stably: equal buckets keep their
+//      position order.  It writes the sorted positions, their segments, and
+//      bstart[block][b], the first sorted index of bucket b (b < kTlBuckets;
+//      bstart[block][kTlBuckets] counts the kept positions).
 //   2. seg_range: workgroup g owns the S segments of bucket g and takes the
 //      slice [bstart[a][g], bstart[a][g+1]) of every block a.  Blocks in
 //      order, each slice in position order: the concatenation is in position
@@ -657,8 +658,8 @@ __global__ __launch_bounds__(THREADS) void seg_block_sort_kernel(
   }
   __syncthreads();
   // per bucket: counts before each step (in place), total, and the bucket
-  // starts by a block scan of the totals (thread t: bucket t; the last
-  // thread also takes the dropped bucket NB)
+  // starts by a block scan of the totals (thread t: bucket t).  Dropped
+  // positions are not written, so their bucket needs no prefix.
   auto prefix_steps = [&](int b) {
     uint32_t c[kSteps];  // all loads first, so they travel together
 #pragma unroll
@@ -672,7 +673,6 @@ __global__ __launch_bounds__(THREADS) void seg_block_sort_kernel(
     return run;
   };
   const uint32_t tot = t < NB ? prefix_steps(t) : 0u;
-  if (t == THREADS - 1) prefix_steps(NB);
   const uint32_t inc = wave_incl_sum(tot);
   if (lane == 63) wsum[wave] = inc;
   __syncthreads();
@@ -680,16 +680,17 @@ __global__ __launch_bounds__(THREADS) void seg_block_sort_kernel(
 #pragma unroll
   for (int w = 0; w < kWaves; ++w) before += w < wave ? wsum[w] : 0u;  // loads in flight together
   if (t < NB) start[t] = before;
-  if (t == THREADS - 1) start[NB] = before + tot;  // first dropped entry
+  if (t == THREADS - 1) start[NB] = before + tot;  // kept positions of the block
   __syncthreads();
   uint32_t* bs = bstart + (int64_t)blockIdx.x * (NB + 1);
   if (t < NB) bs[t] = start[t];
   if (t == THREADS - 1) bs[NB] = start[NB];
 #pragma unroll
   for (int i = 0; i < ITEMS; ++i) {
+    if (key[i] == NB) continue;
     const uint32_t slot = start[key[i]] + cnt[i * kWaves + wave][key[i]] + rank[i];
     if constexpr (!ROWS) sorted_pos[b0 + slot] = static_cast<uint32_t>(b0 + i * THREADS + t);
-    sorted_seg[b0 + slot] = key[i] < NB ? static_cast<uint16_t>(v[i]) : uint16_t(0);
+    sorted_seg[b0 + slot] = static_cast<uint16_t>(v[i]);
     if constexpr (ROWS)
       sorted_row[b0 + slot] = static_cast<uint64_t>(iv[i]) < static_cast<uint64_t>(rows)
                                   ? static_cast<uint32_t>(iv[i]) : 0xffffffffu;
@@ -1042,7 +1043,8 @@ __device__ __forceinline__ int xcd_run(int b, int n) {
   return (x < rem ? x * (per + 1) : rem * (per + 1) + (x - rem) * per) + k;
 }
 
-template <int G, bool MEAN, int NB>
+// PER: blocks per lane at most (nblk <= 64 * PER).
+template <int G, bool MEAN, int NB, int PER>
 __global__ __launch_bounds__(64) void seg_range_wave_kernel(
     const uint32_t* __restrict__ sorted_row, const uint16_t* __restrict__ sorted_seg,
     const uint32_t* __restrict__ bstart, int nblk, int batch, int S, int32_t* __restrict__ perm, const float* __restrict__ data, int64_t rows, int64_t dim,
@@ -1063,9 +1065,9 @@ __global__ __launch_bounds__(64) void seg_range_wave_kernel(
 
   // 1. slices (loads unconditional: block clamped)
   const int per = (nblk + 63) / 64;
-  uint32_t s0[kRwPer], cnt[kRwPer];
+  uint32_t s0[PER], cnt[PER];
 #pragma unroll
-  for (int u = 0; u < kRwPer; ++u) {
+  for (int u = 0; u < PER; ++u) {
     if (u < per) {
       const int a = min(lane * per + u, nblk - 1);
       const uint32_t* bs = bstart + (int64_t)a * (NB + 1) + g;
@@ -1075,7 +1077,7 @@ __global__ __launch_bounds__(64) void seg_range_wave_kernel(
   }
   uint32_t below = 0, mine = 0;
 #pragma unroll
-  for (int u = 0; u < kRwPer; ++u) {
+  for (int u = 0; u < PER; ++u) {
     if (u < per) {
       const bool ok = lane * per + u < nblk;
       cnt[u] = ok ? cnt[u] - s0[u] : 0u;
@@ -1089,7 +1091,7 @@ __global__ __launch_bounds__(64) void seg_range_wave_kernel(
   const uint32_t first = inc - mine;  // this lane's first list entry
   uint32_t run = first;
 #pragma unroll
-  for (int u = 0; u < kRwPer; ++u) {
+  for (int u = 0; u < PER; ++u) {
     if (u < per) {
       const int a = lane * per + u;
       if (a < nblk) {
@@ -1104,7 +1106,7 @@ __global__ __launch_bounds__(64) void seg_range_wave_kernel(
   // 2. list entries [c0, c0 + len) into LDS (row ids and local segments)
   auto gather = [&](uint32_t c0, uint32_t len) {
 #pragma unroll
-    for (int u = 0; u < kRwPer; ++u) {
+    for (int u = 0; u < PER; ++u) {
       if (u < per) {
         const int a = lane * per + u;
         if (a < nblk) {
@@ -1691,8 +1693,12 @@ int segment_reduce_run(hipStream_t s, const float* data, int64_t rows, int64_t d
       auto go = [&](auto g_tag) -> int {
         constexpr int G = decltype(g_tag)::value;
         if (wave) {
-          auto k = mean ? seg_range_wave_kernel<G, true, kRwBuckets>
-                        : seg_range_wave_kernel<G, false, kRwBuckets>;
+          // two blocks per lane up to 128 blocks (the usual case: no loops
+          // over empty block slots), else up to kRwPer
+          auto k = tblk <= 128 ? (mean ? seg_range_wave_kernel<G, true, kRwBuckets, 2>
+                                       : seg_range_wave_kernel<G, false, kRwBuckets, 2>)
+                               : (mean ? seg_range_wave_kernel<G, true, kRwBuckets, kRwPer>
+                                       : seg_range_wave_kernel<G, false, kRwBuckets, kRwPer>);
           hipLaunchKernelGGL(k, dim3((unsigned)ceil_div(batch, Sw)), dim3(64), 0, s, sorted_pos,
                              sorted_seg, bstart, nb, static_cast<int>(batch), Sw, perm,
                              data, rows, dim, out, status);
