@@ -617,10 +617,12 @@ __global__ __launch_bounds__(THREADS) void seg_block_sort_kernel(
   // Positions are striped (item i of thread t is position b0 + i*THREADS + t),
   // so the wave steps (i, wave) taken in order visit positions in order.
   // Each step ranks its lanes per bucket by a ballot match over the key
-  // bits; cnt[i][wave][b] holds the step's bucket counts.  An entry's slot
-  // is then start[b] + (b's entries in the steps before) + its rank.
+  // bits; cnt[b][step] holds the step's bucket counts (a bucket's counts are
+  // 32 contiguous bytes, read and written as two 16-byte words).  An entry's
+  // slot is then start[b] + (b's entries in the steps before) + its rank.
   constexpr int kSteps = ITEMS * kWaves;
-  __shared__ uint16_t cnt[kSteps][NB + 1];
+  static_assert(kSteps == 16, "a bucket's step counts are two 16-byte LDS words");
+  __shared__ __align__(16) uint16_t cnt[NB + 1][kSteps];
   __shared__ uint32_t start[NB + 1];
   __shared__ uint32_t wsum[kWaves];
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
@@ -634,8 +636,8 @@ __global__ __launch_bounds__(THREADS) void seg_block_sort_kernel(
     v[i] = seg[(p < n ? p : n - 1) * stride];
     if constexpr (ROWS) iv[i] = static_cast<int64_t>(indices[p < n ? p : n - 1]);
   }
-  uint16_t* cflat = &cnt[0][0];
-  for (int k = t; k < kSteps * (NB + 1); k += THREADS) cflat[k] = 0;
+  u32x4* cwords = reinterpret_cast<u32x4*>(&cnt[0][0]);
+  for (int k = t; k < 2 * (NB + 1); k += THREADS) cwords[k] = u32x4(0u);
   uint32_t key[ITEMS], rank[ITEMS];
 #pragma unroll
   for (int i = 0; i < ITEMS; ++i) {
@@ -654,22 +656,29 @@ __global__ __launch_bounds__(THREADS) void seg_block_sort_kernel(
       same &= on ? bb : ~bb;
     }
     rank[i] = static_cast<uint32_t>(__popcll(same & lt));
-    if (rank[i] == 0) cnt[i * kWaves + wave][key[i]] = static_cast<uint16_t>(__popcll(same));
+    if (rank[i] == 0) cnt[key[i]][i * kWaves + wave] = static_cast<uint16_t>(__popcll(same));
   }
   __syncthreads();
   // per bucket: counts before each step (in place), total, and the bucket
   // starts by a block scan of the totals (thread t: bucket t).  Dropped
   // positions are not written, so their bucket needs no prefix.
   auto prefix_steps = [&](int b) {
-    uint32_t c[kSteps];  // all loads first, so they travel together
-#pragma unroll
-    for (int k = 0; k < kSteps; ++k) c[k] = cnt[k][b];
+    u32x4* wp = reinterpret_cast<u32x4*>(&cnt[b][0]);
+    const u32x4 w0 = wp[0], w1 = wp[1];
     uint32_t run = 0;
+    u32x4 o0, o1;
 #pragma unroll
-    for (int k = 0; k < kSteps; ++k) {
-      cnt[k][b] = static_cast<uint16_t>(run);
-      run += c[k];
+    for (int q = 0; q < 8; ++q) {  // two counts per 32-bit word
+      const uint32_t x = q < 4 ? w0[q] : w1[q - 4];
+      const uint32_t lo16 = run;
+      run += x & 0xffffu;
+      const uint32_t hi16 = run;
+      run += x >> 16;
+      const uint32_t packed = lo16 | (hi16 << 16);
+      if (q < 4) o0[q] = packed; else o1[q - 4] = packed;
     }
+    wp[0] = o0;
+    wp[1] = o1;
     return run;
   };
   const uint32_t tot = t < NB ? prefix_steps(t) : 0u;
@@ -688,7 +697,7 @@ __global__ __launch_bounds__(THREADS) void seg_block_sort_kernel(
 #pragma unroll
   for (int i = 0; i < ITEMS; ++i) {
     if (key[i] == NB) continue;
-    const uint32_t slot = start[key[i]] + cnt[i * kWaves + wave][key[i]] + rank[i];
+    const uint32_t slot = start[key[i]] + cnt[key[i]][i * kWaves + wave] + rank[i];
     if constexpr (!ROWS) sorted_pos[b0 + slot] = static_cast<uint32_t>(b0 + i * THREADS + t);
     sorted_seg[b0 + slot] = static_cast<uint16_t>(v[i]);
     if constexpr (ROWS)
