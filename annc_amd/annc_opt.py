@@ -8,14 +8,22 @@ Command line, as python/annc/main.py:14-68 (`annc-opt -I <in> -O <out> passes...
 
 Passes run in the order given, except that layout_matmul always runs last.
 
-The reference rewrites a TensorFlow SavedModel.  TensorFlow is not part of
-this build, so a model here is a directory holding
+A model is a TensorFlow SavedModel directory (saved_model.pb and
+variables/variables.{index,data-00000-of-00001}), read and written by
+`annc_amd.savedmodel` without TensorFlow: the graph of the "serve" meta
+graph, and the variables by node name (the key tf.compat.v1.train.Saver,
+which the reference saves with, gives a graph variable; a VarHandleOp is
+also found under its shared_name).  The output directory gets saved_model.pb
+with the rewritten graph, the variables with the packed weights, and
+everything else of the input (assets, ...) except the now stale
+saved_model.pbtxt, fingerprint.pb and old variables.  (The reference writes
+the new graph as saved_model.pbtxt beside an unchanged copy of
+saved_model.pb, graph.py:312-338, which TensorFlow, preferring the .pb,
+does not load.)
 
-    graph.json              {"nodes": [{"name", "op", "inputs": [...], "attrs": {...}}]}
-    variables.safetensors   one float32 array per variable node, keyed by node name
-
-with TensorFlow's op names (MatMul, BatchMatMul, Identity, ReadVariableOp,
-VarHandleOp, VariableV2, Variable) and the operand order of the graph.
+A directory without saved_model.pb is read in this build's plain form, for
+hand-written tests: graph.json ({"nodes": [{"name", "op", "inputs",
+"attrs"}]}) and variables.safetensors (one array per variable node).
 
 `layout_matmul` (constant_folding.py:11-98) pre-packs constant MatMul weights
 for `__layout_matmul`: every MatMul whose rhs resolves through Identity /
@@ -67,6 +75,8 @@ from dataclasses import dataclass, field
 from typing import Dict, List, Optional, Sequence
 
 import numpy as np
+
+from . import savedmodel
 
 VECTOR_LEN = 12                     # constant_folding.py:12 (__vector_len__)
 KN4_TILING = ((0, 352), (1, 128))   # constant_folding.py:94-95 (generate_tiling)
@@ -168,6 +178,7 @@ class Node:
 class Model:
     nodes: List[Node]
     variables: Dict[str, np.ndarray]
+    saved: Optional[savedmodel.SavedModelGraph] = None  # set for a SavedModel directory
 
     def node(self, name: str) -> Optional[Node]:
         base = name.split(":")[0].lstrip("^")
@@ -178,6 +189,10 @@ class Model:
 
 
 def load_model(path: str) -> Model:
+    if savedmodel.has_saved_model(path):
+        saved = savedmodel.read_saved_model(path)
+        nodes = [Node(g.name, g.op, list(g.inputs), dict(g.attrs)) for g in saved.nodes]
+        return Model(nodes, savedmodel.read_variables(path), saved)
     from safetensors.numpy import load_file
     with open(os.path.join(path, "graph.json")) as f:
         spec = json.load(f)
@@ -188,7 +203,36 @@ def load_model(path: str) -> Model:
     return Model(nodes, dict(variables))
 
 
+# input entries a SavedModel output does not copy: rewritten, or stale after the rewrite
+_SAVED_MODEL_OWN = ("saved_model.pb", "saved_model.pbtxt", "fingerprint.pb", "variables")
+
+
+def _save_saved_model(model: Model, path: str, source: Optional[str]) -> None:
+    old = {g.name: g for g in model.saved.nodes}
+    nodes = []
+    for n in model.nodes:
+        g = old.get(n.name)
+        nodes.append(savedmodel.GraphNode(n.name, n.op, list(n.inputs), dict(n.attrs),
+                                          g.device if g else "", list(g.extra) if g else []))
+    model.saved.nodes = nodes
+    os.makedirs(path, exist_ok=True)
+    savedmodel.write_saved_model(path, model.saved)
+    savedmodel.write_variables(path, model.variables)
+    if source and os.path.abspath(source) != os.path.abspath(path):
+        for entry in os.listdir(source):
+            if entry in _SAVED_MODEL_OWN:
+                continue
+            src, dst = os.path.join(source, entry), os.path.join(path, entry)
+            if os.path.isdir(src):
+                shutil.copytree(src, dst, dirs_exist_ok=True)
+            else:
+                shutil.copy2(src, dst)
+
+
 def save_model(model: Model, path: str, source: Optional[str] = None) -> None:
+    if model.saved is not None:
+        _save_saved_model(model, path, source)
+        return
     from safetensors.numpy import save_file
     os.makedirs(path, exist_ok=True)
     with open(os.path.join(path, "graph.json"), "w") as f:
@@ -213,13 +257,18 @@ def save_model(model: Model, path: str, source: Optional[str] = None) -> None:
 # layout_matmul
 # ---------------------------------------------------------------------------
 def _variable_operand(model: Model, name: str) -> Optional[str]:
-    """The variable a MatMul operand reads, through Identity / ReadVariableOp
-    (constant_folding.py:65-75)."""
+    """The key of the variable a MatMul operand reads, through Identity /
+    ReadVariableOp (constant_folding.py:65-75): its node name, or a
+    VarHandleOp's shared_name when only that names a stored variable."""
     nd = model.node(name)
     seen = set()
     while nd is not None and nd.name not in seen:
         seen.add(nd.name)
         if nd.op in VARIABLE_OPS:
+            shared = nd.attrs.get("shared_name")
+            if nd.name not in model.variables and isinstance(shared, str) and \
+                    shared in model.variables:
+                return shared
             return nd.name
         if nd.op in PASS_THROUGH_OPS and nd.inputs:
             nd = model.node(nd.inputs[0])
@@ -440,7 +489,7 @@ def _rewrite_embedding(model: Model, anchor: Node, bound: Dict[str, Node], mean:
     ed, gather, result, hash_node = bound["ed"], bound["gather"], bound["result"], bound["hash"]
     attrs = {k: v for k, v in hash_node.attrs.items() if k != "_output_shapes"}
     attrs["combiner"] = 1 if mean else 0
-    attrs["T_weight"] = "DT_FLOAT" if mean else "DT_RESOURCE"
+    attrs["T_weight"] = savedmodel.DType("DT_FLOAT" if mean else "DT_RESOURCE")
     if "_output_shapes" in result.attrs:
         attrs["_output_shapes"] = result.attrs["_output_shapes"]
     fused = Node(anchor.name + suffix, op, [ed.inputs[0], gather.inputs[0]], attrs)

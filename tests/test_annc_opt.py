@@ -7,6 +7,7 @@ import pytest
 
 from annc_amd import annc_opt
 from annc_amd import device as dev
+from annc_amd import savedmodel as sm
 
 GOLD = os.path.join(os.path.dirname(__file__), "golden", "kn4_pack_vectors.npz")
 
@@ -36,7 +37,30 @@ def test_kn4_round_trip(k, n):
     np.testing.assert_array_equal(annc_opt.unpack_kn4(annc_opt.pack_kn4(w), k, n), w)
 
 
-def _model(tmp_path):
+def _shapes_attr(*shapes):
+    """AttrValue {list {shape ...}} (an `_output_shapes` attr) as raw bytes."""
+    lst = sm.Msg([(7, sm.LEN, sm.shape_proto(s)) for s in shapes])
+    return sm.RawAttr(sm.Msg([(1, sm.LEN, lst)]).serialize())
+
+
+def _as_form(nodes, variables, form):
+    """The model in this build's plain form, or as a SavedModel (graph attrs
+    as TensorFlow types them: dtype attrs as DataType, shape lists raw)."""
+    if form == "json":
+        return annc_opt.Model(nodes, variables)
+    for n in nodes:
+        for k, v in list(n.attrs.items()):
+            if k == "_output_shapes":
+                n.attrs[k] = _shapes_attr(*v)
+            elif k == "dtype":
+                n.attrs[k] = sm.DType(v)
+    return annc_opt.Model(nodes, variables, sm.new_saved_model([]))
+
+
+FORMS = ["json", "saved"]
+
+
+def _model(tmp_path, form="json"):
     g = np.random.default_rng(7)
     f32 = lambda *s: g.standard_normal(s).astype(np.float32)  # noqa: E731
     orig = {"w1": f32(64, 48), "w2": f32(8, 64), "w3l": f32(4, 20), "w3": f32(20, 30),
@@ -58,14 +82,18 @@ def _model(tmp_path):
         annc_opt.Node("m7", "MatMul", ["x", "w7:0"], {"transpose_b": True}),
     ]
     src = tmp_path / "in"
-    annc_opt.save_model(annc_opt.Model(nodes, variables), str(src))
+    annc_opt.save_model(_as_form(nodes, variables, form), str(src))
     (src / "assets").mkdir()
     (src / "assets" / "vocab.txt").write_text("a\nb\n")
     return src, orig, variables
 
 
-def test_layout_matmul_cli(tmp_path):
-    src, orig, before = _model(tmp_path)
+@pytest.mark.parametrize("form", FORMS)
+def test_layout_matmul_cli(tmp_path, form):
+    src, orig, before = _model(tmp_path, form)
+    if form == "saved":  # made stale by the rewrite: not copied
+        (src / "saved_model.pbtxt").write_text("stale")
+        (src / "fingerprint.pb").write_bytes(b"stale")
     out = tmp_path / "out"
     assert annc_opt.main(["-I", str(src), "-O", str(out), "layout_matmul"]) == 0
     m = annc_opt.load_model(str(out))
@@ -84,6 +112,14 @@ def test_layout_matmul_cli(tmp_path):
         assert "rhs_format" not in attrs[node] or node == "m5"
     np.testing.assert_array_equal(m.variables["w5"], before["w5"])
     assert (out / "assets" / "vocab.txt").read_text() == "a\nb\n"
+    if form == "saved":
+        assert sorted(os.listdir(out)) == ["assets", "saved_model.pb", "variables"]
+        assert sorted(os.listdir(out / "variables")) == ["variables.data-00000-of-00001",
+                                                         "variables.index"]
+        # the attrs TensorFlow reads: rhs_format a string, transpose_b a bool
+        g = sm.read_saved_model(str(out))
+        raw = {n.name: n for n in g.nodes}
+        assert raw["m1"].attrs["rhs_format"] == fmt and raw["m7"].attrs["transpose_b"] is True
 
 
 def test_unknown_and_unsupported_passes_are_rejected(tmp_path):
@@ -206,7 +242,7 @@ def _column(p, inp, weight, combiner, num_buckets):
     return nodes, tail[-1].name, fused
 
 
-def _embedding_model(tmp_path, columns=(("sum", 1000), ("mean", 77)), extra=None):
+def _embedding_model(tmp_path, columns=(("sum", 1000), ("mean", 77)), extra=None, form="json"):
     N = annc_opt.Node
     nodes, results, fused = [], [], {}
     g = np.random.default_rng(3)
@@ -234,12 +270,13 @@ def _embedding_model(tmp_path, columns=(("sum", 1000), ("mean", 77)), extra=None
     if extra:
         extra(nodes)
     src = tmp_path / "emb_in"
-    annc_opt.save_model(annc_opt.Model(nodes, variables), str(src))
+    annc_opt.save_model(_as_form(nodes, variables, form), str(src))
     return src, results, fused
 
 
-def test_embed_hash_bucket_fuses_sum_and_mean_columns(tmp_path):
-    src, results, fused = _embedding_model(tmp_path)
+@pytest.mark.parametrize("form", FORMS)
+def test_embed_hash_bucket_fuses_sum_and_mean_columns(tmp_path, form):
+    src, results, fused = _embedding_model(tmp_path, form=form)
     before = annc_opt.load_model(str(src))
     out = tmp_path / "emb_out"
     # layout_matmul given first still runs last, on the fused graph
@@ -252,10 +289,15 @@ def test_embed_hash_bucket_fuses_sum_and_mean_columns(tmp_path):
     f1 = by["col1/SparseFillEmptyRows/rec_embed_kp_bucket"]
     assert f0.op == f1.op == "KPFusedEmbeddingWithHashBucket"
     assert f0.inputs == ["in0", "emb0"] and f1.inputs == ["in1", "emb1/read"]
+    shapes = [[-1, 16]] if form == "json" else _shapes_attr([-1, 16])
     assert f0.attrs == {"num_buckets": 1000, "combiner": 0, "T_weight": "DT_RESOURCE",
-                        "_output_shapes": [[-1, 16]]}
+                        "_output_shapes": shapes}
     assert f1.attrs == {"num_buckets": 77, "combiner": 1, "T_weight": "DT_FLOAT",
-                        "_output_shapes": [[-1, 16]]}
+                        "_output_shapes": shapes}
+    if form == "saved":  # T_weight is a DataType attr (DT_RESOURCE 20, DT_FLOAT 1)
+        assert isinstance(f0.attrs["T_weight"], sm.DType)
+        assert sm.Msg.parse(sm.encode_attr(f0.attrs["T_weight"])).fields == [(6, sm.VARINT, 20)]
+        assert sm.Msg.parse(sm.encode_attr(f1.attrs["T_weight"])).fields == [(6, sm.VARINT, 1)]
     assert len(fused["col0"]) == 45 and len(fused["col1"]) == 42
     for col in fused.values():
         assert not set(col) & set(names)

@@ -415,3 +415,34 @@ def test_custom_calls_from_concurrent_threads():
         t.join(timeout=100)
     assert not any(t.is_alive() for t in threads), "a worker thread did not finish"
     assert not errors, errors[0]
+
+
+def test_layout_matmul_on_weights_packed_in_a_saved_model(tmp_path):
+    """annc-opt's layout_matmul on a SavedModel (graph and variables read and
+    written without TensorFlow): the packed variable read back from the
+    output's tensor bundle drives __layout_matmul to the row-major product."""
+    from annc_amd import annc_opt
+    from annc_amd import savedmodel as sm
+    note("annc-opt layout_matmul on a SavedModel, then __layout_matmul 4096x512x1024")
+    g = workloads.rng(41)
+    w = g.standard_normal((1024, 512)).astype(np.float32)
+    a = g.standard_normal((4096, 1024)).astype(np.float32)
+    nodes = [sm.GraphNode("x", "Placeholder", [], {"dtype": sm.DType("DT_FLOAT")}),
+             sm.GraphNode("dense/kernel", "VariableV2", [], {"dtype": sm.DType("DT_FLOAT")}),
+             sm.GraphNode("dense/kernel/read", "Identity", ["dense/kernel"],
+                          {"T": sm.DType("DT_FLOAT")}),
+             sm.GraphNode("dense/MatMul", "MatMul", ["x", "dense/kernel/read"],
+                          {"T": sm.DType("DT_FLOAT"), "transpose_a": False,
+                           "transpose_b": False})]
+    src, out_dir = tmp_path / "in", tmp_path / "out"
+    sm.write_saved_model(str(src), sm.new_saved_model(nodes))
+    sm.write_variables(str(src), {"dense/kernel": w})
+    assert annc_opt.main(["-I", str(src), "-O", str(out_dir), "layout_matmul"]) == 0
+    graph = sm.read_saved_model(str(out_dir))
+    mm = sm.find_node(graph.nodes, "dense/MatMul")
+    assert mm.attrs["rhs_format"] == annc_opt.mfma_rhs_format()
+    packed = sm.read_variables(str(out_dir))["dense/kernel"]
+    assert packed.shape == w.shape and not np.array_equal(packed, w)
+    out = np.empty((4096, 512), np.float32)
+    xla.layout_matmul(a, packed, 1024, 512, out)
+    assert_gemm_close(out, ora.matmul(a, w), gemm_bound(a, w))
