@@ -397,6 +397,23 @@ def make_case(name: str, device, inp: Inputs) -> Case:
                     "bag kernel, sequential rows: table [4Mi x 64] (1 GiB) read once in order, "
                     "bags of 128 ids (streaming-read reference)", "bag_kernel_stream_reference",
                     launches=10)
+    if name in ("gather_probe", "gather_probe_cold"):
+        # random-row ceiling: rows of 16 floats (configs[3]'s 64 bytes) at
+        # uniformly random positions, 8 in flight per 4-lane group, no index
+        # loads; 2.6 Mi rows (166 MB, configs[3]'s 26 tables, MALL-resident)
+        # or 64 Mi rows (4 GiB, from HBM); 5.2 M rows per launch
+        rows_n = (26 * 100_000) if name == "gather_probe" else (64 << 20)
+        table = torch.ones((rows_n, 16), dtype=torch.float32, device=device)
+        blocks, per = 2048, 40
+        out = torch.empty(blocks * 256, dtype=torch.float32, device=device)
+        n_rows = blocks * 64 * per
+        return Case(name, lambda i: dev.probe_random_rows(table, blocks, per, out),
+                    64 * n_rows, "hbm",
+                    f"random-row probe: {n_rows} rows of 64 B at uniform random positions of a "
+                    f"[{rows_n} x 16] table ({rows_n * 64 / 1e6:.0f} MB), 8 in flight per 4-lane "
+                    "group, no index loads (the random-gather ceiling)",
+                    "probe_random_rows_" + ("mall_166MB" if name == "gather_probe" else "hbm_4GiB"),
+                    launches=10)
     if name == "copy":
         src = torch.ones(64 << 20, dtype=torch.float32, device=device)
         dst = torch.empty_like(src)
@@ -409,12 +426,14 @@ def make_case(name: str, device, inp: Inputs) -> Case:
 CASES = ("tower", "widedeep", "gemm_l1", "gemm_l2", "gemm_l3", "gemm_small", "gemm_e2e_l1", "batch_matmul",
          "bag_sum", "bag_mean", "bag_sum_cold", "hashed", "hashed_cold", "hashed_nohash",
          "hashed_dim32", "sparse_embedding2", "pooling", "segment_reduce_sorted",
-         "segment_reduce_any", "hash_bucket", "copy", "bag_stream", "torch_mm_l1")
+         "segment_reduce_any", "hash_bucket", "copy", "bag_stream", "torch_mm_l1",
+         "gather_probe", "gather_probe_cold")
 # the cases reported under `components` (gemm_l1 is the roofline, copy the calibration)
 COMPONENT_CASES = ("gemm_small", "gemm_l2", "gemm_l3", "gemm_e2e_l1", "batch_matmul",
                    "bag_sum", "bag_mean", "bag_sum_cold", "hashed", "hashed_cold",
                    "hashed_nohash", "hashed_dim32", "sparse_embedding2", "pooling",
-                   "segment_reduce_sorted", "segment_reduce_any", "hash_bucket")
+                   "segment_reduce_sorted", "segment_reduce_any", "hash_bucket",
+                   "gather_probe", "gather_probe_cold")
 
 
 def bench_case(c: Case, replays: int = 5) -> dict:

@@ -512,3 +512,17 @@ def test_bag_random_shapes_bit_exact(seed):
     got = to_host(out)
     np.testing.assert_array_equal(got[:, :dim], ref)
     np.testing.assert_array_equal(got[:, dim:], 3.0)
+
+
+@pytest.mark.parametrize("dim", [16, 32, 64])
+def test_random_row_probe_reads_what_it_counts(dim):
+    """The measurement kernel behind bench.py's gather_probe cases: every lane
+    sums rows_per_group 16-byte chunks of a table of ones, so each lane's
+    output is exactly 4 * rows_per_group (and the grid covers `out`)."""
+    note(f"random-row probe, dim {dim}")
+    table = torch.ones((5000, dim), dtype=torch.float32, device=device())
+    out = torch.full((3 * 256,), -1.0, dtype=torch.float32, device=device())
+    dev.probe_random_rows(table, 3, 24, out)
+    np.testing.assert_array_equal(to_host(out), np.full(3 * 256, 96.0, np.float32))
+    with pytest.raises(Exception, match="multiple of 8"):
+        dev.probe_random_rows(table, 3, 12, out)
