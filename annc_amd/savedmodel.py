@@ -8,9 +8,10 @@ The reference tool goes through TensorFlow (python/annc/optimize/graph.py:
 with tf.compat.v1.train.Saver).  Here the formats are handled directly:
 
   * Protocol-buffer wire format (varints, length-delimited fields, fixed32 /
-    fixed64).  Messages are kept as ordered field lists, so a message that is
-    not edited is written back byte for byte, and fields this module does not
-    name survive a rewrite.  Field numbers follow TensorFlow's .proto files:
+    fixed64).  Messages are kept as ordered field lists, so the SavedModel,
+    meta graph and graph fields around the nodes are written back byte for
+    byte, and fields this module does not name survive a rewrite; the nodes
+    themselves are re-encoded (attrs in key order, as TensorFlow writes them).  Field numbers follow TensorFlow's .proto files:
     SavedModel {1 schema version, 2 meta_graphs}; MetaGraphDef {1
     meta_info_def (4 tags), 2 graph_def, ...}; GraphDef {1 node, ...};
     NodeDef {1 name, 2 op, 3 input, 4 device, 5 attr map}; AttrValue {1
