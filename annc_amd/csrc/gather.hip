@@ -236,6 +236,51 @@ __global__ void fo_mark_kernel(const int64_t* __restrict__ keys, int64_t stride,
   first_mark[i] = first[keys[i * stride] - kmin] == static_cast<int32_t>(i) ? 1 : 0;
 }
 
+// Without global atomics, for small ranges (the segment column of
+// KPFusedSparseSegmentReduceNonzero): workgroup b takes positions
+// [b*kFoBlock, (b+1)*kFoBlock), keeps each key's smallest position in an
+// LDS table (LDS atomics) and writes the table to part[b][0, range);
+// fo_merge_kernel then takes the minimum over the workgroups.  The global
+// table of a small range is a few cache lines, which serialise the atomics
+// of every position on them.
+constexpr int kFoThreads = 1024;
+constexpr int kFoItems = 4;
+constexpr int kFoBlock = kFoThreads * kFoItems;  // positions per workgroup
+constexpr int64_t kFoLdsRange = 8192;            // keys in LDS (32 KiB)
+constexpr int64_t kFoMaxBlocks = 64;             // workgroups merged per key
+
+__global__ __launch_bounds__(kFoThreads) void fo_local_min_kernel(
+    const int64_t* __restrict__ keys, int64_t stride, int64_t n, int64_t kmin, int range,
+    int32_t* __restrict__ part) {
+  extern __shared__ int32_t fo_tab[];
+  for (int r = threadIdx.x; r < range; r += kFoThreads) fo_tab[r] = INT_MAX;
+  const int64_t b0 = (int64_t)blockIdx.x * kFoBlock;
+  int64_t k[kFoItems];
+#pragma unroll
+  for (int u = 0; u < kFoItems; ++u) {  // loads issued together (position clamped)
+    const int64_t i = b0 + u * kFoThreads + threadIdx.x;
+    k[u] = keys[(i < n ? i : n - 1) * stride];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int u = 0; u < kFoItems; ++u) {
+    const int64_t i = b0 + u * kFoThreads + threadIdx.x;
+    if (i < n) atomicMin(fo_tab + (k[u] - kmin), static_cast<int32_t>(i));
+  }
+  __syncthreads();
+  int32_t* dst = part + (int64_t)blockIdx.x * range;
+  for (int r = threadIdx.x; r < range; r += kFoThreads) dst[r] = fo_tab[r];
+}
+
+__global__ void fo_merge_kernel(const int32_t* __restrict__ part, int nblk, int range,
+                                int32_t* __restrict__ first) {
+  const int r = blockIdx.x * kThreads + threadIdx.x;
+  if (r >= range) return;
+  int32_t m = INT_MAX;
+  for (int b = 0; b < nblk; ++b) m = min(m, part[(int64_t)b * range + r]);
+  first[r] = m;
+}
+
 // number[i] = inclusive count of first occurrences up to i
 __global__ void fo_output_kernel(const int64_t* __restrict__ keys, int64_t stride, int64_t n,
                                  int64_t kmin, const int32_t* __restrict__ first,
@@ -262,20 +307,34 @@ int first_occurrence_range(hipStream_t s, const int64_t* keys, int64_t stride, i
   ANNC_HIP_TRY(hipcub::DeviceScan::InclusiveSum(nullptr, scan, (const int32_t*)nullptr,
                                                 (int32_t*)nullptr, (int)n, s));
   auto align = [](size_t x) { return (x + 255) & ~size_t(255); };
+  const int64_t nblk = ceil_div(n, kFoBlock);
+  const bool local = range <= kFoLdsRange && nblk <= kFoMaxBlocks;
   const size_t fb = align(sizeof(int32_t) * (size_t)range);
   const size_t n4 = align(sizeof(int32_t) * (size_t)n);
-  char* ws = static_cast<char*>(stream_workspace(s, fb + 2 * n4 + align(scan)));
+  const size_t pb = local ? align(sizeof(int32_t) * (size_t)(nblk * range)) : 0;
+  char* ws = static_cast<char*>(stream_workspace(s, fb + 2 * n4 + pb + align(scan)));
   if (!ws) return set_error(ANNC_RESOURCE_EXHAUSTED, "workspace allocation failed");
   int32_t* first = reinterpret_cast<int32_t*>(ws);
   int32_t* mark = reinterpret_cast<int32_t*>(ws + fb);
   int32_t* number = reinterpret_cast<int32_t*>(ws + fb + n4);
-  void* tmp = ws + fb + 2 * n4;
+  int32_t* part = reinterpret_cast<int32_t*>(ws + fb + 2 * n4);
+  void* tmp = ws + fb + 2 * n4 + pb;
   const dim3 grid((unsigned)ceil_div(n, kThreads));
-  hipLaunchKernelGGL(fo_fill_kernel, dim3((unsigned)ceil_div(range, kThreads)), dim3(kThreads), 0,
-                     s, first, range);
-  ANNC_HIP_TRY(hipGetLastError());
-  hipLaunchKernelGGL(fo_min_kernel, grid, dim3(kThreads), 0, s, keys, stride, n, kmin, first);
-  ANNC_HIP_TRY(hipGetLastError());
+  if (local) {
+    hipLaunchKernelGGL(fo_local_min_kernel, dim3((unsigned)nblk), dim3(kFoThreads),
+                       sizeof(int32_t) * (size_t)range, s, keys, stride, n, kmin,
+                       static_cast<int>(range), part);
+    ANNC_HIP_TRY(hipGetLastError());
+    hipLaunchKernelGGL(fo_merge_kernel, dim3((unsigned)ceil_div(range, kThreads)), dim3(kThreads),
+                       0, s, part, static_cast<int>(nblk), static_cast<int>(range), first);
+    ANNC_HIP_TRY(hipGetLastError());
+  } else {
+    hipLaunchKernelGGL(fo_fill_kernel, dim3((unsigned)ceil_div(range, kThreads)), dim3(kThreads),
+                       0, s, first, range);
+    ANNC_HIP_TRY(hipGetLastError());
+    hipLaunchKernelGGL(fo_min_kernel, grid, dim3(kThreads), 0, s, keys, stride, n, kmin, first);
+    ANNC_HIP_TRY(hipGetLastError());
+  }
   hipLaunchKernelGGL(fo_mark_kernel, grid, dim3(kThreads), 0, s, keys, stride, n, kmin, first,
                      mark);
   ANNC_HIP_TRY(hipGetLastError());
