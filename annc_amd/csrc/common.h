@@ -5,6 +5,8 @@
 
 #include <hip/hip_runtime.h>
 
+#include <initializer_list>
+
 #include <cstddef>
 #include <cstdint>
 #include <vector>
@@ -35,6 +37,19 @@ bool is_device_ptr(const void* p);
 
 // Copies `count` int64 values from host or device memory into `dst`.
 int read_i64(const void* src, int64_t count, int64_t* dst);
+
+// Small device-to-host reads after the work queued on `stream`: every
+// (host dst, device src, bytes) goes through a pinned buffer of the calling
+// thread (hipHostMalloc'd once per device, at most kReadBackBytes in all),
+// then one synchronisation; a pageable destination would make the runtime
+// stage each copy.
+struct ReadBack {
+  void* dst;
+  const void* src;
+  size_t bytes;
+};
+constexpr size_t kReadBackBytes = 64 << 10;
+int read_back(hipStream_t stream, std::initializer_list<ReadBack> items);
 
 // Staging for synchronous entry points whose operands may live in host
 // memory: inputs are copied to device scratch, outputs are produced in

@@ -1546,9 +1546,8 @@ int segment_scan(hipStream_t s, const int64_t* seg, int64_t stride, int64_t n, i
   hipLaunchKernelGGL(seg_scan_kernel, dim3(blocks), dim3(kThreads), 0, s, seg, stride, n, part);
   ANNC_HIP_TRY(hipGetLastError());
   long long host[3 * kMaxBlocks];
-  ANNC_HIP_TRY(hipMemcpyAsync(host, part, sizeof(long long) * 3 * blocks, hipMemcpyDeviceToHost,
-                              s));
-  ANNC_HIP_TRY(hipStreamSynchronize(s));
+  const int rc = read_back(s, {{host, part, sizeof(long long) * 3 * blocks}});
+  if (rc != ANNC_OK) return rc;
   for (int b = 0; b < blocks; ++b) {
     *min_out = std::min<int64_t>(*min_out, host[3 * b]);
     *max_out = std::max<int64_t>(*max_out, host[3 * b + 1]);

@@ -1035,9 +1035,9 @@ int run_sparse_embedding(hipStream_t s, const int64_t* offsets, const int64_t* b
                      keep, pos, n, indices, values, empty);
   ANNC_HIP_TRY(hipGetLastError());
   int32_t last[2];
-  ANNC_HIP_TRY(hipMemcpyAsync(&last[0], pos + n - 1, sizeof(int32_t), hipMemcpyDeviceToHost, s));
-  ANNC_HIP_TRY(hipMemcpyAsync(&last[1], keep + n - 1, sizeof(int32_t), hipMemcpyDeviceToHost, s));
-  ANNC_HIP_TRY(hipStreamSynchronize(s));
+  const int rc = read_back(s, {{&last[0], pos + n - 1, sizeof(int32_t)},
+                               {&last[1], keep + n - 1, sizeof(int32_t)}});
+  if (rc != ANNC_OK) return rc;
   *num_values = (int64_t)last[0] + last[1];
   return ANNC_OK;
 }

@@ -118,6 +118,38 @@ int read_i64(const void* src, int64_t count, int64_t* dst) {
 }
 
 namespace {
+// Pinned bounce buffers of the calling thread, one per device (kept until
+// the process ends: releasing them at thread exit could run after the HIP
+// runtime has shut down).
+thread_local std::map<int, char*> t_pinned;
+}  // namespace
+
+int read_back(hipStream_t stream, std::initializer_list<ReadBack> items) {
+  size_t total = 0;
+  for (const ReadBack& it : items) total += (it.bytes + 15) & ~size_t(15);
+  if (total > kReadBackBytes)
+    return set_error(ANNC_INTERNAL, "read-back of %zu bytes above the %zu-byte buffer", total,
+                     kReadBackBytes);
+  char*& pin = t_pinned[current_device()];
+  if (!pin) {
+    ANNC_HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(&pin), kReadBackBytes,
+                               hipHostMallocDefault));
+  }
+  size_t off = 0;
+  for (const ReadBack& it : items) {
+    ANNC_HIP_TRY(hipMemcpyAsync(pin + off, it.src, it.bytes, hipMemcpyDeviceToHost, stream));
+    off += (it.bytes + 15) & ~size_t(15);
+  }
+  ANNC_HIP_TRY(hipStreamSynchronize(stream));
+  off = 0;
+  for (const ReadBack& it : items) {
+    std::memcpy(it.dst, pin + off, it.bytes);
+    off += (it.bytes + 15) & ~size_t(15);
+  }
+  return ANNC_OK;
+}
+
+namespace {
 // Grow-only device staging memory of the calling thread (one per device).
 // A Staging object carves its buffers from it and releases them when it is
 // destroyed, after its stream has drained, so the next synchronous call of
@@ -233,9 +265,9 @@ int annc_hip_stream_status(void* stream) {
   hipStream_t s = static_cast<hipStream_t>(stream);
   int* st = annc::stream_status(s);
   if (!st) return annc::set_error(ANNC_INTERNAL, "status word allocation failed");
-  ANNC_HIP_TRY(hipStreamSynchronize(s));
   int host = 0;
-  ANNC_HIP_TRY(hipMemcpy(&host, st, sizeof(int), hipMemcpyDeviceToHost));
+  const int rc = annc::read_back(s, {{&host, st, sizeof(int)}});
+  if (rc != ANNC_OK) return rc;
   if (host != 0) {
     ANNC_HIP_TRY(hipMemset(st, 0, sizeof(int)));
     return annc::set_error(ANNC_INVALID_ARGUMENT,

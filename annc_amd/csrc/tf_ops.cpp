@@ -145,7 +145,8 @@ int annc_kp_fused_sparse_segment_reduce(const float* data, int data_rank, const 
   rc = st.finish();
   if (rc != ANNC_OK) return rc;
   int bad = 0;
-  ANNC_HIP_TRY(hipMemcpy(&bad, status, sizeof(int), hipMemcpyDeviceToHost));
+  rc = read_back(s, {{&bad, status, sizeof(int)}});
+  if (rc != ANNC_OK) return rc;
   if (bad) {
     ANNC_HIP_TRY(hipMemset(status, 0, sizeof(int)));
     return set_error(ANNC_INVALID_ARGUMENT, "indices out of range of the %lld data rows",
@@ -228,8 +229,8 @@ int annc_kp_fused_sparse_segment_reduce_nonzero(
                                 d_uniq, d_slot, nullptr);
   if (rc != ANNC_OK) return rc;
   int64_t nseg = 0;
-  ANNC_HIP_TRY(hipMemcpyAsync(&nseg, d_nu, sizeof(int64_t), hipMemcpyDeviceToHost, s));
-  ANNC_HIP_TRY(hipStreamSynchronize(s));
+  rc = read_back(s, {{&nseg, d_nu, sizeof(int64_t)}});
+  if (rc != ANNC_OK) return rc;
   rc = widen_i32(s, d_slot, num_indices, d_slot64);
   if (rc != ANNC_OK) return rc;
 
@@ -263,10 +264,9 @@ int annc_kp_fused_sparse_segment_reduce_nonzero(
                        cap, d_out_idx, d_out_val);
   if (rc != ANNC_OK) return rc;
   int32_t nnz = 0;
-  ANNC_HIP_TRY(hipMemcpyAsync(&nnz, d_incl + (count - 1), sizeof(int32_t), hipMemcpyDeviceToHost, s));
   int bad = 0;
-  ANNC_HIP_TRY(hipMemcpyAsync(&bad, status, sizeof(int), hipMemcpyDeviceToHost, s));
-  ANNC_HIP_TRY(hipStreamSynchronize(s));
+  rc = read_back(s, {{&nnz, d_incl + (count - 1), sizeof(int32_t)}, {&bad, status, sizeof(int)}});
+  if (rc != ANNC_OK) return rc;
   if (bad) {
     ANNC_HIP_TRY(hipMemset(status, 0, sizeof(int)));
     return set_error(ANNC_INVALID_ARGUMENT, "indices out of range of the %lld data rows",
@@ -399,7 +399,8 @@ int annc_kp_fused_gather(const float* data, int data_rank, const int64_t* data_d
   if (annc_hip_stream_status(s) != ANNC_OK)  // synchronises
     return set_error(ANNC_INTERNAL, "idx out of table range");
   int64_t u = 0;
-  ANNC_HIP_TRY(hipMemcpy(&u, d_nu, sizeof(u), hipMemcpyDeviceToHost));
+  rc = read_back(s, {{&u, d_nu, sizeof(u)}});
+  if (rc != ANNC_OK) return rc;
   *num_unique = u;
   if (out_unique)
     ANNC_HIP_TRY(hipMemcpy(out_unique, d_uniq, sizeof(int64_t) * (size_t)u, hipMemcpyDefault));
