@@ -171,6 +171,25 @@ def test_device_segment_reduce_orders(what, batch, n, combiner):
         np.testing.assert_array_equal(to_host(out), ref)
 
 
+@pytest.mark.parametrize("dim", [4, 6, 12, 16, 32, 64, 128, 256, 300])
+@pytest.mark.parametrize("idx64", [True, False])
+def test_device_segment_reduce_any_order_dims(dim, idx64):
+    """Unsorted segment ids at every lane-group width of the fused range
+    kernels (G = 4..64 lanes a segment; dim 300 takes two column chunks;
+    dim 6 is not a multiple of 4 and takes the sort with perm and the bag
+    kernel), int32 and int64 indices, both combiners: bit-exact."""
+    note(f"device segment reduce any order dim={dim} idx64={idx64}")
+    g = workloads.rng(dim * 2 + idx64)
+    rows, n, batch = 700, 9000, 1500
+    data = g.standard_normal((rows, dim)).astype(np.float32)
+    idx = g.integers(0, rows, size=n).astype(np.int64 if idx64 else np.int32)
+    seg = g.integers(0, batch, size=n).astype(np.int64)
+    for combiner in (0, 1):
+        out = dev.segment_reduce(to_dev(data), to_dev(idx), to_dev(seg), batch, combiner)
+        np.testing.assert_array_equal(to_host(out), ora.segment_reduce(data, idx, seg, batch,
+                                                                       combiner))
+
+
 def test_device_segment_reduce_unsorted():
     note("device segment reduce")
     g = workloads.rng(8)
