@@ -162,6 +162,31 @@ struct GlobalIds {
   }
 };
 
+// Row ids of bag positions from an LDS copy of ids[w0, w0 + wn) when every
+// position the wave asks for lies there, else from global memory (the
+// choice is made per wave, so either way the loads need no per-lane branch).
+template <typename IdxT>
+struct WindowIds {
+  const IdxT* ids;
+  const IdxT* win;  // LDS
+  int64_t w0, wn;
+  template <int K>
+  __device__ __forceinline__ void operator()(int64_t (&at)[K], const bool (&loaded)[K],
+                                             int64_t (&idv)[K]) const {
+    bool out = false;
+#pragma unroll
+    for (int t = 0; t < K; ++t)
+      out |= loaded[t] && static_cast<uint64_t>(at[t] - w0) >= static_cast<uint64_t>(wn);
+    if (__ballot(out) == 0) {
+#pragma unroll
+      for (int t = 0; t < K; ++t) idv[t] = loaded[t] ? static_cast<int64_t>(win[at[t] - w0]) : 0;
+    } else {
+#pragma unroll
+      for (int t = 0; t < K; ++t) idv[t] = loaded[t] ? static_cast<int64_t>(ids[at[t]]) : 0;
+    }
+  }
+};
+
 // One bag, reduced by this lane's aligned group of G lanes (every lane of
 // the group calls it with the same bag; groups of a wave may hold different
 // bags).  The bag is walked in rounds of kGroupRound positions: the round's
@@ -317,6 +342,183 @@ int launch_bag_idx(const BagArgs& a, hipStream_t s) {
     return a.dim % v == 0 && a.ldo % v == 0 && aligned(a.table, 4 * v) && aligned(a.out, 4 * v);
   };
   return vec_ok(4) ? launch_bag_vec<IdxT, 4>(a, s) : launch_bag_vec<IdxT, 1>(a, s);
+}
+
+// ---------------------------------------------------------------------------
+// Segment reduction over non-decreasing segment ids in one launch, without
+// an offsets pass.  Ids are clamped to [-1, batch] (positions outside
+// [0, batch) belong to no segment) and position n is a closing sentinel of
+// id `batch`.  A position whose id differs from the one before it is a
+// boundary: the segments strictly between the two ids hold no positions and
+// get zero rows, and if its id is a segment, that segment starts there and
+// runs to the next boundary.  Workgroup w owns the boundaries at positions
+// [w*P, (w+1)*P): it lists them in LDS in position order, finds where its
+// last segment ends by reading ahead P positions past its chunk, and hands
+// its segments to its groups of G lanes, which reduce them in index order as
+// the bag kernel does.  The row ids of those 2P positions are read in the
+// same round as their segment ids and kept in LDS, so a segment that ends
+// inside them waits for one global round (its rows) after the boundaries:
+// two dependent rounds in all, against the offsets kernel plus the bag
+// kernel's three (offsets, row ids, rows).
+// ---------------------------------------------------------------------------
+// Positions per workgroup (at most kThreads): 160 keeps a chunk's segments
+// (20 positions each in configs[2]) within the 16 lane groups of a
+// workgroup, so none takes a second turn, and the grid of configs[2] within
+// one resident wave of workgroups (2 a CU).
+constexpr int kSsChunk = 160;
+
+template <typename IdxT, int G, int VEC, bool MEAN, bool BUF, int P = kSsChunk>
+__global__ __launch_bounds__(kThreads) void seg_sorted_kernel(
+    const float* __restrict__ table, int64_t rows, int64_t dim, const IdxT* __restrict__ ids,
+    const int64_t* __restrict__ seg, int64_t stride, int64_t n, int64_t batch,
+    float* __restrict__ out, int64_t ldo, int* __restrict__ status) {
+  typedef typename VecT<VEC>::type V;
+  constexpr int kWaves = kThreads / 64;
+  static_assert(P <= kThreads, "one position per thread");
+  __shared__ int32_t bpos[P];
+  __shared__ int64_t bkey[P];
+  __shared__ int64_t bprev[P];
+  __shared__ int32_t wcnt[kWaves];
+  __shared__ int32_t wend[kWaves];
+  __shared__ int32_t wgap[kWaves];
+  __shared__ IdxT win[2 * P];  // row ids of positions [p0, p0 + 2P)
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const int64_t p0 = (int64_t)blockIdx.x * P;
+  const int64_t p1 = p0 + P;
+  // Ids are loaded from a clamped, always valid position and fixed up once
+  // all loads are issued, so no load sits in a per-lane branch.
+  auto load = [&](int64_t j) -> int64_t {
+    return seg[(j < 0 ? 0 : (j >= n ? n - 1 : j)) * stride];
+  };
+  auto fix = [&](int64_t j, int64_t v) -> int64_t {
+    return j < 0 ? int64_t(-1)
+                 : (j >= n ? batch : (v < -1 ? int64_t(-1) : (v > batch ? batch : v)));
+  };
+  auto key = [&](int64_t j) { return fix(j, load(j)); };
+  // this position and the one before it, and the same a chunk ahead (no
+  // positions at all: every id is the sentinel's)
+  const int64_t i = p0 + t;
+  int64_t prev = batch, cur = batch, ahead_prev = batch, ahead = batch;
+  if (n > 0) {
+    // the row ids of the chunk and of the read-ahead come in the same round,
+    // into LDS: the segments then wait for their rows only
+    const IdxT d0 = ids[i < n ? i : n - 1], d1 = ids[p1 + t < n ? p1 + t : n - 1];
+    const int64_t v0 = load(i - 1), v1 = load(i), v2 = load(p1 + t - 1), v3 = load(p1 + t);
+    if (t < P) {
+      win[t] = d0;
+      win[P + t] = d1;
+    }
+    prev = fix(i - 1, v0);
+    cur = fix(i, v1);
+    ahead_prev = fix(p1 + t - 1, v2);
+    ahead = fix(p1 + t, v3);
+  }
+  if (i == 0) prev = -1;
+  const bool bnd = t < P && i <= n && cur != prev;
+  const uint64_t m = __ballot(bnd);
+  const int rank = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32),
+                                             __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0));
+  const uint64_t ma = __ballot(t < P && ahead != ahead_prev);
+  const uint64_t mg = __ballot(bnd && cur > prev + 1);
+  if (lane == 0) {
+    wcnt[w] = __popcll(m);
+    wend[w] = ma ? (int)(p1 + 64 * w + __builtin_ctzll(ma)) : INT32_MAX;
+    wgap[w] = mg != 0;
+  }
+  __syncthreads();
+  int before = 0, nb = 0, any_gap = 0;
+  int32_t end_last = INT32_MAX;
+#pragma unroll
+  for (int q = 0; q < kWaves; ++q) {
+    before += q < w ? wcnt[q] : 0;
+    nb += wcnt[q];
+    any_gap |= wgap[q];
+    end_last = wend[q] < end_last ? wend[q] : end_last;
+  }
+  if (bnd) {
+    bpos[before + rank] = static_cast<int32_t>(i);
+    bkey[before + rank] = cur;
+    bprev[before + rank] = prev;
+  }
+  __syncthreads();
+  if (nb == 0) return;
+  // The last listed segment, when it is one, ends at the first boundary past
+  // the chunk: found above unless it lies beyond the read-ahead (a segment
+  // longer than the chunk), then searched for a chunk at a time.  It exists:
+  // position n closes every segment.
+  const int64_t last = bkey[nb - 1];
+  if (last >= 0 && last < batch) {
+    for (int64_t base = p1 + P; end_last == INT32_MAX; base += kThreads) {
+      const uint64_t mb = __ballot(key(base + t) != last);
+      __syncthreads();
+      if (lane == 0) wend[w] = mb ? (int)(base + 64 * w + __builtin_ctzll(mb)) : INT32_MAX;
+      __syncthreads();
+#pragma unroll
+      for (int q = 0; q < kWaves; ++q) end_last = wend[q] < end_last ? wend[q] : end_last;
+    }
+  }
+  // zero rows for the segments that no position names
+  if (any_gap) {
+    const int64_t dv = dim / VEC;
+    for (int k = 0; k < nb; ++k) {
+      const int64_t lo = bprev[k] + 1, hi = bkey[k] < batch ? bkey[k] : batch;
+      for (int64_t e = t; e < (hi - lo) * dv; e += kThreads) {
+        const int64_t r = lo + e / dv;
+        store_row<VEC>(out + r * ldo + (e % dv) * VEC, V(0.0f));
+      }
+    }
+  }
+  bool bad = false;
+  const int64_t wn = n - p0 < 2 * P ? n - p0 : 2 * P;
+  for (int k = t / G; k < nb; k += kThreads / G) {
+    const int64_t sk = bkey[k];
+    if (sk < 0 || sk >= batch) continue;
+    const int64_t beg = bpos[k], end = k + 1 < nb ? bpos[k + 1] : end_last;
+    bad |= bag_group<G, VEC, MEAN, BUF>(table, rows, dim, beg, end,
+                                        WindowIds<IdxT>{ids, win, p0, wn}, out + sk * ldo);
+  }
+  if (bad) atomicOr(status, 1);
+}
+
+template <typename IdxT, int G, int VEC>
+int launch_seg_sorted_g(const BagArgs& a, const int64_t* seg, int64_t stride, int64_t n,
+                        hipStream_t s) {
+  const IdxT* ids = static_cast<const IdxT*>(a.ids);
+  const bool mean = a.combiner == ANNC_COMBINER_MEAN;
+  const bool buf = a.rows * a.dim * static_cast<int64_t>(sizeof(float)) < (int64_t(1) << 31);
+  auto pick = [&](auto buf_tag) {
+    constexpr bool B = decltype(buf_tag)::value;
+    return mean ? seg_sorted_kernel<IdxT, G, VEC, true, B> : seg_sorted_kernel<IdxT, G, VEC, false, B>;
+  };
+  auto kernel = buf ? pick(std::true_type{}) : pick(std::false_type{});
+  // one workgroup per kSsChunk positions, position n (the sentinel) included
+  const dim3 grid((unsigned)(n / kSsChunk + 1));
+  hipLaunchKernelGGL(kernel, grid, dim3(kThreads), 0, s, a.table, a.rows, a.dim, ids, seg, stride,
+                     n, a.num_bags, a.out, a.ldo, a.status);
+  ANNC_HIP_TRY(hipGetLastError());
+  return ANNC_OK;
+}
+
+template <typename IdxT, int VEC>
+int launch_seg_sorted_vec(const BagArgs& a, const int64_t* seg, int64_t stride, int64_t n,
+                          hipStream_t s) {
+  const int64_t lanes = ceil_div(a.dim, VEC);
+  if (lanes <= 4) return launch_seg_sorted_g<IdxT, 4, VEC>(a, seg, stride, n, s);
+  if (lanes <= 8) return launch_seg_sorted_g<IdxT, 8, VEC>(a, seg, stride, n, s);
+  if (lanes <= 16) return launch_seg_sorted_g<IdxT, 16, VEC>(a, seg, stride, n, s);
+  if (lanes <= 32) return launch_seg_sorted_g<IdxT, 32, VEC>(a, seg, stride, n, s);
+  return launch_seg_sorted_g<IdxT, 64, VEC>(a, seg, stride, n, s);
+}
+
+template <typename IdxT>
+int launch_seg_sorted(const BagArgs& a, const int64_t* seg, int64_t stride, int64_t n,
+                      hipStream_t s) {
+  auto aligned = [](const void* p, int bytes) {
+    return (reinterpret_cast<uintptr_t>(p) & (bytes - 1)) == 0;
+  };
+  const bool v4 = a.dim % 4 == 0 && a.ldo % 4 == 0 && aligned(a.table, 16) && aligned(a.out, 16);
+  return v4 ? launch_seg_sorted_vec<IdxT, 4>(a, seg, stride, n, s)
+            : launch_seg_sorted_vec<IdxT, 1>(a, seg, stride, n, s);
 }
 
 // ---------------------------------------------------------------------------
@@ -1561,13 +1763,12 @@ size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 }  // namespace
 
 int segment_reduce_plan(int64_t n, int64_t batch, int sorted_hint, hipStream_t s, SegPlan* plan) {
-  ANNC_REQUIRE(n < (1ll << 31), "too many indices");
+  ANNC_REQUIRE(n < (1ll << 31) - 1, "too many indices");
   ANNC_REQUIRE(batch < (1ll << 32), "too many segments");
   *plan = SegPlan{};
   const size_t off_bytes = align256(sizeof(int64_t) * (size_t)(batch + 1));
   if (sorted_hint == 1) {
-    plan->path = SegPlan::kSorted;
-    plan->bytes = off_bytes;
+    plan->path = SegPlan::kSorted;  // no workspace
     return ANNC_OK;
   }
   const int64_t tblk = std::max<int64_t>(1, ceil_div(n, kTlBlock));
@@ -1626,13 +1827,11 @@ int segment_reduce_run(hipStream_t s, const float* data, int64_t rows, int64_t d
   const size_t off_bytes = align256(sizeof(int64_t) * (size_t)(batch + 1));
 
   if (plan.path == SegPlan::kSorted) {
-    int64_t* offsets = reinterpret_cast<int64_t*>(ws);
-    hipLaunchKernelGGL(seg_bounds_kernel<int64_t>, dim3((unsigned)ceil_div(n + 1, kThreads)),
-                       dim3(kThreads), 0, s, seg, stride, n, batch, offsets);
-    ANNC_HIP_TRY(hipGetLastError());
-    a.offsets = offsets;
-    a.perm = nullptr;
-    return launch_bag(a, s);
+    // one launch: segment boundaries found in LDS, no offsets array
+    ANNC_REQUIRE(rows < static_cast<int64_t>(kNoRow), "tables of 2^32-1 rows or more are not supported");
+    ANNC_REQUIRE(dim < (int64_t(1) << 29), "embedding dim must be below 2^29");
+    return indices_is_64 ? launch_seg_sorted<int64_t>(a, seg, stride, n, s)
+                         : launch_seg_sorted<int32_t>(a, seg, stride, n, s);
   }
 
   if (plan.path == SegPlan::kTwoLevel) {
@@ -1793,8 +1992,8 @@ int segment_reduce(hipStream_t s, const float* data, int64_t rows, int64_t dim,
   SegPlan plan;
   int rc = segment_reduce_plan(n, batch, sorted_hint, s, &plan);
   if (rc != ANNC_OK) return rc;
-  void* ws = stream_workspace(s, plan.bytes);
-  if (!ws) return set_error(ANNC_RESOURCE_EXHAUSTED, "workspace allocation failed");
+  void* ws = plan.bytes ? stream_workspace(s, plan.bytes) : nullptr;
+  if (plan.bytes && !ws) return set_error(ANNC_RESOURCE_EXHAUSTED, "workspace allocation failed");
   return segment_reduce_run(s, data, rows, dim, indices, indices_is_64, seg, stride, n, combiner,
                             batch, out, plan, ws, status);
 }

@@ -149,7 +149,8 @@ def segment_reduce(data: torch.Tensor, indices: torch.Tensor, segment_ids: torch
     sorted_ids=True promises non-decreasing segment ids (skips the sort)."""
     _require_cuda(data, indices, segment_ids)
     rows, dim = data.shape
-    seg_stride = segment_ids.stride(0) if segment_ids.dim() == 1 else segment_ids.stride(0)
+    # (torch may give an empty or one-element view any stride, 0 included)
+    seg_stride = max(segment_ids.stride(0), 1)
     out = torch.empty((batch, dim), dtype=torch.float32, device=data.device)
     check(_lib.lib().annc_hip_segment_reduce(stream_ptr(stream), ptr(data.contiguous()), rows, dim,
                                              ptr(indices), 1 if indices.dtype == torch.int64 else 0,

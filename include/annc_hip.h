@@ -232,7 +232,7 @@ int annc_hip_segment_reduce(void* stream, const float* data, int64_t rows, int64
  * It calls no hipMalloc/hipFree: its workspace is a 16 MiB device array of
  * the library, one per GPU, held until the process ends.  Inputs that need
  * more workspace than that are rejected with ANNC_INVALID_ARGUMENT (sorted
- * ids: up to about 2 M segments; any order: the stable counting sort needs
+ * ids need none; any order: the stable counting sort needs
  * 8 * ceil(n/1024) * batch + 4 * n bytes and more, up to 16384 segments; the
  * radix sort beyond that about 16 * n bytes).  Every call on a GPU uses that
  * GPU's one array, so calls that overlap on one GPU (two streams, two

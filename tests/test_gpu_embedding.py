@@ -171,6 +171,83 @@ def test_device_segment_reduce_orders(what, batch, n, combiner):
         np.testing.assert_array_equal(to_host(out), ref)
 
 
+SORTED_CHUNK = 160  # positions per workgroup of the sorted-id kernel
+
+
+def _sorted_segments(what, g):
+    """Non-decreasing segment ids for the sorted-id path, and the batch.
+    The path cuts positions into chunks of SORTED_CHUNK (plus the closing
+    position n) and reads one chunk ahead: the cases put boundaries on and
+    around chunk edges, segments longer than the read-ahead, and runs of
+    empty segments."""
+    c = SORTED_CHUNK
+    if what == "no positions":
+        return np.zeros(0, np.int64), 5
+    if what == "one position":
+        return np.array([2], np.int64), 3
+    sizes = {"n = chunk - 1": c - 1, "n = chunk": c, "n = chunk + 1": c + 1,
+             "n = 2 * chunk - 1": 2 * c - 1, "n = 2 * chunk": 2 * c}
+    if what in sizes:
+        return np.sort(g.integers(0, 50, size=sizes[what])), 50
+    if what == "empty segments at both ends":
+        return np.sort(g.integers(10, 90, size=3000)), 100
+    if what == "one segment over 30 chunks":
+        return np.repeat(np.array([0, 1, 2, 4]), [3, 5000, 1, 700]), 6
+    if what == "segments of one chunk, on chunk edges":
+        return np.repeat(np.arange(40), c), 40
+    if what == "segments of two chunks, on chunk edges":
+        return np.repeat(np.arange(20), 2 * c), 21
+    if what == "segments of a chunk -1 and +1 positions":
+        return np.repeat(np.arange(30), np.tile([c - 1, c + 1], 15)), 30
+    if what == "mostly empty segments":
+        return np.sort(g.choice(100000, size=300, replace=False)), 100000
+    if what == "ids outside [0, batch) at both ends":
+        seg = np.concatenate([g.integers(-10, 1010, size=20000), [-2**40, -2, 2**40, 1000]])
+        return np.sort(seg), 1000
+    if what == "every id outside [0, batch)":
+        return np.full(700, -5, np.int64), 10
+    if what == "configs[2] shape":
+        return np.sort(g.integers(0, 4096, size=81857)), 4096
+    raise AssertionError(what)
+
+
+SORTED_CASES = ["no positions", "one position", "n = chunk - 1", "n = chunk", "n = chunk + 1",
+                "n = 2 * chunk - 1", "n = 2 * chunk", "empty segments at both ends",
+                "one segment over 30 chunks", "segments of one chunk, on chunk edges",
+                "segments of two chunks, on chunk edges",
+                "segments of a chunk -1 and +1 positions", "mostly empty segments",
+                "ids outside [0, batch) at both ends", "every id outside [0, batch)",
+                "configs[2] shape"]
+
+
+@pytest.mark.parametrize("what", SORTED_CASES)
+@pytest.mark.parametrize("dim,idx64", [(16, True), (6, False), (300, True), (64, False)])
+def test_device_segment_reduce_sorted_ids(what, dim, idx64):
+    """The caller's promise of non-decreasing segment ids takes the one-launch
+    path (segment boundaries found per chunk of positions, no offsets array):
+    bit-exact against the sequential loop, both combiners, with the ids read
+    in place from a column of a [n, 3] slice (stride 3) as the TF op passes
+    them; dim 6 takes the scalar lane groups, 300 two column chunks."""
+    note(f"device segment reduce sorted ids: {what} (dim {dim}, idx64 {idx64})")
+    g = workloads.rng(len(what) * 131 + dim)
+    seg, batch = _sorted_segments(what, g)
+    seg = seg.astype(np.int64)
+    n = seg.size
+    assert (np.diff(seg) >= 0).all()
+    rows = 900
+    data = g.standard_normal((rows, dim)).astype(np.float32)
+    idx = g.integers(0, rows, size=n).astype(np.int64 if idx64 else np.int32)
+    keep = (seg >= 0) & (seg < batch)
+    slice3 = np.stack([np.zeros(n, np.int64), seg, -seg], axis=1)
+    seg_col = to_dev(slice3)[:, 1]
+    assert n < 2 or seg_col.stride(0) == 3
+    for combiner in (0, 1):
+        out = dev.segment_reduce(to_dev(data), to_dev(idx), seg_col, batch, combiner,
+                                 sorted_ids=True)
+        ref = ora.segment_reduce(data, idx[keep], seg[keep], batch, combiner)
+        np.testing.assert_array_equal(to_host(out), ref)
+
+
 @pytest.mark.parametrize("dim", [4, 6, 12, 16, 32, 64, 128, 256, 300])
 @pytest.mark.parametrize("idx64", [True, False])
 def test_device_segment_reduce_any_order_dims(dim, idx64):
