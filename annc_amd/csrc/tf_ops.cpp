@@ -382,7 +382,9 @@ int annc_kp_fused_gather(const float* data, int data_rank, const int64_t* data_d
   ANNC_REQUIRE(slice_input && (data || rows * dim == 0), "null operand");
   hipStream_t s = lib_stream();
   if (!s) return set_error(ANNC_INTERNAL, "no HIP stream");
-  (void)annc_hip_stream_status(s);  // start from a clear status word
+  int* status = stream_status(s);
+  if (!status) return set_error(ANNC_RESOURCE_EXHAUSTED, "status allocation failed");
+  ANNC_HIP_TRY(hipMemsetAsync(status, 0, sizeof(int), s));  // start from a clear status word
   Staging st(s);
   const float* d_data =
       static_cast<const float*>(st.in(data, sizeof(float) * (size_t)(rows * dim > 0 ? rows * dim : 1)));
@@ -396,18 +398,24 @@ int annc_kp_fused_gather(const float* data, int data_rank, const int64_t* data_d
   rc = unique_gather(s, d_data, rows, dim, d_keys + col, slice_dims[1], n, d_nu, d_uniq, d_idx,
                      d_out);
   if (rc != ANNC_OK) return rc;
-  if (annc_hip_stream_status(s) != ANNC_OK)  // synchronises
-    return set_error(ANNC_INTERNAL, "idx out of table range");
+  // the status word and the unique count in one synchronisation
+  int bad = 0;
   int64_t u = 0;
-  rc = read_back(s, {{&u, d_nu, sizeof(u)}});
+  rc = read_back(s, {{&bad, status, sizeof(int)}, {&u, d_nu, sizeof(u)}});
   if (rc != ANNC_OK) return rc;
+  if (bad) {
+    ANNC_HIP_TRY(hipMemset(status, 0, sizeof(int)));
+    return set_error(ANNC_INTERNAL, "idx out of table range");
+  }
   *num_unique = u;
+  // the outputs are sized by u: copied once it is known, then one wait
   if (out_unique)
-    ANNC_HIP_TRY(hipMemcpy(out_unique, d_uniq, sizeof(int64_t) * (size_t)u, hipMemcpyDefault));
+    ANNC_HIP_TRY(hipMemcpyAsync(out_unique, d_uniq, sizeof(int64_t) * (size_t)u, hipMemcpyDefault, s));
   if (out_indices)
-    ANNC_HIP_TRY(hipMemcpy(out_indices, d_idx, sizeof(int32_t) * (size_t)n, hipMemcpyDefault));
+    ANNC_HIP_TRY(hipMemcpyAsync(out_indices, d_idx, sizeof(int32_t) * (size_t)n, hipMemcpyDefault, s));
   if (out_data && u * dim > 0)
-    ANNC_HIP_TRY(hipMemcpy(out_data, d_out, sizeof(float) * (size_t)(u * dim), hipMemcpyDefault));
+    ANNC_HIP_TRY(hipMemcpyAsync(out_data, d_out, sizeof(float) * (size_t)(u * dim), hipMemcpyDefault, s));
+  ANNC_HIP_TRY(hipStreamSynchronize(s));
   return set_error(ANNC_OK, "");
 }
 

@@ -186,7 +186,7 @@ def unique_gather(table: torch.Tensor, keys: torch.Tensor, col: int = 0, stream=
         raise ValueError("col outside the key columns")
     rows, dim = table.shape
     n = k2.shape[0]
-    nu = torch.zeros(1, dtype=torch.int64, device=table.device)
+    nu = torch.empty(1, dtype=torch.int64, device=table.device)  # always written
     uniq = torch.empty(max(n, 1), dtype=torch.int64, device=table.device)
     idx = torch.empty(n, dtype=torch.int32, device=table.device)
     out = torch.empty((max(n, 1), dim), dtype=torch.float32, device=table.device)

@@ -38,7 +38,7 @@ def _empty_like_kind(ref, shape, np_dtype):
     if _is_torch(ref):
         import torch
 
-        tdt = {np.float32: torch.float32, np.int32: torch.int32}[np_dtype]
+        tdt = {np.float32: torch.float32, np.int32: torch.int32, np.int64: torch.int64}[np_dtype]
         return torch.empty(shape, dtype=tdt, device=ref.device)
     return np.empty(shape, dtype=np_dtype)
 
@@ -127,7 +127,8 @@ def kp_fused_gather(data, slice_input, begin):
     annc/tensorflow/kernels/embedding_fused_gather.cc:26-85).
 
     Returns (out_shape int64[U]: the distinct keys of column begin[1] in order
-    of first occurrence, out_indices int32[N], out_data float32[U, D]).
+    of first occurrence, out_indices int32[N], out_data float32[U, D]), as
+    host arrays for a host table and device tensors for a device one.
     Errors raise AnncError (code 13, errors::Internal) with the reference text.
     """
     lib = _lib.lib()
@@ -141,13 +142,14 @@ def kp_fused_gather(data, slice_input, begin):
             ptr(sdims), ptr(begin_h), begin_h.size, ptr(nu))
     n = int(sdims[0]) if sdims.size else 0
     dim = int(ddims[1]) if ddims.size == 2 else 0
-    # outputs sized for every key being distinct, trimmed to U afterwards
-    uniq = np.empty(max(n, 1), dtype=np.int64)
+    # outputs sized for every key being distinct, trimmed to U afterwards;
+    # device tables give device outputs (no copy through pageable memory)
+    uniq = _empty_like_kind(data, (max(n, 1),), np.int64)
     idx = _empty_like_kind(data, (n,), np.int32)
     out = _empty_like_kind(data, (max(n, 1), dim), np.float32)
     check(lib.annc_kp_fused_gather(*args, ptr(uniq), ptr(idx), ptr(out)))
     u = int(nu[0])
-    return uniq[:u].copy(), idx, out[:u]
+    return (uniq[:u].copy() if isinstance(uniq, np.ndarray) else uniq[:u]), idx, out[:u]
 
 
 def kp_fused_batch_matmul_add_sigmoid(lhs, rhs, bias):
