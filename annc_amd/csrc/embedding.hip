@@ -2116,11 +2116,19 @@ int nonzero_compact(hipStream_t s, const float* dense, int64_t count, int64_t di
   hipLaunchKernelGGL(nz_flag_kernel, grid, dim3(kThreads), 0, s, dense, count, flags);
   ANNC_HIP_TRY(hipGetLastError());
   ANNC_HIP_TRY(hipcub::DeviceScan::InclusiveSum(tmp, tmp_bytes, flags, incl, (int)count, s));
-  if (out_idx) {
-    hipLaunchKernelGGL(nz_write_kernel, grid, dim3(kThreads), 0, s, dense, count, dim, seg_of_row,
-                       one_d, flags, incl, cap, out_idx, out_val);
-    ANNC_HIP_TRY(hipGetLastError());
-  }
+  if (out_idx) return nonzero_write(s, dense, count, dim, seg_of_row, one_d, flags, incl, cap,
+                                    out_idx, out_val);
+  return ANNC_OK;
+}
+
+int nonzero_write(hipStream_t s, const float* dense, int64_t count, int64_t dim,
+                  const int64_t* seg_of_row, int one_d, const int32_t* flags, const int32_t* incl,
+                  int64_t cap, int32_t* out_idx, float* out_val) {
+  if (count <= 0 || cap <= 0) return ANNC_OK;
+  const dim3 grid((unsigned)ceil_div(count, kThreads));
+  hipLaunchKernelGGL(nz_write_kernel, grid, dim3(kThreads), 0, s, dense, count, dim, seg_of_row,
+                     one_d, flags, incl, cap, out_idx, out_val);
+  ANNC_HIP_TRY(hipGetLastError());
   return ANNC_OK;
 }
 

@@ -76,6 +76,10 @@ size_t nonzero_scan_temp_bytes(int64_t count);
 int nonzero_compact(hipStream_t s, const float* dense, int64_t count, int64_t dim,
                     const int64_t* seg_of_row, int one_d, int32_t* flags, int32_t* incl, void* tmp,
                     size_t tmp_bytes, int64_t cap, int32_t* out_idx, float* out_val);
+// The write step of nonzero_compact alone, over flags and incl it computed.
+int nonzero_write(hipStream_t s, const float* dense, int64_t count, int64_t dim,
+                  const int64_t* seg_of_row, int one_d, const int32_t* flags, const int32_t* incl,
+                  int64_t cap, int32_t* out_idx, float* out_val);
 
 int launch_sparse_embedding2(hipStream_t s, const float* table, int64_t rows, int64_t dim,
                              const void* ids, int ids_is_64, int64_t n, int64_t fallback,

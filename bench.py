@@ -561,7 +561,7 @@ def bench_nonzero(device, inp: Inputs):
     """KPFusedSparseSegmentReduceNonzero on configs[2] in TF form (positions
     shuffled, segment ids in column 1 of slice_input), device tensors, mean:
     median wall time of the two-phase op (phase 1 counts the nonzeros and
-    reads the count back; phase 2 runs the pipeline again and writes them),
+    reads the count back; phase 2 writes the values phase 1 kept),
     and of phase 1 alone."""
     import ctypes
     import numpy as np
@@ -600,7 +600,7 @@ def bench_nonzero(device, inp: Inputs):
                         f"{int(vals.numel())} nonzero values listed",
             "two_phase_wall_us_median": round(statistics.median(ts) * 1e6, 1),
             "phase1_wall_us_median": round(statistics.median(t1) * 1e6, 1),
-            "note": "each phase synchronises (count read-back); phase 2 reruns the reduction"}
+            "note": "each phase synchronises; phase 2 writes the values phase 1 kept"}
 
 
 def bench_config5(device, inp: Inputs, steps: int):

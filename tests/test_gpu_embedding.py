@@ -434,13 +434,29 @@ def test_tf_segment_reduce_nonzero_order_sensitive(case):
         np.testing.assert_array_equal(val, want[2])
 
 
-def test_tf_segment_reduce_nonzero_short_phase2_buffer():
+def _nonzero_args(data, indices, slice_input, rows, dim, n, combiner, shape, nnz, keep):
+    """C-ABI arguments of annc_kp_fused_sparse_segment_reduce_nonzero (the
+    host shape arrays are appended to `keep` so they outlive the call)."""
+    from annc_amd import _lib
+    ddims = np.array([rows, dim], np.int64)
+    sdims = np.array([n, 2], np.int64)
+    begin = np.array([0, 1], np.int32)
+    keep += [ddims, sdims, begin]
+    return (_lib.ptr(data), 2, _lib.ptr(ddims), _lib.ptr(indices), 0, n, _lib.ptr(slice_input),
+            2, _lib.ptr(sdims), _lib.ptr(begin), 2, combiner, _lib.ptr(shape), _lib.ptr(nnz))
+
+
+@pytest.mark.parametrize("reuse", [True, False])
+def test_tf_segment_reduce_nonzero_short_phase2_buffer(reuse):
     """A phase-2 call whose buffers hold one value fewer than phase 1
     counted is refused with the count mismatch, and writes nothing past the
-    buffers it was given (a guard word after them keeps its value)."""
+    buffers it was given (a guard word after them keeps its value): both when
+    phase 2 takes phase 1's kept results (reuse) and when a phase 1 on other
+    operands came in between, so phase 2 recomputes and its write kernel
+    must stop at the buffer's end itself."""
     import ctypes
     from annc_amd import _lib
-    note("KPFusedSparseSegmentReduceNonzero short phase-2 buffer")
+    note(f"KPFusedSparseSegmentReduceNonzero short phase-2 buffer (reuse={reuse})")
     g = workloads.rng(35)
     n, rows, dim = 500, 50, 4
     data = to_dev(g.standard_normal((rows, dim)).astype(np.float32))
@@ -458,6 +474,11 @@ def test_tf_segment_reduce_nonzero_short_phase2_buffer():
     _lib.check(lib.annc_kp_fused_sparse_segment_reduce_nonzero(*args, None, None))
     count = int(nnz[0])
     assert count > 1
+    if not reuse:  # phase 1 of other operands (the other combiner) in between
+        keep, nnz2, shape2 = [], np.zeros(1, np.int64), np.zeros(2, np.int32)
+        _lib.check(lib.annc_kp_fused_sparse_segment_reduce_nonzero(
+            *_nonzero_args(data, indices, slice_input, rows, dim, n, 1, shape2, nnz2, keep),
+            None, None))
     short = count - 1
     guard = np.float32(123.5)
     out_idx = torch.full((short * 2 + 64,), -5, dtype=torch.int32, device=device())
@@ -470,6 +491,47 @@ def test_tf_segment_reduce_nonzero_short_phase2_buffer():
     torch.cuda.synchronize()
     assert (to_host(out_idx)[short * 2:] == -5).all()
     assert (to_host(out_val)[short:] == guard).all()
+
+
+def test_tf_segment_reduce_nonzero_phase2_after_other_operands():
+    """Phase 1 on A, phase 1 on B, phase 2 on A: the results kept from B's
+    phase 1 must not be written for A, so A's phase 2 recomputes and
+    matches the oracle; then phase 1 and 2 on B reuse B's results."""
+    from annc_amd import _lib
+    note("KPFusedSparseSegmentReduceNonzero phase 2 after other operands")
+    g = workloads.rng(36)
+    n, rows, dim = 3000, 200, 8
+    lib = _lib.lib()
+    cases = []
+    for seg_hi in (300, 40):
+        data = g.standard_normal((rows, dim)).astype(np.float32)
+        data[g.random((rows, dim)) < 0.3] = 0.0
+        idx = g.integers(0, rows, size=n).astype(np.int32)
+        seg = g.integers(0, seg_hi, size=n).astype(np.int64)
+        sl = np.stack([np.zeros(n, np.int64), seg], axis=1)
+        cases.append((data, idx, seg, to_dev(data), to_dev(idx), to_dev(sl)))
+    keep, counts = [], []
+    shape, nnz = np.zeros(2, np.int32), np.zeros(1, np.int64)
+    for data, idx, seg, dd, di, ds in cases:  # phase 1 on A, then on B
+        _lib.check(lib.annc_kp_fused_sparse_segment_reduce_nonzero(
+            *_nonzero_args(dd, di, ds, rows, dim, n, 0, shape, nnz, keep), None, None))
+        counts.append(int(nnz[0]))
+    for k in (0, 1, 1):  # phase 2 on A (recomputed), phase 2 on B (reused), B again
+        data, idx, seg, dd, di, ds = cases[k]
+        if k == 1:
+            _lib.check(lib.annc_kp_fused_sparse_segment_reduce_nonzero(
+                *_nonzero_args(dd, di, ds, rows, dim, n, 0, shape, nnz, keep), None, None))
+        want = ora.segment_reduce_nonzero(data, idx, seg, 0)
+        out_idx = torch.full((counts[k], 2), -1, dtype=torch.int32, device=device())
+        out_val = torch.full((counts[k],), -1.0, dtype=torch.float32, device=device())
+        nnz[0] = counts[k]
+        _lib.check(lib.annc_kp_fused_sparse_segment_reduce_nonzero(
+            *_nonzero_args(dd, di, ds, rows, dim, n, 0, shape, nnz, keep),
+            _lib.ptr(out_idx), _lib.ptr(out_val)))
+        assert int(nnz[0]) == counts[k] == want[1].shape[0]
+        np.testing.assert_array_equal(shape, want[0])
+        np.testing.assert_array_equal(to_host(out_idx), want[1])
+        np.testing.assert_array_equal(to_host(out_val), want[2])
 
 
 def test_tf_segment_reduce_nonzero_index_out_of_range():
