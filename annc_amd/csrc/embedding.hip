@@ -422,7 +422,9 @@ __global__ __launch_bounds__(kThreads) void seg_sorted_kernel(
   const uint64_t mg = __ballot(bnd && cur > prev + 1);
   if (lane == 0) {
     wcnt[w] = __popcll(m);
-    wend[w] = ma ? (int)(p1 + 64 * w + __builtin_ctzll(ma)) : INT32_MAX;
+    // (a segment's end is at most n: candidates are clamped there, so the
+    // int never wraps)
+    wend[w] = ma ? (int)min(p1 + 64 * w + __builtin_ctzll(ma), n) : INT32_MAX;
     wgap[w] = mg != 0;
   }
   __syncthreads();
@@ -451,7 +453,7 @@ __global__ __launch_bounds__(kThreads) void seg_sorted_kernel(
     for (int64_t base = p1 + P; end_last == INT32_MAX; base += kThreads) {
       const uint64_t mb = __ballot(key(base + t) != last);
       __syncthreads();
-      if (lane == 0) wend[w] = mb ? (int)(base + 64 * w + __builtin_ctzll(mb)) : INT32_MAX;
+      if (lane == 0) wend[w] = mb ? (int)min(base + 64 * w + __builtin_ctzll(mb), n) : INT32_MAX;
       __syncthreads();
 #pragma unroll
       for (int q = 0; q < kWaves; ++q) end_last = wend[q] < end_last ? wend[q] : end_last;
