@@ -267,6 +267,41 @@ def test_device_segment_reduce_any_order_dims(dim, idx64):
                                                                        combiner))
 
 
+@pytest.mark.parametrize("seed", range(24))
+def test_device_segment_reduce_random_configurations(seed):
+    """Seeded random configurations across both paths (sorted promise or
+    not): dims of every lane-group width and the scalar path, int32 and
+    int64 indices, Poisson or heavy-tailed segment lengths with empty
+    segments, ids outside [0, batch), both combiners; bit-exact against the
+    sequential loop."""
+    g = np.random.default_rng(1000 + seed)
+    dim = int(g.choice([1, 3, 4, 8, 12, 16, 20, 32, 64, 100, 128, 256, 260]))
+    rows = int(g.integers(50, 3000))
+    batch = int(g.choice([1, 7, 100, 1000, 5000]))
+    lens = (g.poisson(g.choice([0.5, 3, 20]), size=batch) if seed % 3 else
+            np.minimum(g.zipf(1.5, size=batch), 3000))
+    seg = np.repeat(np.arange(batch, dtype=np.int64), lens)
+    n = seg.size
+    bad = g.random(n) < (0.05 if seed % 4 == 0 else 0.0)
+    seg[bad] = g.choice([-3, -1, batch, batch + 9], size=int(bad.sum()))
+    sorted_ids = bool(seed % 2)
+    if sorted_ids:
+        seg = np.sort(seg)
+    else:
+        seg = seg[g.permutation(n)]
+    idx64 = bool(seed % 5 < 3)
+    idx = g.integers(0, rows, size=n).astype(np.int64 if idx64 else np.int32)
+    data = g.standard_normal((rows, dim)).astype(np.float32)
+    keep = (seg >= 0) & (seg < batch)
+    note(f"segment reduce random config seed={seed}: dim {dim} batch {batch} n {n} "
+         f"sorted {sorted_ids} idx64 {idx64}")
+    for combiner in (0, 1):
+        out = dev.segment_reduce(to_dev(data), to_dev(idx), to_dev(seg), batch, combiner,
+                                 sorted_ids=sorted_ids)
+        np.testing.assert_array_equal(
+            to_host(out), ora.segment_reduce(data, idx[keep], seg[keep], batch, combiner))
+
+
 def test_device_segment_reduce_unsorted():
     note("device segment reduce")
     g = workloads.rng(8)
