@@ -494,8 +494,11 @@ __device__ __forceinline__ uint32_t row_offset_of(int q, uint32_t off0, uint32_t
   return q < 64 ? a : b;
 }
 
+// Five waves a SIMD: the kernel needs 97 VGPRs unconstrained (four waves);
+// at 96 it keeps every value in registers (a few scalars move to VGPR
+// lanes) and configs[3] runs 16.75 against 16.91 us.
 template <bool MEAN>
-__global__ __launch_bounds__(kThreads) void hashed_bags_pipe_kernel(
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(5))) void hashed_bags_pipe_kernel(
     FieldSet fs, int64_t field0, int64_t batch, int64_t dim, int64_t runs_per_field,
     int64_t total_runs, int64_t runs_per_wave, const int64_t* __restrict__ ids,
     const int64_t* __restrict__ offsets, float* __restrict__ out, int64_t ldo,
