@@ -675,6 +675,18 @@ def test_embedding_bag_table_over_2gib(combiner):
     ref = ora.embedding_bag(_formula_rows_host(uniq, dim), inv.astype(np.int64), offsets, combiner)
     got = to_host(dev.embedding_bag(table, to_dev(ids), to_dev(offsets), combiner))
     np.testing.assert_array_equal(got, ref)
+    # the same bags as a segment reduction: sorted segment ids (one-kernel
+    # path) and shuffled positions (the sort paths), 64-bit addressing too
+    seg = np.repeat(np.arange(300, dtype=np.int64), lens)
+    got = to_host(dev.segment_reduce(table, to_dev(ids), to_dev(seg), 300, combiner,
+                                     sorted_ids=True))
+    np.testing.assert_array_equal(got, ref)
+    order = g.permutation(seg.size)  # each segment sums in its shuffled order
+    ref_shuffled = ora.segment_reduce(_formula_rows_host(uniq, dim), inv[order].astype(np.int64),
+                                      seg[order], 300, combiner)
+    got = to_host(dev.segment_reduce(table, to_dev(ids[order]), to_dev(seg[order]), 300,
+                                     combiner))
+    np.testing.assert_array_equal(got, ref_shuffled)
     del table
     torch.cuda.empty_cache()
 
