@@ -731,3 +731,53 @@ def test_random_row_probe_reads_what_it_counts(dim):
     np.testing.assert_array_equal(to_host(out), np.full(3 * 256, 96.0, np.float32))
     with pytest.raises(Exception, match="multiple of 8"):
         dev.probe_random_rows(table, 3, 12, out)
+
+
+def test_tf_ops_from_concurrent_threads():
+    """KPFusedSparseSegmentReduceNonzero (two phases), KPFusedGather and
+    KPFusedSparseSegmentReduce called from 4 threads at once, each on its own
+    inputs: the library stream, pinned read-back buffer and kept phase-1
+    results are per thread, so every thread gets its own oracle result."""
+    import threading
+    note("TF ops from 4 threads")
+    cases = []
+    for t in range(4):
+        g = workloads.rng(900 + t)
+        rows, dim, n = 500 + 100 * t, 8 + 4 * t, 3000 + 700 * t
+        data = g.standard_normal((rows, dim)).astype(np.float32)
+        data[g.random((rows, dim)) < 0.2] = 0.0
+        idx = g.integers(0, rows, size=n).astype(np.int64)
+        seg = g.integers(0, 200 + 50 * t, size=n).astype(np.int64)
+        sl = np.stack([np.zeros(n, np.int64), seg], axis=1)
+        cases.append((data, idx, seg, sl))
+    errors = []
+
+    def work(c):
+        data, idx, seg, sl = c
+        try:
+            want = ora.segment_reduce_nonzero(data, idx, seg, 1)
+            want_u, want_i, want_r = ora.fused_gather(data, sl, 1)
+            batch = int(seg.max()) + 1
+            want_sr = ora.segment_reduce(data, idx, seg, batch, 0)
+            for _ in range(3):
+                shape, oi, ov = tf_ops.kp_fused_sparse_segment_reduce_nonzero(
+                    data, idx, sl, np.array([0, 1], np.int32), 1)
+                np.testing.assert_array_equal(shape, want[0])
+                np.testing.assert_array_equal(oi, want[1])
+                np.testing.assert_array_equal(ov, want[2])
+                u, gi, gr = tf_ops.kp_fused_gather(data, sl, np.array([0, 1], np.int32))
+                np.testing.assert_array_equal(u, want_u)
+                np.testing.assert_array_equal(gi, want_i)
+                np.testing.assert_array_equal(gr, want_r)
+                out, so = tf_ops.kp_fused_sparse_segment_reduce(
+                    data, idx, sl, np.array([0, 1], np.int32), np.array([0], np.int32), 0)
+                np.testing.assert_array_equal(out, want_sr)
+        except Exception as e:  # reported by the main thread
+            errors.append(e)
+
+    threads = [threading.Thread(target=work, args=(c,)) for c in cases]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert not errors, errors
