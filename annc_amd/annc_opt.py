@@ -1,5 +1,6 @@
 """annc-opt: the offline model rewriter: the `layout_matmul` pass and the
-hash-bucket embedding passes `embed_hash_bucket` / `lookup_embedding_hash`.
+hash-bucket embedding passes `embed_hash_bucket` / `lookup_embedding_hash` /
+`dnn_sparse` / `dnn_hash_bucket` / `linear_sparse`.
 
 Command line, as python/annc/main.py:14-68 (`annc-opt -I <in> -O <out> passes...`):
 
@@ -41,9 +42,17 @@ SparseFillEmptyRows / Unique / gather / SparseSegmentSum-or-Mean chain, about
 45 nodes) by one KPFusedEmbeddingWithHashBucket node with inputs (the string
 tensor, the embedding weight) and attrs num_buckets, combiner (0 sum, 1 mean)
 and T_weight.  `lookup_embedding_hash` emits KPLookupEmbeddingByHash for the
-same subgraph.  The other pattern passes of the reference (dnn_sparse,
-dnn_hash_bucket, embed, linear_sparse, softmax) emit ops outside this
-library and are refused.
+same subgraph.
+
+`dnn_sparse` and `linear_sparse` (rec_embedding.py:6-86, 794-891) replace a
+hash-bucket column's sparse-id subgraph (ExpandDims ... SparseFillEmptyRows,
+20 to 26 nodes) by one KPFusedSparseEmbedding (the strings in; the
+SparseFillEmptyRows' indices, values and empty-row indicator and the dense
+shape out).  `dnn_hash_bucket` (rec_embedding.py:88-211) replaces the column
+through its SparseSegmentMean and reshapes (43 nodes) by one
+KPFusedDnnEmbeddingWithHashBucket (strings and embedding weight in).  The
+remaining pattern passes of the reference (embed, softmax) emit ops outside
+this library and are refused.
 
 Differences from the reference, each deliberate:
   * lhs variables are not packed: the reference's "k4m4" lhs packing has no
@@ -59,10 +68,11 @@ Differences from the reference, each deliberate:
     converted: unpacked with the kn4 order (data_pack.py:24-149, restated in
     `kn4_permutation`) and re-packed into the MFMA format.
   * an embedding subgraph is fused only if nothing outside it reads a node
-    the rewrite removes; the reference removes them regardless, leaving
-    dangling inputs.  Users are taken from the graph as it stands before
-    each match, and every SparseFillEmptyRows is visited (the reference
-    walks its node list while editing it).
+    the rewrite removes (other than the outputs the fused node takes over);
+    the reference removes them regardless, leaving dangling inputs.  Users
+    are taken from the graph as it stands before each match, and every
+    anchor (SparseFillEmptyRows, or ExpandDims for the sparse passes) is
+    visited (the reference walks its node list while editing it).
 """
 from __future__ import annotations
 
@@ -72,7 +82,7 @@ import os
 import shutil
 import sys
 from dataclasses import dataclass, field
-from typing import Dict, List, Optional, Sequence
+from typing import Dict, List, Optional, Sequence, Tuple
 
 import numpy as np
 
@@ -88,7 +98,8 @@ VARIABLE_OPS = frozenset(["VarHandleOp", "VariableV2", "Variable"])
 # Pattern passes of the reference (rec_embedding.py) this build implements,
 # and the ones it does not (their fused ops are not part of this library)
 EMBEDDING_PASSES = ("embed_hash_bucket", "lookup_embedding_hash")
-UNSUPPORTED_PASSES = ("dnn_sparse", "dnn_hash_bucket", "embed", "linear_sparse", "softmax")
+SPARSE_PASSES = ("dnn_sparse", "dnn_hash_bucket", "linear_sparse")
+UNSUPPORTED_PASSES = ("embed", "softmax")
 
 
 def mfma_rhs_format() -> str:
@@ -457,8 +468,9 @@ class _GraphIndex:
         return [self.by_name.get(_input_node(i)) for i in node.inputs if not i.startswith("^")]
 
 
-def _match(index: _GraphIndex, anchor: Node, pattern) -> Optional[Dict[str, Node]]:
-    bound = {"sfer": anchor}
+def _match(index: _GraphIndex, anchor: Node, pattern,
+           anchor_var: str = "sfer") -> Optional[Dict[str, Node]]:
+    bound = {anchor_var: anchor}
     for kind, var, entries, count in pattern:
         node = bound[var]
         seq = index.operands(node) if kind == "in" else index.users[node.name]
@@ -543,6 +555,200 @@ def embedding_with_hash_bucket(model: Model, pass_name: str = "embed_hash_bucket
     return made
 
 
+# ---------------------------------------------------------------------------
+# dnn_sparse / linear_sparse -> KPFusedSparseEmbedding and dnn_hash_bucket ->
+# KPFusedDnnEmbeddingWithHashBucket (rec_embedding.py:6-211, 794-891): the
+# same step lists as above, anchored at the ExpandDims ("ed") that reads the
+# string placeholder.  Steps with a None name check the type only, as the
+# reference's unnamed checks do.
+# ---------------------------------------------------------------------------
+_DNN_FRONT = [  # rec_embedding.py:9-53 (and 91-135)
+    ("in", "ed", [("Placeholder", "ph"), ("Const", "ed_dim")], None),
+    ("out", "ed", [("NotEqual", "ne"), ("GatherNd", "gnd"), ("Shape", "sh")], 3),
+    ("out", "ne", [("Where", "wh")], 1),
+    ("out", "wh", [("GatherNd", "gnd"), ("SparseReshape", "sr")], None),
+    ("out", "gnd", [("StringToHashBucketFast", "hash")], 1),
+    ("out", "hash", [("Identity", "id")], 1),
+    ("out", "id", [("GreaterEqual", "ge"), ("GatherV2", "gv")], 2),
+    ("out", "ge", [("Where", "wh2")], 1),
+    ("out", "wh2", [("Reshape", "rs")], 1),
+    ("out", "rs", [("GatherV2", "gv1"), ("GatherV2", "gv")], 2),
+    ("out", "sh", [("Slice", "sl"), ("GatherV2", "gv3"), ("SparseReshape", "sr"),
+                   ("Cast", None)], 4),
+    ("out", "sl", [("Prod", "pr")], 1),
+    ("out", "pr", [("Pack", "pk")], 1),
+    ("out", "gv3", [("Pack", "pk")], 1),
+    ("out", "pk", [("SparseReshape", "sr")], 1),
+    ("out", "sr", [("GatherV2", "gv1"), ("Identity", "id2")], 2),
+    ("out", "id2", [("SparseFillEmptyRows", "sfer")], 1),
+    ("out", "gv", [("SparseFillEmptyRows", None)], 1),
+    ("out", "gv1", [("SparseFillEmptyRows", None)], 1),
+]
+
+_DNN_SPARSE_PATTERN = _DNN_FRONT
+
+_DNN_HASH_BUCKET_PATTERN = _DNN_FRONT + [  # rec_embedding.py:137-172
+    ("out", "sfer", [("StridedSlice", "ss"), ("Unique", "uq"), ("Reshape", "rsh")], 3),
+    ("out", "rsh", [("Tile", None)], 1),
+    ("out", "uq", [("GatherV2", "gv4"), ("SparseSegmentMean", "ssm")], 2),
+    ("out", "gv4", [("Identity", "id3")], 1),
+    ("out", "id3", [("SparseSegmentMean", None)], 1),
+    ("out", "ss", [("Cast", "cst")], 1),
+    ("out", "cst", [("SparseSegmentMean", None)], 1),
+    ("out", "ssm", [("Shape", "sh2"), ("ZerosLike", "zl"), ("Select", "sel")], 3),
+    ("out", "zl", [("Select", None)], 1),
+    ("out", "sh2", [("StridedSlice", "ss2")], 1),
+    ("out", "ss2", [("Pack", "pk2")], 1),
+    ("out", "pk2", [("Tile", "tl")], 1),
+    ("out", "tl", [("Select", None)], 1),
+    ("out", "sel", [("Shape", "sh3"), ("Reshape", "rs2")], 2),
+    ("out", "sh3", [("Slice", "sl2")], 1),
+    ("out", "sl2", [("ConcatV2", None)], 1),
+    ("out", "sh", [(None, None), (None, None), (None, None), ("Cast", "cst2")], 4),
+    ("out", "cst2", [("Slice", "sl3")], 1),
+    ("out", "sl3", [("ConcatV2", "cc")], 1),
+    ("out", "cc", [("Reshape", None)], 1),
+    ("out", "rs2", [("Shape", "sh4"), ("Reshape", "rs3")], 2),
+    ("out", "sh4", [("StridedSlice", "ss3")], 1),
+    ("out", "ss3", [("Pack", "pk3")], 1),
+    ("out", "pk3", [("Reshape", None)], 1),
+]
+
+_LINEAR_SPARSE_PATTERN = [  # rec_embedding.py:797-855
+    ("in", "ed", [("Placeholder", "ph"), ("Const", "ed_dim")], None),
+    ("out", "ed", [("NotEqual", "ne"), ("GatherNd", "gnd"), ("Shape", "sh")], 3),
+    ("out", "ne", [("Where", "wh")], 1),
+    ("out", "wh", [("GatherNd", "gnd"), ("SparseReshape", "sr")], None),
+    ("out", "gnd", [("StringToHashBucketFast", "hash")], 1),
+    ("out", "hash", [("Identity", "id")], 1),
+    ("out", "id", [("Identity", "id2")], 1),
+    ("out", "id2", [("GreaterEqual", "ge"), ("GatherV2", "gv")], 2),
+    ("out", "ge", [("Where", "wh2")], 1),
+    ("out", "wh2", [("Reshape", "rs")], 1),
+    ("out", "rs", [("GatherV2", "gv1"), ("GatherV2", "gv")], 2),
+    ("out", "sh", [("Cast", "c0"), ("SparseReshape", "sr")], 2),
+    ("out", "c0", [("StridedSlice", "ss0")], 1),
+    ("out", "ss0", [("Pack", "pk0")], 1),
+    ("out", "pk0", [("Cast", "c1")], 1),
+    ("out", "c1", [("SparseReshape", "sr")], 1),
+    ("out", "sr", [("Slice", "sl"), ("GatherV2", "gvb"), ("SparseReshape", "sr2"),
+                   ("SparseReshape", None), ("Cast", None)], 5),
+    ("out", "sl", [("Prod", "pr")], 1),
+    ("out", "pr", [("Pack", "pk1")], 1),
+    ("out", "gvb", [("Pack", "pk1")], 1),
+    ("out", "sr2", [("GatherV2", "gv1"), ("Identity", "id3")], 2),
+    ("out", "id3", [("SparseFillEmptyRows", "sfer")], 1),
+    ("out", "gv1", [("SparseFillEmptyRows", "sfer")], 1),
+    ("out", "gv", [("SparseFillEmptyRows", "sfer")], 1),
+]
+
+
+def _shape_entries(attr) -> list:
+    """Entries of an `_output_shapes` attr: shape lists in the plain form,
+    TensorShapeProto bytes in a SavedModel (AttrValue.list.shape)."""
+    if isinstance(attr, savedmodel.RawAttr):
+        lst = savedmodel.Msg.parse(attr.data).get(1)
+        return savedmodel.Msg.parse(lst).all(7) if lst is not None else []
+    return list(attr or [])
+
+
+def _shapes_like(entries: list, like):
+    """An `_output_shapes` attr of `entries`, in the form of `like`."""
+    if isinstance(like, savedmodel.RawAttr):
+        lst = savedmodel.Msg([(7, savedmodel.LEN, e) for e in entries])
+        return savedmodel.RawAttr(savedmodel.Msg([(1, savedmodel.LEN, lst)]).serialize())
+    return entries
+
+
+def _tensor(node: Node, index: int) -> str:
+    return node.name if index == 0 else f"{node.name}:{index}"
+
+
+def _fuse(model: Model, index: _GraphIndex, bound: Dict[str, Node], keep: Sequence[str],
+          op: str, name: str, inputs: List[str], attrs: Dict[str, object],
+          outputs: Sequence[Tuple[Node, int]], after: Node) -> Optional[Node]:
+    """Replace the bound nodes (less `keep`) by one node of type `op` whose
+    output j stands for tensor outputs[j]: every reader of that tensor
+    outside the match reads output j instead (replace_all_users_with,
+    rewriter.py:82-88).  Returns None, changing nothing, when a node outside
+    the match reads any other output of a removed node, or names one as a
+    control input (the reference removes the nodes regardless)."""
+    gone = {bound[v].name for v in bound if v not in keep}
+    remap = {(node.name, k): j for j, (node, k) in enumerate(outputs)}
+    for n in model.nodes:
+        if n.name in gone:
+            continue
+        for inp in n.inputs:
+            if inp.startswith("^"):
+                if inp[1:] in gone:
+                    return None
+                continue
+            src, _, k = inp.partition(":")
+            if src in gone and (src, int(k or 0)) not in remap:
+                return None
+    fused = Node(name, op, list(inputs), attrs)
+    for n in model.nodes:
+        if n.name in gone:
+            continue
+        for i, inp in enumerate(n.inputs):
+            src, _, k = inp.partition(":")
+            j = remap.get((src, int(k or 0))) if not inp.startswith("^") else None
+            if j is not None:
+                n.inputs[i] = _tensor(fused, j)
+    at = model.nodes.index(after)
+    model.nodes.insert(at + 1, fused)
+    model.nodes[:] = [n for n in model.nodes if n.name not in gone]
+    return fused
+
+
+def sparse_embedding_passes(model: Model, pass_name: str) -> List[str]:
+    """DnnSparseEmbeddingPatternRewriter, DnnEmbeddingWithHashBucket-
+    PatternRewriter and LinearSparseEmbeddingPatternRewriter
+    (rec_embedding.py:6-211, 794-891): every ExpandDims at the root of such a
+    hash-bucket column becomes one KPFusedSparseEmbedding (outputs: the
+    SparseFillEmptyRows' indices, values and empty-row indicator, then the
+    dense shape) or KPFusedDnnEmbeddingWithHashBucket (inputs: the strings
+    and the embedding weight; output: the column's [batch, dim] result),
+    with the hash node's attrs (num_buckets).  Returns the fused node names."""
+    pattern = {"dnn_sparse": _DNN_SPARSE_PATTERN, "dnn_hash_bucket": _DNN_HASH_BUCKET_PATTERN,
+               "linear_sparse": _LINEAR_SPARSE_PATTERN}[pass_name]
+    made: List[str] = []
+    for anchor_name in [n.name for n in model.nodes if n.op == "ExpandDims"]:
+        index = _GraphIndex(model)
+        ed = index.by_name.get(anchor_name)
+        if ed is None:
+            continue
+        b = _match(index, ed, pattern, "ed")
+        if b is None:
+            continue
+        sfer, hash_node = b["sfer"], b["hash"]
+        attrs = {k: v for k, v in hash_node.attrs.items() if k != "_output_shapes"}
+        if pass_name == "dnn_hash_bucket":
+            # rec_embedding.py:186-196
+            outputs = [(b["rs3"], 0)]
+            shapes = _shape_entries(b["rs3"].attrs.get("_output_shapes"))[:1]
+            like = b["rs3"].attrs.get("_output_shapes")
+            op, suffix = "KPFusedDnnEmbeddingWithHashBucket", "/rec_embed_kp_dnn_bucket"
+            inputs = [ed.inputs[0], b["gv4"].inputs[0]]
+        else:
+            # rec_embedding.py:57-72 (dense shape: the Shape node's output) and
+            # 863-877 (the SparseReshape's output 1)
+            tail = (b["sh"], 0) if pass_name == "dnn_sparse" else (b["sr"], 1)
+            outputs = [(sfer, 0), (sfer, 1), (sfer, 2), tail]
+            like = sfer.attrs.get("_output_shapes")
+            shapes = (_shape_entries(like)[:3] +
+                      _shape_entries(tail[0].attrs.get("_output_shapes"))[tail[1]:tail[1] + 1])
+            op, suffix = "KPFusedSparseEmbedding", "/rec_embed_kp_sparse"
+            inputs = [ed.inputs[0]]
+        if like is not None:
+            attrs["_output_shapes"] = _shapes_like(shapes, like)
+        fused = _fuse(model, index, b, ("ph",), op, sfer.name + suffix, inputs, attrs, outputs,
+                      after=ed)
+        if fused is not None:
+            made.append(fused.name)
+    return made
+
+
 def optimize(input_path: str, output_path: str, passes: Sequence[str]) -> List[str]:
     """main.opt (main.py:43-68): load, run the passes in the order given with
     layout_matmul moved last, save.  Returns the variables layout_matmul
@@ -551,7 +757,7 @@ def optimize(input_path: str, output_path: str, passes: Sequence[str]) -> List[s
     for p in passes:
         if p in UNSUPPORTED_PASSES:
             raise TypeError(f"Pass '{p}' emits a fused op this build does not implement")
-        if p != "layout_matmul" and p not in EMBEDDING_PASSES:
+        if p != "layout_matmul" and p not in EMBEDDING_PASSES + SPARSE_PASSES:
             raise TypeError(f"Pass '{p}' not found")
     if "layout_matmul" in passes:
         passes = [p for p in passes if p != "layout_matmul"] + ["layout_matmul"]
@@ -560,6 +766,8 @@ def optimize(input_path: str, output_path: str, passes: Sequence[str]) -> List[s
     for p in passes:
         if p == "layout_matmul":
             packed = layout_matmul(model)
+        elif p in SPARSE_PASSES:
+            sparse_embedding_passes(model, p)
         else:
             embedding_with_hash_bucket(model, p)
     save_model(model, output_path, source=input_path)
@@ -571,7 +779,7 @@ def parse_args(argv=None):
     parser.add_argument("-I", "--input", required=True, help="Input model path")
     parser.add_argument("-O", "--output", required=True, help="Output model path")
     parser.add_argument("passes", nargs="+",
-                        help="opt: " + ", ".join(repr(p) for p in EMBEDDING_PASSES)
+                        help="opt: " + ", ".join(repr(p) for p in EMBEDDING_PASSES + SPARSE_PASSES)
                              + ", 'layout_matmul'")
     return parser.parse_args(argv)
 

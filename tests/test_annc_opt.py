@@ -126,7 +126,7 @@ def test_unknown_and_unsupported_passes_are_rejected(tmp_path):
     src, _, _ = _model(tmp_path)
     with pytest.raises(TypeError, match="not found"):
         annc_opt.optimize(str(src), str(tmp_path / "o1"), ["layout_matmul", "fold_all"])
-    for p in ("dnn_sparse", "dnn_hash_bucket", "embed", "linear_sparse", "softmax"):
+    for p in ("embed", "softmax"):
         with pytest.raises(TypeError, match="does not implement"):
             annc_opt.optimize(str(src), str(tmp_path / "o2"), [p])
 
