@@ -63,6 +63,7 @@ _PROTOTYPES = {
     "__batch_matmul": (None, [_c_void_p, _c_void_p]),
     "__layout_matmul": (None, [_c_void_p, _c_void_p]),
     "__pooling": (None, [_c_void_p, _c_void_p]),
+    "__reduce_mean": (None, [_c_void_p, _c_void_p]),
     "annc_custom_call_target": (_c_void_p, [_cp]),
     "annc_register_custom_call_targets": (_i32, [_c_void_p, _c_void_p]),
     "annc_layout_matmul_rhs_format": (_cp, []),

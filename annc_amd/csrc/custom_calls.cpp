@@ -12,6 +12,7 @@
 #include <cstring>
 
 #include "common.h"
+#include "embedding_impl.h"
 
 namespace annc {
 namespace {
@@ -117,6 +118,26 @@ int run_pooling(void* out, void** in) {
   return st.finish();
 }
 
+int run_reduce_mean(void* out, const void** in) {
+  // reduce_rewriter.cc:31-46: in[0] (the axis, read as a float) is unused;
+  // in[1] holds n runs of m values, m = shape[0] and n = shape[1] of in[3].
+  int64_t shape[2];
+  const int rc0 = read_i64(in[3], 2, shape);
+  if (rc0 != ANNC_OK) return rc0;
+  const int64_t m = shape[0], n = shape[1];
+  ANNC_REQUIRE(m >= 0 && n >= 0, "negative dimension in shape info");
+  if (n == 0) return ANNC_OK;
+  hipStream_t s = lib_stream();
+  if (!s) return set_error(ANNC_INTERNAL, "no HIP stream");
+  Staging st(s);
+  const float* x = static_cast<const float*>(st.in(in[1], sizeof(float) * (size_t)(m * n)));
+  float* o = static_cast<float*>(st.out(out, sizeof(float) * (size_t)n));
+  if (st.status() != ANNC_OK) return st.status();
+  const int rc = launch_abs_mean(s, x, m, n, o);
+  if (rc != ANNC_OK) return rc;
+  return st.finish();
+}
+
 struct Target {
   const char* name;
   void* fn;
@@ -160,11 +181,16 @@ void __layout_matmul(void* out, const void** in) {
 
 void __pooling(void* out, void** in) { annc::report("__pooling", annc::run_pooling(out, in)); }
 
+void __reduce_mean(void* out, const void** in) {
+  annc::report("__reduce_mean", annc::run_reduce_mean(out, in));
+}
+
 static const annc::Target kTargets[] = {
     {"__matmul", reinterpret_cast<void*>(&__matmul)},
     {"__batch_matmul", reinterpret_cast<void*>(&__batch_matmul)},
     {"__matmul_add", reinterpret_cast<void*>(&__matmul_add)},
     {"__matmul_add_relu", reinterpret_cast<void*>(&__matmul_add_relu)},
+    {"__reduce_mean", reinterpret_cast<void*>(&__reduce_mean)},
     {"__pooling", reinterpret_cast<void*>(&__pooling)},
     {"__layout_matmul", reinterpret_cast<void*>(&__layout_matmul)},
 };

@@ -2057,6 +2057,22 @@ int launch_sparse_embedding2(hipStream_t s, const float* table, int64_t rows, in
   return ANNC_OK;
 }
 
+// __reduce_mean (reduce_rewriter.cc:31-46): out[i] = (sum of |x| over the
+// i-th run of m consecutive values) / m, one wave per output.  The lanes
+// take strided values and a butterfly of lane shuffles adds their sums (the
+// reference's cblas_sasum fixes no order either).
+__global__ __launch_bounds__(kThreads) void abs_mean_kernel(const float* __restrict__ x, int64_t m,
+                                                            int64_t n, float* __restrict__ out) {
+  const int64_t i = ((int64_t)blockIdx.x * kThreads + threadIdx.x) >> 6;
+  const int lane = threadIdx.x & 63;
+  if (i >= n) return;
+  const float* __restrict__ row = x + i * m;
+  float acc = 0.0f;
+  for (int64_t j = lane; j < m; j += 64) acc += fabsf(row[j]);
+  for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
+  if (lane == 0) out[i] = acc / static_cast<float>(static_cast<int>(m));
+}
+
 int launch_pooling(hipStream_t s, const int64_t* ids, const float* gathered, int64_t m, int64_t k,
                    int64_t n, const int64_t* ss, const int64_t* sl, float* out) {
   if (m * n == 0) return ANNC_OK;
@@ -2092,6 +2108,14 @@ int launch_pooling(hipStream_t s, const int64_t* ids, const float* gathered, int
   }
   hipLaunchKernelGGL(pooling_kernel, dim3((unsigned)ceil_div(m * n, kThreads)), dim3(kThreads), 0,
                      s, ids, gathered, m, k, n, ss[0], ss[1], ss[2], sl[0], sl[1], sl[2], out);
+  ANNC_HIP_TRY(hipGetLastError());
+  return ANNC_OK;
+}
+
+int launch_abs_mean(hipStream_t s, const float* x, int64_t m, int64_t n, float* out) {
+  if (n <= 0) return ANNC_OK;
+  hipLaunchKernelGGL(abs_mean_kernel, dim3((unsigned)ceil_div(n * 64, kThreads)), dim3(kThreads),
+                     0, s, x, m, n, out);
   ANNC_HIP_TRY(hipGetLastError());
   return ANNC_OK;
 }

@@ -87,6 +87,8 @@ int launch_sparse_embedding2(hipStream_t s, const float* table, int64_t rows, in
 
 int launch_pooling(hipStream_t s, const int64_t* ids, const float* gathered, int64_t m, int64_t k,
                    int64_t n, const int64_t* ss, const int64_t* sl, float* out);
+// out[i] = sum(|x[i*m .. i*m+m)|) / m for i < n (the __reduce_mean target).
+int launch_abs_mean(hipStream_t s, const float* x, int64_t m, int64_t n, float* out);
 
 // Hash-bucket helpers (hash.hip).
 struct StringsArgs {

@@ -17,8 +17,8 @@ from . import _lib
 from ._lib import ptr
 
 # Operand order of every target (gemm_rewriter.cc:136-281, graph_opt.cc:100-107).
-TARGETS = ("__matmul", "__batch_matmul", "__matmul_add", "__matmul_add_relu", "__pooling",
-           "__layout_matmul")
+TARGETS = ("__matmul", "__batch_matmul", "__matmul_add", "__matmul_add_relu", "__reduce_mean",
+           "__pooling", "__layout_matmul")
 
 _FN = ctypes.CFUNCTYPE(None, ctypes.c_void_p, ctypes.c_void_p)
 
@@ -77,6 +77,13 @@ def batch_matmul(a, b, out):
 
 def layout_matmul(a, b_packed, k: int, n: int, out):
     call("__layout_matmul", out, [a, b_packed, shape_info(_shape(a)), shape_info((k, n))])
+
+
+def reduce_mean(x, out, axis: float = 0.0):
+    """__reduce_mean on x of shape (m, n): out (n values) gets, for each i,
+    the mean of |x| over the i-th run of m consecutive values of x."""
+    call("__reduce_mean", out, [np.asarray([axis], dtype=np.float32), x, shape_info((1,)),
+                                shape_info(_shape(x))])
 
 
 def pooling(ids, gathered, slice_starts, slice_limits, out):

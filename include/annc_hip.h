@@ -156,14 +156,21 @@ void __layout_matmul(void* out, const void** in);
 /* graph_opt.cc:131-176  in = {ids s64[m,k], gathered f32[m,k,n], slice_starts s64[3],
  *                             slice_limits s64[3], shape(ids), shape(gathered)} ; out f32[m,n] */
 void __pooling(void* out, void** in);
+/* reduce_rewriter.cc:31-46 (registered by REGISTER_ALL_GEMM_KERNELS,
+ * kdnn_rewriter.h:148-155; the rewriter that would emit it is disabled,
+ * reduce_rewriter.cc:24-27)  in = {axis (read as f32, unused), x f32,
+ * shape(axis), shape(x) s64 with m = [0], n = [1]} ; out f32[n]:
+ * out[i] = (sum of |x[i*m + j]|, j < m) / m, the reference's cblas_sasum
+ * over n consecutive runs of m values. */
+void __reduce_mean(void* out, const void** in);
 
 /* Function pointer of a custom-call target by its registered name, or NULL.
  * Equivalent of the lookup XLA performs after
  * XLA_CPU_REGISTER_CUSTOM_CALL_TARGET (kdnn_rewriter.h:148-155). */
 void* annc_custom_call_target(const char* name);
 /* Calls cb(name, fn, user) once per target, in the order of
- * REGISTER_ALL_GEMM_KERNELS (kdnn_rewriter.h:148-155, minus the
- * never-registered __reduce_mean); returns the number of targets. */
+ * REGISTER_ALL_GEMM_KERNELS (kdnn_rewriter.h:148-155); returns the number
+ * of targets. */
 int annc_register_custom_call_targets(void (*cb)(const char* name, void* fn, void* user),
                                       void* user);
 

@@ -26,6 +26,7 @@
  *   ora_embedding_bag      same order as ora_segment_reduce (CSR form);
  *                          checked equal to it in tests/.
  *   ora_pooling            brute force on tiny inputs in tests/.
+ *   ora_reduce_mean        numpy's sum of |x| per run (float64) in tests/.
  *   ora_hash_bucket_int64  decimal text checked against Python's str(int);
  *                          the hash as ora_fingerprint64.
  *   ora_embedding_with_hash_bucket, ora_dnn_embedding_with_hash_bucket,
@@ -365,6 +366,16 @@ void ora_pooling(const int64_t* ids, const float* gathered, int64_t m, int64_t k
       }
       out[i * n + p] = empty ? 0.0f : sum / red;
     }
+  }
+}
+
+/* __reduce_mean (annc/service/cpu/reduce_rewriter.cc:31-46): out[i] =
+ * sasum of the i-th run of m values, divided by (int)m. */
+void ora_reduce_mean(const float* x, int64_t m, int64_t n, float* out) {
+  for (int64_t i = 0; i < n; ++i) {
+    float s = 0.0f;
+    for (int64_t j = 0; j < m; ++j) s += fabsf(x[i * m + j]);
+    out[i] = s / (float)(int)m;
   }
 }
 

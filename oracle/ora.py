@@ -34,6 +34,7 @@ _PROTO = {
     "ora_segment_reduce_nonzero": (_i64, [_v, _i64, _i64, _v, _i32, _v, _i64, _i64, _i32, _i32,
                                           _v, _v, _v, _i64]),
     "ora_pooling": (None, [_v, _v, _i64, _i64, _i64, _v, _v, _v]),
+    "ora_reduce_mean": (None, [_v, _i64, _i64, _v]),
     "ora_sparse_embedding2": (None, [_v, _i64, _i64, _v, _i32, _i64, _i64, _v]),
     "ora_fused_gather": (_i64, [_v, _i64, _i64, _v, _i64, _i64, _v, _v, _v]),
     "ora_batch_matmul_add_sigmoid": (None, [_v, _v, _i32, _v, _v, _i64, _i64, _i64, _i64, _v]),
@@ -185,6 +186,15 @@ def embedding_bag(table, ids, offsets, combiner, threads=1) -> np.ndarray:
     out = np.empty((nb, table.shape[1]), dtype=np.float32)
     lib().ora_embedding_bag(_p(table), table.shape[0], table.shape[1], _p(ids), int(idx64),
                             _p(offsets), nb, int(combiner), _p(out), table.shape[1], int(threads))
+    return out
+
+
+def reduce_mean(x) -> np.ndarray:
+    """__reduce_mean on x [m, n]: n means of |x| over runs of m values."""
+    x = _c(x, np.float32)
+    m, n = x.shape
+    out = np.empty(n, dtype=np.float32)
+    lib().ora_reduce_mean(_p(x), m, n, _p(out))
     return out
 
 

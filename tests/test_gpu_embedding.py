@@ -781,3 +781,27 @@ def test_tf_ops_from_concurrent_threads():
     for t in threads:
         t.join()
     assert not errors, errors
+
+
+@pytest.mark.parametrize("m,n", [(7, 5), (1, 3), (64, 1), (100_000, 3), (300, 4097), (0, 2)])
+@pytest.mark.parametrize("where", ["host", "device"])
+def test_reduce_mean_custom_call(m, n, where):
+    """__reduce_mean through the registered target (reduce_rewriter.cc:31-46):
+    the mean of |x| over each run of m consecutive values, against the
+    oracle's sequential sum at fp32 tolerance (cblas_sasum fixes no order);
+    m = 0 gives 0/0."""
+    note(f"__reduce_mean m={m} n={n} {where}")
+    g = workloads.rng(m + n)
+    x = g.standard_normal((m, n)).astype(np.float32)
+    want = ora.reduce_mean(x)
+    if where == "host":
+        out = np.full(n, -1.0, np.float32)
+        xla.reduce_mean(x, out)
+    else:
+        out_d = torch.full((n,), -1.0, device=device())
+        xla.reduce_mean(to_dev(x), out_d)
+        out = to_host(out_d)
+    if m == 0:
+        assert np.isnan(out).all()
+    else:
+        np.testing.assert_allclose(out, want, rtol=1e-5 + 2e-7 * np.sqrt(m))

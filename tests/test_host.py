@@ -35,12 +35,14 @@ def test_library_exports_every_header_symbol():
 
 
 def test_custom_call_registry():
+    # REGISTER_ALL_GEMM_KERNELS's order (kdnn_rewriter.h:148-155)
     assert xla.registered_targets() == ["__matmul", "__batch_matmul", "__matmul_add",
-                                        "__matmul_add_relu", "__pooling", "__layout_matmul"]
+                                        "__matmul_add_relu", "__reduce_mean", "__pooling",
+                                        "__layout_matmul"]
     lib = _lib.lib()
     for t in xla.TARGETS:
         assert lib.annc_custom_call_target(t.encode())
-    assert not lib.annc_custom_call_target(b"__reduce_mean")
+    assert not lib.annc_custom_call_target(b"__softmax")
 
 
 # ------------------------------------------------------------------ flags

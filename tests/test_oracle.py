@@ -167,6 +167,21 @@ def test_pooling_matches_brute_force():
                                       _brute_pooling(ids, gathered, ss, sl))
 
 
+def test_reduce_mean_is_the_mean_absolute_value_of_consecutive_runs():
+    """__reduce_mean (reduce_rewriter.cc:31-46): cblas_sasum over n runs of m
+    consecutive values, divided by m: the absolute values (not the values)
+    of x viewed as [n, m], whatever x's [m, n] shape says."""
+    g = np.random.Generator(np.random.PCG64(9))
+    for m, n in [(7, 5), (1, 3), (64, 1), (300, 17)]:
+        x = g.standard_normal((m, n)).astype(np.float32)
+        want = np.abs(x.astype(np.float64)).reshape(n, m).sum(axis=1) / m
+        np.testing.assert_allclose(ora.reduce_mean(x), want, rtol=2e-6)
+        if m > 1 and n > 1:  # a plain mean of the values, or of x's columns, is not it
+            assert not np.allclose(ora.reduce_mean(x), x.reshape(n, m).mean(axis=1), rtol=1e-3)
+            assert not np.allclose(ora.reduce_mean(x), np.abs(x).mean(axis=0), rtol=1e-3)
+    assert np.isnan(ora.reduce_mean(np.zeros((0, 2), np.float32))).all()  # 0 / 0
+
+
 def test_sparse_embedding2_mask_semantics():
     table = np.arange(12, dtype=np.float32).reshape(4, 3) - 5.0
     ids = np.array([0, 3, -1, 4, 2], dtype=np.int64)
