@@ -89,8 +89,10 @@ namespace {
 // Phase-1 results of KPFusedSparseSegmentReduceNonzero, kept for the phase-2
 // call that follows on the same thread and device with the same operands
 // (as one TensorFlow Compute() makes them: count, allocate, write), so that
-// phase 2 only writes the listed values.  Buffers grow as needed and are
-// held until the thread ends.
+// phase 2 only writes the listed values.  Buffers grow as needed and, like
+// the thread's pinned and staging buffers, are kept until the process ends
+// (releasing them at thread exit could run after the HIP runtime has shut
+// down).
 struct NzKey {
   const void* data;
   int data_rank;
