@@ -10,16 +10,15 @@
 //      key, linear probing, capacity a power of two >= 2n, a separate slot
 //      for the empty marker's own value) and the slot keeps the smallest
 //      position of its key (atomicMin): the key's first occurrence;
-//   2. position i is a first occurrence iff its slot's minimum is i; an
-//      inclusive scan of those marks numbers the unique keys in order of
-//      first occurrence (the reference's order), U = the last sum;
+//   2. position i is a first occurrence iff its slot's minimum is i; the
+//      first occurrences are numbered in position order (the reference's
+//      order) by block-local ranks plus a prefix over the blocks' counts;
 //   3. indices[i] = number of the first occurrence of i's key; that
-//      occurrence also writes unique[number] = key;
-//   4. out rows of the U unique keys, G lanes per row, 16-byte loads where
-//      the rows allow.
-// U is only known on the device; kernels sized by n test r < U themselves.
+//      occurrence also writes unique[number] = key, and its workgroup copies
+//      the table row of the key (G lanes per row, 16-byte loads where the
+//      rows allow).
+// U, the number of unique keys, is only known on the device.
 #include <hip/hip_runtime.h>
-#include <hipcub/hipcub.hpp>
 
 #include <algorithm>
 #include <climits>
@@ -145,71 +144,272 @@ __global__ __launch_bounds__(kUgThreads) void ug_insert_kernel(
   }
 }
 
-__global__ void ug_mark_kernel(const int32_t* __restrict__ slot_of,
-                               const int32_t* __restrict__ tab_first, int64_t n,
-                               int32_t* __restrict__ first_mark) {
-  const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-  if (i >= n) return;
-  first_mark[i] = tab_first[slot_of[i]] == static_cast<int32_t>(i) ? 1 : 0;
+// ---------------------------------------------------------------------------
+// Numbering first occurrences (both engines).  With f(i) the smallest
+// position of i's key, position i is a first occurrence iff f(i) == i, and
+// its key's number is the count of first occurrences at positions <= f(i).
+//   fr_rank_kernel    per block of kFrBlock positions: f(i) for every
+//                     position, the block-local inclusive rank of each first
+//                     occurrence, the block's count;
+//   fr_prefix_kernel  (beyond kFrLdsBlocks blocks only) exclusive prefix of
+//                     the block counts, one workgroup;
+//   fr_number_kernel  one position per thread: number = prefix[block(f)] +
+//                     rank[f], giving the inverse index, the unique keys,
+//                     their count and (with a table) the rows of the unique
+//                     keys whose first occurrence is in the workgroup.
+// Up to kFrLdsBlocks blocks each number workgroup forms the prefix of the
+// counts it needs in LDS, so the chain is two launches; the row copy runs in
+// n/256 workgroups spread over the chip.
+// ---------------------------------------------------------------------------
+constexpr int kFrThreads = 256;
+constexpr int kFrItems = 2;
+constexpr int kFrShift = 9;
+constexpr int kFrBlock = 1 << kFrShift;  // kFrThreads * kFrItems positions
+constexpr int kFrWaves = kFrThreads / 64;
+constexpr int kFrLdsBlocks = 1024;      // prefix formed in LDS: n <= 2^19
+static_assert(kFrBlock == kFrThreads * kFrItems, "block = threads x items");
+
+// f(i) through the hash table: the slot's smallest position
+struct FirstBySlot {
+  const int32_t* slot_of;
+  const int32_t* tab_first;
+  __device__ int32_t operator()(int64_t i) const { return tab_first[slot_of[i]]; }
+};
+// f(i) through the directly indexed table of a small key range
+struct FirstByKey {
+  const int64_t* keys;
+  int64_t stride, kmin;
+  const int32_t* first;
+  __device__ int32_t operator()(int64_t i) const { return first[keys[i * stride] - kmin]; }
+};
+
+// Inclusive sum over the workgroup of one value per thread; *total gets the
+// workgroup's sum.  Uses wsum[kFrWaves]; ends with every wave past its reads.
+__device__ __forceinline__ int32_t fr_block_scan(int32_t v, int32_t* wsum, int32_t* total) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  int32_t incl = v;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int32_t x = __shfl_up(incl, off, 64);
+    if (lane >= off) incl += x;
+  }
+  if (lane == 63) wsum[w] = incl;
+  __syncthreads();
+  int32_t before = 0, all = 0;
+#pragma unroll
+  for (int q = 0; q < kFrWaves; ++q) {
+    before += q < w ? wsum[q] : 0;
+    all += wsum[q];
+  }
+  __syncthreads();
+  *total = all;
+  return before + incl;
 }
 
-// number[i] = inclusive count of first occurrences up to i
-__global__ void ug_output_kernel(const int64_t* __restrict__ keys, int64_t stride, int64_t n,
-                                 const int32_t* __restrict__ slot_of,
-                                 const int32_t* __restrict__ tab_first,
-                                 const int32_t* __restrict__ number, int32_t* __restrict__ indices,
-                                 int64_t* __restrict__ unique, int64_t* __restrict__ num_unique) {
-  const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-  if (i >= n) return;
-  const int32_t first = tab_first[slot_of[i]];
-  const int32_t r = number[first] - 1;
-  indices[i] = r;
-  if (first == static_cast<int32_t>(i)) unique[r] = keys[i * stride];
-  if (i == n - 1) num_unique[0] = number[n - 1];
+// fpos[i] = f(i) (fpos may be the slot_of array f reads: each thread reads
+// its own positions before writing them); rank[i] = 1-based rank of i among
+// its block's first occurrences (written at first occurrences only);
+// count[b] = the block's first occurrences.
+template <class F>
+__global__ __launch_bounds__(kFrThreads) void fr_rank_kernel(F first_of, int64_t n,
+                                                             int32_t* fpos,
+                                                             int32_t* __restrict__ rank,
+                                                             int32_t* __restrict__ count) {
+  __shared__ int32_t wc[kFrItems][kFrWaves];
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const int64_t b0 = (int64_t)blockIdx.x << kFrShift;
+  int32_t f[kFrItems];
+#pragma unroll
+  for (int u = 0; u < kFrItems; ++u) {
+    const int64_t i = b0 + u * kFrThreads + t;
+    f[u] = i < n ? first_of(i) : -1;
+  }
+  bool mk[kFrItems];
+  int rk[kFrItems];
+#pragma unroll
+  for (int u = 0; u < kFrItems; ++u) {
+    const int64_t i = b0 + u * kFrThreads + t;
+    mk[u] = i < n && f[u] == static_cast<int32_t>(i);
+    const uint64_t m = __ballot(mk[u]);
+    rk[u] = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32),
+                                      __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0));
+    if (lane == 0) wc[u][w] = __popcll(m);
+  }
+  __syncthreads();
+  // ranks in position order: item u's positions follow all of item u-1's
+  int32_t before = 0;
+#pragma unroll
+  for (int u = 0; u < kFrItems; ++u) {
+    int32_t off = before;
+#pragma unroll
+    for (int q = 0; q < kFrWaves; ++q) off += q < w ? wc[u][q] : 0;
+    const int64_t i = b0 + u * kFrThreads + t;
+    if (i < n) {
+      fpos[i] = f[u];
+      if (mk[u]) rank[i] = off + rk[u] + 1;
+    }
+#pragma unroll
+    for (int q = 0; q < kFrWaves; ++q) before += wc[u][q];
+  }
+  if (t == 0) count[blockIdx.x] = before;
 }
 
-// out[r, :] = table[unique[r], :] for r < U, G lanes per row (VEC floats per
-// lane); keys outside the table give a zero row and set the status word.
-template <int G, int VEC>
-__global__ __launch_bounds__(kThreads) void ug_gather_kernel(
-    const float* __restrict__ table, int64_t rows, int64_t dim, const int64_t* __restrict__ unique,
-    const int64_t* __restrict__ num_unique, int64_t n, float* __restrict__ out,
-    int* __restrict__ status) {
-  const int g = threadIdx.x & (G - 1);
-  const int64_t r = ((int64_t)blockIdx.x * kThreads + threadIdx.x) / G;
-  if (r >= n || r >= num_unique[0]) return;
-  const int64_t id = unique[r];
-  const bool ok = id >= 0 && id < rows;
-  if (!ok && g == 0) atomicOr(status, 1);
-  const float* src = table + (ok ? id : 0) * dim;
-  float* dst = out + r * dim;
-  for (int64_t c = (int64_t)g * VEC; c < dim; c += (int64_t)G * VEC) {
-    if constexpr (VEC == 4) {
-      typedef float V __attribute__((ext_vector_type(4)));
-      const V v = ok ? *reinterpret_cast<const V*>(src + c) : V(0.0f);
-      *reinterpret_cast<V*>(dst + c) = v;
-    } else {
-      dst[c] = ok ? src[c] : 0.0f;
+// pre[b] = sum of count[0..b) over nblk blocks, one workgroup
+__global__ __launch_bounds__(kFrThreads) void fr_prefix_kernel(const int32_t* __restrict__ count,
+                                                               int64_t nblk,
+                                                               int32_t* __restrict__ pre) {
+  __shared__ int32_t wsum[kFrWaves];
+  int32_t carry = 0;
+  for (int64_t base = 0; base < nblk; base += kFrThreads) {
+    const int64_t j = base + threadIdx.x;
+    const int32_t v = j < nblk ? count[j] : 0;
+    int32_t total;
+    const int32_t incl = fr_block_scan(v, wsum, &total);
+    if (j < nblk) pre[j] = carry + incl - v;
+    carry += total;
+  }
+}
+
+// Position i = workgroup * kFrThreads + thread: indices[i] = number(f(i)) -
+// 1; at first occurrences unique[number - 1] = key; the thread of the last
+// position writes num_unique; with dim > 0 the workgroup then copies the
+// rows of its first occurrences' keys, g lanes per row (VEC floats per
+// lane), keys outside the table giving a zero row and the status bit.
+// GPRE: the prefix comes from fr_prefix_kernel instead of being formed here.
+template <int VEC, bool GPRE>
+__global__ __launch_bounds__(kFrThreads) void fr_number_kernel(
+    const int64_t* __restrict__ keys, int64_t stride, int64_t n, const int32_t* __restrict__ fpos,
+    const int32_t* __restrict__ rank, const int32_t* __restrict__ count,
+    const int32_t* __restrict__ gpre, int32_t* __restrict__ indices, int64_t* __restrict__ unique,
+    int64_t* __restrict__ num_unique, const float* __restrict__ table, int64_t rows, int64_t dim,
+    int g, float* __restrict__ out, int* __restrict__ status) {
+  __shared__ int32_t pre[GPRE ? 1 : kFrLdsBlocks];
+  __shared__ int32_t wsum[kFrWaves];
+  __shared__ int64_t lkey[kFrThreads];
+  __shared__ int32_t lnum[kFrThreads];
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const int64_t i = (int64_t)blockIdx.x * kFrThreads + t;
+  const int64_t ic = i < n ? i : n - 1;
+  const int32_t f = fpos[ic];
+  const int64_t key = keys[ic * stride];
+  const int32_t fb = f >> kFrShift;
+  int32_t p;  // exclusive prefix of f's block
+  if constexpr (GPRE) {
+    p = gpre[fb];
+  } else {
+    // prefix of the counts of blocks 0 .. (last position of the workgroup's block)
+    const int64_t last = min((int64_t)(blockIdx.x + 1) * kFrThreads, n) - 1;
+    const int64_t nb = (last >> kFrShift) + 1;
+    int32_t carry = 0;
+    for (int64_t base = 0; base < nb; base += kFrThreads) {
+      const int64_t j = base + t;
+      const int32_t v = j < nb ? count[j] : 0;
+      int32_t total;
+      const int32_t incl = fr_block_scan(v, wsum, &total);
+      if (j < nb) pre[j] = carry + incl - v;
+      carry += total;
+    }
+    __syncthreads();
+    p = pre[fb];
+    if (i == n - 1) num_unique[0] = carry;
+  }
+  const bool valid = i < n;
+  const bool first = valid && f == static_cast<int32_t>(i);
+  const int32_t r = p + rank[f] - 1;
+  if (valid) indices[i] = r;
+  if (first) unique[r] = key;
+  if constexpr (GPRE) {
+    if (i == n - 1) {  // the last block's prefix and count: the total
+      const int64_t lb = (n - 1) >> kFrShift;
+      num_unique[0] = gpre[lb] + count[lb];
+    }
+  }
+  if (dim == 0) return;
+  // list the workgroup's first occurrences in LDS, then copy their rows
+  const uint64_t m = __ballot(first);
+  const int rk = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32),
+                                           __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0));
+  if (lane == 0) wsum[w] = __popcll(m);
+  __syncthreads();
+  int before = 0, cnt = 0;
+#pragma unroll
+  for (int q = 0; q < kFrWaves; ++q) {
+    before += q < w ? wsum[q] : 0;
+    cnt += wsum[q];
+  }
+  if (first) {
+    lkey[before + rk] = key;
+    lnum[before + rk] = r;
+  }
+  __syncthreads();
+  const int lane_g = t & (g - 1);
+  for (int e = t / g; e < cnt; e += kFrThreads / g) {
+    const int64_t id = lkey[e];
+    const bool ok = id >= 0 && id < rows;
+    if (!ok && lane_g == 0) atomicOr(status, 1);
+    const float* src = table + (ok ? id : 0) * dim;
+    float* dst = out + (int64_t)lnum[e] * dim;
+    for (int64_t c = (int64_t)lane_g * VEC; c < dim; c += (int64_t)g * VEC) {
+      if constexpr (VEC == 4) {
+        typedef float V __attribute__((ext_vector_type(4)));
+        const V v = ok ? *reinterpret_cast<const V*>(src + c) : V(0.0f);
+        *reinterpret_cast<V*>(dst + c) = v;
+      } else {
+        dst[c] = ok ? src[c] : 0.0f;
+      }
     }
   }
 }
 
 __global__ void store_i64_kernel(int64_t* p, int64_t v) { *p = v; }
 
-template <int VEC>
-void launch_ug_gather(hipStream_t s, int g, const float* table, int64_t rows, int64_t dim,
-                      const int64_t* unique, const int64_t* num_unique, int64_t n, float* out,
-                      int* status) {
-  const dim3 grid((unsigned)ceil_div(n * g, kThreads));
-  switch (g) {
-#define ANNC_UG(G)                                                                          \
-  case G:                                                                                   \
-    hipLaunchKernelGGL((ug_gather_kernel<G, VEC>), grid, dim3(kThreads), 0, s, table, rows, \
-                       dim, unique, num_unique, n, out, status);                            \
-    break;
-    ANNC_UG(1) ANNC_UG(2) ANNC_UG(4) ANNC_UG(8) ANNC_UG(16) ANNC_UG(32) ANNC_UG(64)
-#undef ANNC_UG
+// Workspace of the numbering: rank (n) and count (+ prefix beyond the LDS
+// limit) as int32, each 256-byte aligned.
+size_t fr_workspace(int64_t n) {
+  auto align = [](size_t x) { return (x + 255) & ~size_t(255); };
+  const int64_t nblk = ceil_div(n, kFrBlock);
+  return align(sizeof(int32_t) * (size_t)n) +
+         align(sizeof(int32_t) * (size_t)nblk) * (nblk > kFrLdsBlocks ? 2 : 1);
+}
+
+// Numbers first occurrences given f (fpos receives f(i); it may be the
+// array f reads), writes indices, unique, num_unique, and the rows of the
+// unique keys when dim > 0.
+template <class F>
+int first_numbering(hipStream_t s, F first_of, const int64_t* keys, int64_t stride, int64_t n,
+                    int32_t* fpos, char* ws, int64_t* num_unique, int64_t* unique,
+                    int32_t* indices, const float* table, int64_t rows, int64_t dim, float* out,
+                    int* status) {
+  auto align = [](size_t x) { return (x + 255) & ~size_t(255); };
+  const int64_t nblk = ceil_div(n, kFrBlock);
+  int32_t* rank = reinterpret_cast<int32_t*>(ws);
+  int32_t* count = reinterpret_cast<int32_t*>(ws + align(sizeof(int32_t) * (size_t)n));
+  int32_t* gpre = count + align(sizeof(int32_t) * (size_t)nblk) / sizeof(int32_t);
+  const bool gp = nblk > kFrLdsBlocks;
+  hipLaunchKernelGGL(fr_rank_kernel<F>, dim3((unsigned)nblk), dim3(kFrThreads), 0, s, first_of, n,
+                     fpos, rank, count);
+  ANNC_HIP_TRY(hipGetLastError());
+  if (gp) {
+    hipLaunchKernelGGL(fr_prefix_kernel, dim3(1), dim3(kFrThreads), 0, s, count, nblk, gpre);
+    ANNC_HIP_TRY(hipGetLastError());
   }
+  int g = 1;
+  const bool vec = dim > 0 && dim % 4 == 0 &&
+                   ((reinterpret_cast<uintptr_t>(table) | reinterpret_cast<uintptr_t>(out)) & 15) == 0;
+  const int64_t lanes = vec ? dim / 4 : dim;
+  while (g < 64 && g < lanes) g <<= 1;
+  auto launch = [&](auto kernel) {
+    hipLaunchKernelGGL(kernel, dim3((unsigned)ceil_div(n, kFrThreads)), dim3(kFrThreads), 0, s,
+                       keys, stride, n, fpos,
+                       rank, count, gpre, indices, unique, num_unique, table, rows, dim, g, out,
+                       status);
+  };
+  if (vec)
+    gp ? launch(fr_number_kernel<4, true>) : launch(fr_number_kernel<4, false>);
+  else
+    gp ? launch(fr_number_kernel<1, true>) : launch(fr_number_kernel<1, false>);
+  ANNC_HIP_TRY(hipGetLastError());
+  return ANNC_OK;
 }
 
 // ---------------------------------------------------------------------------
@@ -231,14 +431,6 @@ __global__ void fo_min_kernel(const int64_t* __restrict__ keys, int64_t stride, 
   int32_t* f = first + (keys[i * stride] - kmin);
   if (__hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) > static_cast<int32_t>(i))
     atomicMin(f, static_cast<int32_t>(i));
-}
-
-__global__ void fo_mark_kernel(const int64_t* __restrict__ keys, int64_t stride, int64_t n,
-                               int64_t kmin, const int32_t* __restrict__ first,
-                               int32_t* __restrict__ first_mark) {
-  const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-  if (i >= n) return;
-  first_mark[i] = first[keys[i * stride] - kmin] == static_cast<int32_t>(i) ? 1 : 0;
 }
 
 // Without global atomics, for small ranges (the segment column of
@@ -286,44 +478,25 @@ __global__ void fo_merge_kernel(const int32_t* __restrict__ part, int nblk, int 
   first[r] = m;
 }
 
-// number[i] = inclusive count of first occurrences up to i
-__global__ void fo_output_kernel(const int64_t* __restrict__ keys, int64_t stride, int64_t n,
-                                 int64_t kmin, const int32_t* __restrict__ first,
-                                 const int32_t* __restrict__ number,
-                                 int32_t* __restrict__ indices, int64_t* __restrict__ unique,
-                                 int64_t* __restrict__ num_unique) {
-  const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-  if (i >= n) return;
-  const int64_t key = keys[i * stride];
-  const int32_t f = first[key - kmin];
-  const int32_t r = number[f] - 1;
-  indices[i] = r;
-  if (f == static_cast<int32_t>(i)) unique[r] = key;
-  if (i == n - 1) num_unique[0] = number[n - 1];
-}
-
 }  // namespace
 
 int first_occurrence_range(hipStream_t s, const int64_t* keys, int64_t stride, int64_t n,
                            int64_t kmin, int64_t range, int64_t* num_unique, int64_t* unique,
                            int32_t* indices) {
   ANNC_REQUIRE(n > 0 && n < INT_MAX && range >= 1, "bad first-occurrence size");
-  size_t scan = 0;
-  ANNC_HIP_TRY(hipcub::DeviceScan::InclusiveSum(nullptr, scan, (const int32_t*)nullptr,
-                                                (int32_t*)nullptr, (int)n, s));
+  int* status = stream_status(s);
+  if (!status) return set_error(ANNC_RESOURCE_EXHAUSTED, "status allocation failed");
   auto align = [](size_t x) { return (x + 255) & ~size_t(255); };
   const int64_t nblk = ceil_div(n, kFoBlock);
   const bool local = range <= kFoLdsRange && nblk <= kFoMaxBlocks;
   const size_t fb = align(sizeof(int32_t) * (size_t)range);
   const size_t n4 = align(sizeof(int32_t) * (size_t)n);
   const size_t pb = local ? align(sizeof(int32_t) * (size_t)(nblk * range)) : 0;
-  char* ws = static_cast<char*>(stream_workspace(s, fb + 2 * n4 + pb + align(scan)));
+  char* ws = static_cast<char*>(stream_workspace(s, fb + n4 + pb + fr_workspace(n)));
   if (!ws) return set_error(ANNC_RESOURCE_EXHAUSTED, "workspace allocation failed");
   int32_t* first = reinterpret_cast<int32_t*>(ws);
-  int32_t* mark = reinterpret_cast<int32_t*>(ws + fb);
-  int32_t* number = reinterpret_cast<int32_t*>(ws + fb + n4);
-  int32_t* part = reinterpret_cast<int32_t*>(ws + fb + 2 * n4);
-  void* tmp = ws + fb + 2 * n4 + pb;
+  int32_t* fpos = reinterpret_cast<int32_t*>(ws + fb);
+  int32_t* part = reinterpret_cast<int32_t*>(ws + fb + n4);
   const dim3 grid((unsigned)ceil_div(n, kThreads));
   if (local) {
     hipLaunchKernelGGL(fo_local_min_kernel, dim3((unsigned)nblk), dim3(kFoThreads),
@@ -340,14 +513,9 @@ int first_occurrence_range(hipStream_t s, const int64_t* keys, int64_t stride, i
     hipLaunchKernelGGL(fo_min_kernel, grid, dim3(kThreads), 0, s, keys, stride, n, kmin, first);
     ANNC_HIP_TRY(hipGetLastError());
   }
-  hipLaunchKernelGGL(fo_mark_kernel, grid, dim3(kThreads), 0, s, keys, stride, n, kmin, first,
-                     mark);
-  ANNC_HIP_TRY(hipGetLastError());
-  ANNC_HIP_TRY(hipcub::DeviceScan::InclusiveSum(tmp, scan, mark, number, (int)n, s));
-  hipLaunchKernelGGL(fo_output_kernel, grid, dim3(kThreads), 0, s, keys, stride, n, kmin, first,
-                     number, indices, unique, num_unique);
-  ANNC_HIP_TRY(hipGetLastError());
-  return ANNC_OK;
+  return first_numbering(s, FirstByKey{keys, stride, kmin, first}, keys, stride, n, fpos,
+                         ws + fb + n4 + pb, num_unique, unique, indices, nullptr, 0, 0, nullptr,
+                         status);
 }
 
 int unique_gather(hipStream_t s, const float* table, int64_t rows, int64_t dim,
@@ -357,47 +525,25 @@ int unique_gather(hipStream_t s, const float* table, int64_t rows, int64_t dim,
   if (!status) return set_error(ANNC_RESOURCE_EXHAUSTED, "status allocation failed");
   int64_t cap = 1024;
   while (cap < 2 * n) cap <<= 1;
-  size_t scan = 0;
-  ANNC_HIP_TRY(hipcub::DeviceScan::InclusiveSum(nullptr, scan, (const int32_t*)nullptr,
-                                                (int32_t*)nullptr, (int)n, s));
   auto align = [](size_t x) { return (x + 255) & ~size_t(255); };
   const size_t kb = align(sizeof(int64_t) * (size_t)(cap + 1));
   const size_t fb = align(sizeof(int32_t) * (size_t)(cap + 1));
   const size_t n4 = align(sizeof(int32_t) * (size_t)n);
-  char* ws = static_cast<char*>(stream_workspace(s, kb + fb + 3 * n4 + align(scan)));
+  char* ws = static_cast<char*>(stream_workspace(s, kb + fb + n4 + fr_workspace(n)));
   if (!ws) return set_error(ANNC_RESOURCE_EXHAUSTED, "workspace allocation failed");
   int64_t* tab_key = reinterpret_cast<int64_t*>(ws);
   int32_t* tab_first = reinterpret_cast<int32_t*>(ws + kb);
   int32_t* slot_of = reinterpret_cast<int32_t*>(ws + kb + fb);
-  int32_t* mark = reinterpret_cast<int32_t*>(ws + kb + fb + n4);
-  int32_t* number = reinterpret_cast<int32_t*>(ws + kb + fb + 2 * n4);
-  void* tmp = ws + kb + fb + 3 * n4;
-  const dim3 grid((unsigned)ceil_div(n, kThreads));
   hipLaunchKernelGGL(ug_clear_kernel, dim3((unsigned)ceil_div(cap + 1, kThreads)), dim3(kThreads),
                      0, s, tab_key, tab_first, cap + 1);
   ANNC_HIP_TRY(hipGetLastError());
   hipLaunchKernelGGL(ug_insert_kernel, dim3((unsigned)ceil_div(n, kUgBlock)), dim3(kUgThreads), 0, s,
                      keys, stride, n, cap, tab_key, tab_first, slot_of, status);
   ANNC_HIP_TRY(hipGetLastError());
-  hipLaunchKernelGGL(ug_mark_kernel, grid, dim3(kThreads), 0, s, slot_of, tab_first, n, mark);
-  ANNC_HIP_TRY(hipGetLastError());
-  ANNC_HIP_TRY(hipcub::DeviceScan::InclusiveSum(tmp, scan, mark, number, (int)n, s));
-  hipLaunchKernelGGL(ug_output_kernel, grid, dim3(kThreads), 0, s, keys, stride, n, slot_of,
-                     tab_first, number, indices, unique, num_unique);
-  ANNC_HIP_TRY(hipGetLastError());
-  if (dim > 0) {
-    int g = 1;
-    const bool vec = dim % 4 == 0 && ((reinterpret_cast<uintptr_t>(table) |
-                                       reinterpret_cast<uintptr_t>(out)) & 15) == 0;
-    const int64_t lanes = vec ? dim / 4 : dim;
-    while (g < 64 && g < lanes) g <<= 1;
-    if (vec)
-      launch_ug_gather<4>(s, g, table, rows, dim, unique, num_unique, n, out, status);
-    else
-      launch_ug_gather<1>(s, g, table, rows, dim, unique, num_unique, n, out, status);
-    ANNC_HIP_TRY(hipGetLastError());
-  }
-  return ANNC_OK;
+  // f(i) = tab_first[slot_of[i]], written over slot_of
+  return first_numbering(s, FirstBySlot{slot_of, tab_first}, keys, stride, n, slot_of,
+                         ws + kb + fb + n4, num_unique, unique, indices, table, rows, dim, out,
+                         status);
 }
 
 }  // namespace annc

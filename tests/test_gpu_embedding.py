@@ -645,6 +645,29 @@ def test_fused_gather_negative_and_huge_keys_group_correctly():
     assert to_host(didx).tolist() == [0, 1, 2, 0, 3, 1, 4]
 
 
+@pytest.mark.parametrize("n", [512 * 1024, 512 * 1024 + 4097, 2**24 + 3])
+def test_fused_gather_beyond_the_lds_prefix(n):
+    """Up to 2^19 keys (1024 blocks of 512 positions) the number workgroups
+    form the prefix of the block counts in LDS; beyond, a separate launch
+    forms it.  Checked against numpy.unique (first indices, inverse)."""
+    note(f"KPFusedGather n={n} (block prefix in LDS / separate launch)")
+    g = workloads.rng(n)
+    rows, dim = 3_000_000, 4
+    keys = g.integers(0, rows, size=n).astype(np.int64)
+    keys[n // 3] = rows - 1
+    u, first, inv = np.unique(keys, return_index=True, return_inverse=True)
+    order = np.argsort(first, kind="stable")
+    ref_u = u[order]
+    number = np.empty(len(order), np.int64)
+    number[order] = np.arange(len(order))
+    ref_idx = number[inv.reshape(-1)].astype(np.int32)
+    table = _formula_table_dev(rows, dim)
+    du, didx, drows = dev.unique_gather(table, to_dev(keys[:, None].copy()), col=0)
+    np.testing.assert_array_equal(to_host(du), ref_u)
+    np.testing.assert_array_equal(to_host(didx), ref_idx)
+    np.testing.assert_array_equal(to_host(drows), _formula_rows_host(ref_u, dim))
+
+
 def _formula_table_dev(rows, dim):
     """[rows, dim] float32 on the device with value ((r % 1000) - 500) * 0.001 + c,
     exactly reproducible on the host for any row subset."""
