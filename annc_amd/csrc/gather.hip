@@ -50,24 +50,6 @@ __global__ void ug_clear_kernel(int64_t* __restrict__ tab_key, int32_t* __restri
   tab_first[c] = INT_MAX;
 }
 
-// Probe for `key` from its hash, inserting it into a free slot if it is
-// new; returns the slot, or -1 after `cap` probes (cannot happen while at
-// most cap/2 distinct keys are inserted).  A slot's key never changes once
-// set, so a plain read that already shows a key decides without an atomic.
-__device__ __forceinline__ int64_t probe_insert(int64_t* tab_key, int64_t cap, int64_t key) {
-  int64_t h = static_cast<int64_t>(mix64(static_cast<uint64_t>(key)) & (uint64_t)(cap - 1));
-  for (int64_t probe = 0; probe < cap; ++probe) {
-    int64_t seen = __hip_atomic_load(tab_key + h, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    if (seen == kEmpty)
-      seen = static_cast<int64_t>(atomicCAS(reinterpret_cast<unsigned long long*>(tab_key + h),
-                                            static_cast<unsigned long long>(kEmpty),
-                                            static_cast<unsigned long long>(key)));
-    if (seen == kEmpty || seen == key) return h;
-    h = (h + 1) & (cap - 1);
-  }
-  return -1;
-}
-
 // Insert workgroups of 1024 threads over 2048 positions: a key that is
 // frequent in the data costs one global atomic per 2048 positions, not per
 // 256 (configs[2]'s ids: 42.5 -> 37.4 us for the whole unique + gather;
@@ -77,7 +59,9 @@ constexpr int kUgBlock = 2048;           // positions per workgroup
 constexpr int kUgLocal = 2 * kUgBlock;   // LDS table slots (+1 for the empty marker's value)
 
 // Slot of every position's key in the global table, whose slots keep their
-// key's smallest position.  Each workgroup first de-duplicates its 256
+// key's smallest position (open addressing, linear probing; capacity a
+// power of two >= 2n, so at most half the slots fill and every probe
+// sequence ends).  Each workgroup first de-duplicates its kUgBlock
 // positions in an LDS table (block minimum per key), then inserts each of
 // its distinct keys once: a key that is frequent in the data costs one
 // global CAS and one atomicMin per workgroup, not one per occurrence.
@@ -89,10 +73,16 @@ __global__ __launch_bounds__(kUgThreads) void ug_insert_kernel(
   __shared__ int32_t lfirst[kUgLocal + 1];
   __shared__ int32_t lslot[kUgLocal + 1];
   __shared__ int lempty;  // some position holds the empty marker's value
+  __shared__ int32_t llist[kUgBlock];  // used LDS slots
+  __shared__ int lcount;
   constexpr int kPer = kUgBlock / kUgThreads;
+  static_assert(kUgBlock <= 2 * kUgThreads, "at most two listed keys per thread");
   for (int l = threadIdx.x; l < kUgLocal; l += kUgThreads) lkey[l] = kEmpty;
   for (int l = threadIdx.x; l <= kUgLocal; l += kUgThreads) lfirst[l] = INT_MAX;
-  if (threadIdx.x == 0) lempty = 0;
+  if (threadIdx.x == 0) {
+    lempty = 0;
+    lcount = 0;
+  }
   __syncthreads();
   const int64_t b0 = (int64_t)blockIdx.x * kUgBlock;
   int local[kPer];
@@ -120,21 +110,62 @@ __global__ __launch_bounds__(kUgThreads) void ug_insert_kernel(
     local[u] = l;
   }
   __syncthreads();
+  // List the used LDS slots (at most one per position, so at most two per
+  // thread), then insert each listed key: a thread's two probe chains run
+  // side by side, each step one CAS that returns the slot's key, and the
+  // block minimum goes in with an atomicMin whose result nobody waits for.
   for (int l = threadIdx.x; l <= kUgLocal; l += kUgThreads) {
     const bool used = l < kUgLocal ? lkey[l] != kEmpty : lempty != 0;
-    if (!used) continue;
-    int64_t g = cap;  // the empty marker's value has the extra global slot
-    if (l < kUgLocal) {
-      g = probe_insert(tab_key, cap, lkey[l]);
-      if (g < 0) {  // reported, never hangs
-        atomicOr(status, 2);
-        g = cap;
-      }
+    const uint64_t m = __ballot(used);
+    int base = 0;
+    if ((threadIdx.x & 63) == 0 && m) base = atomicAdd(&lcount, __popcll(m));
+    base = __shfl(base, 0, 64);
+    if (used)
+      llist[base + __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32),
+                                             __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0))] = l;
+  }
+  __syncthreads();
+  const int cnt = lcount;
+  int sl[2];
+  int64_t hk[2], key2[2];
+  bool pend[2];
+#pragma unroll
+  for (int v = 0; v < 2; ++v) {
+    const int e = threadIdx.x + v * kUgThreads;
+    sl[v] = e < cnt ? llist[e] : -1;
+    pend[v] = sl[v] >= 0 && sl[v] < kUgLocal;
+    key2[v] = pend[v] ? lkey[sl[v]] : kEmpty;
+    hk[v] = pend[v] ? static_cast<int64_t>(mix64(static_cast<uint64_t>(key2[v])) &
+                                           (uint64_t)(cap - 1))
+                    : cap;  // the empty marker's value has the extra global slot
+  }
+  for (int64_t probe = 0; probe < cap && (pend[0] || pend[1]); ++probe) {
+    int64_t seen[2];
+#pragma unroll
+    for (int v = 0; v < 2; ++v)
+      seen[v] = pend[v] ? static_cast<int64_t>(atomicCAS(
+                              reinterpret_cast<unsigned long long*>(tab_key + hk[v]),
+                              static_cast<unsigned long long>(kEmpty),
+                              static_cast<unsigned long long>(key2[v])))
+                        : kEmpty;
+#pragma unroll
+    for (int v = 0; v < 2; ++v) {
+      if (!pend[v]) continue;
+      if (seen[v] == kEmpty || seen[v] == key2[v])
+        pend[v] = false;
+      else
+        hk[v] = (hk[v] + 1) & (cap - 1);
     }
-    const int32_t first = lfirst[l];
-    if (__hip_atomic_load(tab_first + g, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) > first)
-      atomicMin(tab_first + g, first);
-    lslot[l] = static_cast<int32_t>(g);
+  }
+#pragma unroll
+  for (int v = 0; v < 2; ++v) {
+    if (sl[v] < 0) continue;
+    if (pend[v]) {  // cap probes without a slot: reported, never hangs
+      atomicOr(status, 2);
+      hk[v] = cap;
+    }
+    atomicMin(tab_first + hk[v], lfirst[sl[v]]);
+    lslot[sl[v]] = static_cast<int32_t>(hk[v]);
   }
   __syncthreads();
 #pragma unroll
