@@ -504,9 +504,23 @@ __global__ void fo_merge_kernel(const int32_t* __restrict__ part, int nblk, int 
                                 int32_t* __restrict__ first) {
   const int r = blockIdx.x * kThreads + threadIdx.x;
   if (r >= range) return;
-  int32_t m = INT_MAX;
-  for (int b = 0; b < nblk; ++b) m = min(m, part[(int64_t)b * range + r]);
-  first[r] = m;
+  // eight independent loads in flight per step (a plain loop waited for
+  // each load before issuing the next)
+  int32_t m[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) m[j] = INT_MAX;
+  int b = 0;
+  for (; b + 8 <= nblk; b += 8) {
+    int32_t v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = part[(int64_t)(b + j) * range + r];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) m[j] = min(m[j], v[j]);
+  }
+  for (; b < nblk; ++b) m[0] = min(m[0], part[(int64_t)b * range + r]);
+#pragma unroll
+  for (int j = 1; j < 8; ++j) m[0] = min(m[0], m[j]);
+  first[r] = m[0];
 }
 
 }  // namespace
