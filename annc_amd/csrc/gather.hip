@@ -57,6 +57,9 @@ __global__ void ug_clear_kernel(int64_t* __restrict__ tab_key, int32_t* __restri
 constexpr int kUgThreads = 1024;         // threads of an insert workgroup
 constexpr int kUgBlock = 2048;           // positions per workgroup
 constexpr int kUgLocal = 2 * kUgBlock;   // LDS table slots (+1 for the empty marker's value)
+// Largest key count of the global table: capacity is the power of two at
+// or above 2n, and slot numbers (the empty marker `cap` too) are int32.
+constexpr int64_t kMaxUniqueKeys = int64_t(1) << 29;
 
 // Slot of every position's key in the global table, whose slots keep their
 // key's smallest position (open addressing, linear probing; capacity a
@@ -566,6 +569,8 @@ int first_occurrence_range(hipStream_t s, const int64_t* keys, int64_t stride, i
 int unique_gather(hipStream_t s, const float* table, int64_t rows, int64_t dim,
                   const int64_t* keys, int64_t stride, int64_t n, int64_t* num_unique,
                   int64_t* unique, int32_t* indices, float* out) {
+  // Slot numbers, the empty marker `cap` included, are int32: cap <= 2^30.
+  ANNC_REQUIRE(n <= kMaxUniqueKeys, "too many keys for the unique table (at most 2^29)");
   int* status = stream_status(s);
   if (!status) return set_error(ANNC_RESOURCE_EXHAUSTED, "status allocation failed");
   int64_t cap = 1024;
@@ -599,7 +604,7 @@ extern "C" int annc_hip_unique_gather(void* stream, const float* table, int64_t 
                                       float* out) {
   using namespace annc;
   ANNC_REQUIRE(rows >= 0 && dim >= 0 && n >= 0 && key_stride >= 1, "bad dimensions");
-  ANNC_REQUIRE(n < INT_MAX, "too many keys");
+  ANNC_REQUIRE(n <= kMaxUniqueKeys, "too many keys for the unique table (at most 2^29)");
   ANNC_REQUIRE(num_unique != nullptr, "null num_unique");
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (n == 0) {

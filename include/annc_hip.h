@@ -269,7 +269,8 @@ int annc_hip_pooling(void* stream, const int64_t* ids, const float* gathered, in
  * r-th distinct key, indices[i] the rank of keys[i], out[r, :] =
  * table[unique[r], :] (a zero row, and the stream's status word set, for a
  * key outside [0, rows)).  unique and out must hold n keys / n rows; the
- * count U is written to the device int64 *num_unique.  All device pointers,
+ * count U is written to the device int64 *num_unique.  n is at most 2^29
+ * (INVALID_ARGUMENT beyond, before any launch).  All device pointers,
  * asynchronous on `stream`. */
 int annc_hip_unique_gather(void* stream, const float* table, int64_t rows, int64_t dim,
                            const int64_t* keys, int64_t key_stride, int64_t n,

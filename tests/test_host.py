@@ -202,6 +202,19 @@ def test_hash_ops_reject_zero_buckets():
         tf_ops.kp_fused_sparse_embedding([b"a"], 0)
 
 
+@pytest.mark.parametrize("n", [(1 << 29) + 1, 1 << 30, (1 << 31) - 2])
+def test_unique_gather_rejects_key_counts_past_the_table_limit(n):
+    """Slot numbers of the unique table are int32 and its capacity is the
+    power of two at or above 2n, so n is capped at 2^29; the check runs before
+    any launch (no device pointers are touched)."""
+    import ctypes
+    lib = _lib.lib()
+    dummy = ctypes.c_void_p(16)
+    rc = lib.annc_hip_unique_gather(None, None, 0, 0, dummy, 1, n, dummy, dummy, dummy, None)
+    assert rc == _lib.INVALID_ARGUMENT
+    assert b"at most 2^29" in lib.annc_hip_last_error()
+
+
 def test_shape_info_encoding():
     # hlo_util.h:14-21 -- dims then minor_to_major; row-major [512,256] -> {512,256,1,0}
     assert xla.shape_info((512, 256)).tolist() == [512, 256, 1, 0]
