@@ -228,24 +228,33 @@ def test_relu_propagates_nan_and_clamps():
     assert out[2, 2] == 0.0
 
 
+def _check_tower_layers(tower, x_host, hidden, y, weights, biases, lda=None):
+    """Each layer against the oracle fed with the GPU's previous layer: the
+    ReLU layers at the GEMM bound, the sigmoid head at rtol 1e-4."""
+    h = x_host
+    outs = list(hidden) + [y]
+    for i in range(len(weights)):
+        out = outs[i]
+        act = 2 if i == len(weights) - 1 else 1
+        ref = ora.dense_layer(h, weights[i], biases[i], act)
+        note(f"  layer {i + 1}: [{h.shape[0]}x{h.shape[1]}] . [{weights[i].shape[0]}x"
+             f"{weights[i].shape[1]}] act {act}")
+        if act == 2:
+            np.testing.assert_allclose(out, ref, rtol=1e-4, atol=1e-6)
+        else:
+            assert_gemm_close(out, ref, gemm_bound(h, weights[i],
+                                                   np.broadcast_to(biases[i], ref.shape)))
+        h = out
+
+
 def test_config2_mlp_tower():
     note("config2 MLP tower")
     w = workloads.config2(seed=0)
     tower = MLPTower(w.weights, w.biases, device=device(), packed=True)
     x = to_dev(w.x)
     y = to_host(tower(x))
-    # layer by layer against the oracle fed with the GPU's previous layer
-    h = w.x
-    for i, layer in enumerate(tower.layers):
-        out = to_host(tower.buffers(x.shape[0])[i])
-        act = 2 if i == len(tower.layers) - 1 else 1
-        ref = ora.dense_layer(h, w.weights[i], w.biases[i], act)
-        if act == 2:
-            np.testing.assert_allclose(out, ref, rtol=1e-4, atol=1e-6)
-        else:
-            assert_gemm_close(out, ref, gemm_bound(h, w.weights[i],
-                                                   np.broadcast_to(w.biases[i], ref.shape)))
-        h = out
+    bufs = [to_host(b) for b in tower.buffers(x.shape[0])]
+    _check_tower_layers(tower, w.x, bufs[:-1], bufs[-1], w.weights, w.biases)
     np.testing.assert_allclose(y, ora.mlp_tower(w.x, w.weights, w.biases), rtol=1e-3, atol=1e-5)
 
 
@@ -255,11 +264,16 @@ def test_config5_wide_deep_graph():
     h = w.hashed
     cfg = WideDeepConfig()
     graph = WideDeepGraph(cfg, [to_dev(t) for t in h.tables], w.weights, w.biases, device=device())
-    y = to_host(graph(to_dev(h.ids), to_dev(h.offsets), to_dev(w.dense)))
+    y = to_host(graph(to_dev(h.ids), to_dev(h.offsets), to_dev(w.dense))).copy()
     emb = ora.hashed_embedding_bags(h.tables, h.num_buckets, h.ids, h.offsets, h.batch, 1, threads=8)
     x = np.concatenate([emb, w.dense], axis=1)
     concat = to_host(graph.concat_buffer(h.batch))[:, :x.shape[1]]
     np.testing.assert_array_equal(concat, x)  # embeddings bit-exact, dense copied
+    # the four GEMM layers at full size, each against the oracle fed with the
+    # GPU's previous layer: 4096x845 (concat rows, stride 848) -> 1024 -> 512
+    # -> 256 at the GEMM bound, then the 256 -> 1 sigmoid head
+    bufs = [to_host(b) for b in graph.tower.buffers(h.batch)]
+    _check_tower_layers(graph.tower, x, bufs[:-1], bufs[-1], w.weights, w.biases)
     np.testing.assert_allclose(y, ora.mlp_tower(x, w.weights, w.biases), rtol=1e-3, atol=1e-5)
     # dense features written straight into the concat buffer: same result, no copy
     graph.concat_buffer(h.batch).zero_()
