@@ -4,8 +4,8 @@
 Headline (`value`): BASELINE.json configs[1], the layout_matmul MLP tower
 1024-512-256-1 at batch 4096 in fp32, as whole-tower TFLOP/s.  One step =
 one forward of the tower (3 kernels, bias/ReLU/sigmoid fused) launched on
-one stream on device-resident inputs; a HIP-graph replay per step is
-reported beside it.
+one stream on device-resident inputs, after `--settle-ms` of untimed steps
+and `--warmup` more; a HIP-graph replay per step is reported beside it.
 
 `roofline` is the dominant kernel (layer 1, 4096x512x1024 packed-weight
 GEMM + bias + ReLU): 2*M*N*K flops per launch over its average duration,
@@ -109,6 +109,21 @@ def time_steps(step, steps: int, warmup: int):
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     return e0.elapsed_time(e1) / steps, wall / steps
+
+
+def settle_steps(step, settle_ms: float) -> int:
+    """Run `step` untimed for `settle_ms` of wall time (synchronising every
+    50 steps so the queue stays short); returns the number of steps."""
+    import torch
+    t0 = time.perf_counter()
+    n = 0
+    while time.perf_counter() - t0 < settle_ms * 1e-3:
+        step()
+        n += 1
+        if n % 50 == 0:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
+    return n
 
 
 def read_profile(profile: str) -> dict:
@@ -442,10 +457,25 @@ def bench_case(c: Case, replays: int = 5) -> dict:
            ("algorithmic_bytes" if c.bound == "hbm" else "flops"): c.work,
            "kernel_us": round(ms * 1e3, 3)}
     res.update(c.rate(ms))
+    if c.bound == "hbm" and "unique_row_bytes" in c.extra:
+        # bytes that must come from memory at least once (each distinct row
+        # once); Zipf-repeated rows are served from L2 / MALL
+        ub = c.extra["unique_row_bytes"] / (ms * 1e-3) / 1e9
+        res["GBps_unique_rows"] = round(ub, 1)
+        res["hbm_frac_unique_rows"] = round(ub / HBM_PEAK_GBS, 4)
+        if res["hbm_frac"] > 1.0:
+            # the algorithmic rate passes the peak only through cache hits:
+            # the headline fraction of this entry is the unique-row one
+            res["GBps_algorithmic"], res["hbm_frac_algorithmic"] = res["GBps"], res["hbm_frac"]
+            res["GBps"], res["hbm_frac"] = res["GBps_unique_rows"], res["hbm_frac_unique_rows"]
+            res["hbm_frac_basis"] = "unique_row_bytes"
     prof = read_profile(c.profile)
     res["profile"] = f"profiles/{c.profile}.md"
     if "rocprof_avg_ns" in prof:
         r = c.rate(prof["rocprof_avg_ns"] * 1e-6)
+        if res.get("hbm_frac_basis") == "unique_row_bytes":
+            ub = c.extra["unique_row_bytes"] / (prof["rocprof_avg_ns"] * 1e-9) / 1e9
+            r = {"GBps": round(ub, 1), "hbm_frac": round(ub / HBM_PEAK_GBS, 4)}
         res["rocprof_us"] = round(prof["rocprof_avg_ns"] * 1e-3, 3)
         res.update({k + "_rocprof": v for k, v in r.items()})
     if "traffic_bytes_per_launch" in prof:
@@ -459,7 +489,9 @@ def bench_case(c: Case, replays: int = 5) -> dict:
             res["traffic_GBps"] = round(tg, 1)
             res["traffic_hbm_frac"] = round(tg / HBM_PEAK_GBS, 4)
     res.update(c.extra)
-    log(f"{c.name}: {ms * 1e3:.2f} us, " + ", ".join(f"{k} {v}" for k, v in c.rate(ms).items()))
+    shown = ("GBps", "hbm_frac", "tflops", "mfma_frac", "samples_per_s")
+    log(f"{c.name}: {ms * 1e3:.2f} us, " + ", ".join(f"{k} {res[k]}" for k in shown if k in res)
+        + (" (on unique-row bytes)" if res.get("hbm_frac_basis") else ""))
     return res
 
 
@@ -475,12 +507,19 @@ def bench_tower(args, device, inp: Inputs):
     x = torch.from_numpy(w.x).to(device)
     batch = x.shape[0]
     flops = tower.flops(batch)
-    # One step = the 3-layer forward launched on one stream (3 kernels).  A
-    # HIP-graph replay per step is timed too: each graph launch adds a few us
-    # of boundary on the box, more than the host needs to enqueue 3 kernels.
+    # One step = the 3-layer forward launched on one stream (3 kernels).
+    # Untimed steps run for `settle_ms` first, then the `warmup` ones: after
+    # start-up the clocks need some ms of load before they settle (5 warm-up
+    # steps alone left the tower at 59.5 us/step, against 52.9 after 300 ms
+    # on the same box).  A HIP-graph replay per step is timed too: each graph
+    # launch adds a few us of boundary on the box, more than the host needs
+    # to enqueue 3 kernels.
+    settle = settle_steps(lambda: tower(x), args.settle_ms)
     ms, wall = time_steps(lambda: tower(x), args.steps, args.warmup)
-    log(f"tower: {ms * 1e3:.1f} us/step ({wall * 1e6:.1f} us wall)")
+    log(f"tower: {ms * 1e3:.1f} us/step ({wall * 1e6:.1f} us wall) after {args.settle_ms:.0f} ms "
+        f"({settle} steps) of settling and {args.warmup} warm-up steps")
     graph = CapturedGraph(tower, x)
+    settle_steps(graph.replay, args.settle_ms)
     graph_ms, _ = time_steps(graph.replay, args.steps, args.warmup)
     log(f"tower (graph replay per step): {graph_ms * 1e3:.1f} us/step")
 
@@ -510,6 +549,7 @@ def bench_tower(args, device, inp: Inputs):
     log(f"layer1 gemm: {k1_ms * 1e3:.2f} us, {achieved:.1f} TFLOP/s")
     value = flops / (ms * 1e-3) / 1e12
     return {"value": value, "ms": ms, "flops": flops, "batch": batch, "roofline": roofline,
+            "settle_steps": settle,
             "graph": {"us_per_step": round(graph_ms * 1e3, 2),
                       "tflops": round(flops / (graph_ms * 1e-3) / 1e12, 2)}}
 
@@ -696,16 +736,24 @@ def cpu_baseline(inp: Inputs):
             out[f"threads_{t}_ms"] = round(sec * 1e3, 3)
         return out
 
+    def show(key):
+        e = res[key]
+        log(f"cpu_baseline {key}: " + ", ".join(
+            f"{t} thread{'s' if t > 1 else ''} {e[f'threads_{t}']} {e['unit']} "
+            f"({e[f'threads_{t}_ms']} ms)" for t in threads))
+
     c1 = inp.get("config1")
     res["config1_matmul_add_relu"] = entry(
         lambda t: ora.matmul_add_relu(c1.e, c1.a, c1.b), 2.0 * 512 * 256 * 256, 1e12, "TFLOP/s",
         "configs[0] 512x256x256: memcpy of the materialised addend, sgemm beta=1, ReLU loop "
         "(gemm_rewriter.cc:249-281)", True)
+    show("config1_matmul_add_relu")
     c2 = inp.get("config2")
     flops2 = 2.0 * c2.x.shape[0] * sum(w.shape[0] * w.shape[1] for w in c2.weights)
     res["config2_tower"] = entry(
         lambda t: ora.mlp_tower(c2.x, c2.weights, c2.biases), flops2, 1e12, "TFLOP/s",
         "full configs[1] tower (batch 4096, 5.37 GFLOP): sgemm + bias/ReLU/sigmoid loops", True)
+    show("config2_tower")
     c3 = inp.get("config3")
     bags3, dim3 = c3.offsets.size - 1, c3.table.shape[1]
     bytes3 = _bag_bytes(int(c3.offsets[-1]), bags3, dim3)
@@ -715,6 +763,7 @@ def cpu_baseline(inp: Inputs):
             bytes3, 1e9, "GB/s (algorithmic bytes)",
             f"full configs[2] bag ({cname}): per-bag sequential row adds "
             "(embedding_fused_sparse_segment_reduce.cc:92-131), OpenMP over bags", False)
+        show(f"config3_bag_{cname}")
     c4 = inp.get("config4")
     nf4 = len(c4.tables)
     nnz4 = int(c4.offsets[-1])
@@ -728,6 +777,7 @@ def cpu_baseline(inp: Inputs):
         False)
     res["config4_hashed_bags"]["ids_per_s_threads_1"] = round(
         nnz4 / (res["config4_hashed_bags"]["threads_1_ms"] * 1e-3), 1)
+    show("config4_hashed_bags")
     c5 = inp.get("config5")
     h5 = c5.hashed
     nf5 = len(h5.tables)
@@ -746,6 +796,7 @@ def cpu_baseline(inp: Inputs):
         f"full configs[4] graph, batch {h5.batch}: {nf5} hashed bags (dim {h5.dim}, mean), concat "
         "with the 13 dense features, 3 x __matmul_add_relu (memcpy E, sgemm beta=1, ReLU), "
         "256->1 dot + sigmoid", True)
+    show("config5_wide_deep")
     ora.set_threads(1)
     top = res["config2_tower"]
     return {"value": top[f"threads_{cores}"], "unit": "TFLOP/s", "cores": cores, "kind": "port",
@@ -798,6 +849,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=500)
     # untimed steps: after start-up the clocks need a few ms of load to settle
     ap.add_argument("--warmup", type=int, default=500)
+    ap.add_argument("--settle-ms", type=float, default=300.0,
+                    help="untimed steps for this long before the warm-up steps (clocks)")
     ap.add_argument("--no-components", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--kernel", choices=CASES, default=None,
@@ -853,7 +906,8 @@ def main() -> int:
         "config": {"workload": "configs[1]: layout_matmul MLP tower 1024-512-256-1, fp32, "
                                "batch 4096, pre-packed weights, bias+ReLU fused, sigmoid out",
                    "batch": tower["batch"], "flops_per_step": tower["flops"],
-                   "step": "one 3-layer forward (3 kernels) launched on one stream"},
+                   "step": "one 3-layer forward (3 kernels) launched on one stream",
+                   "settle_ms": args.settle_ms, "settle_steps": tower["settle_steps"]},
         "roofline": tower["roofline"],
         "cpu_baseline": cpu,
         "components": components,
