@@ -17,7 +17,6 @@
 // exactly: the sum is bit-identical.  The ids and rows of up to kGroupRound
 // positions are loaded before the first add, so they are in flight together.
 #include <hip/hip_runtime.h>
-#include <hipcub/hipcub.hpp>
 
 #include <algorithm>
 #include <map>
@@ -25,6 +24,7 @@
 #include <utility>
 
 #include "common.h"
+#include "scan_sort.h"
 #include "embedding_impl.h"
 
 namespace annc {
@@ -1802,10 +1802,7 @@ int segment_reduce_plan(int64_t n, int64_t batch, int sorted_hint, hipStream_t s
   plan->path = SegPlan::kRadix;
   int end_bit = 1;
   while (end_bit < 32 && (1ull << end_bit) <= (uint64_t)batch) ++end_bit;  // batch fits too
-  size_t temp_bytes = 0;
-  ANNC_HIP_TRY(hipcub::DeviceRadixSort::SortPairs(nullptr, temp_bytes, (const uint32_t*)nullptr,
-                                                  (uint32_t*)nullptr, (const int32_t*)nullptr,
-                                                  (int32_t*)nullptr, (int)n, 0, end_bit, s));
+  const size_t temp_bytes = radix_sort_temp_bytes(n);
   const size_t nk = align256(sizeof(uint32_t) * (size_t)std::max<int64_t>(n, 1));
   plan->end_bit = end_bit;
   plan->temp_bytes = temp_bytes;
@@ -1973,19 +1970,20 @@ int segment_reduce_run(hipStream_t s, const float* data, int64_t rows, int64_t d
   int32_t* vals_out = reinterpret_cast<int32_t*>(ws + 3 * nk);
   int64_t* offsets = reinterpret_cast<int64_t*>(ws + 4 * nk);
   void* temp = ws + 4 * nk + off_bytes;
-  size_t temp_bytes = plan.temp_bytes;
   if (n > 0) {
     hipLaunchKernelGGL(make_keys_kernel, dim3((unsigned)ceil_div(n, kThreads)), dim3(kThreads), 0,
                        s, seg, stride, n, batch, keys_in, vals_in);
     ANNC_HIP_TRY(hipGetLastError());
-    ANNC_HIP_TRY(hipcub::DeviceRadixSort::SortPairs(temp, temp_bytes, keys_in, keys_out, vals_in,
-                                                    vals_out, (int)n, 0, plan.end_bit, s));
+    // sorted pairs end in keys_in / vals_in (the pointers follow the passes)
+    const int rc = radix_sort_pairs(s, &keys_in, &keys_out, &vals_in, &vals_out, n, plan.end_bit,
+                                    temp);
+    if (rc != ANNC_OK) return rc;
   }
   hipLaunchKernelGGL(seg_bounds_kernel<uint32_t>, dim3((unsigned)ceil_div(n + 1, kThreads)),
-                     dim3(kThreads), 0, s, keys_out, (int64_t)1, n, batch, offsets);
+                     dim3(kThreads), 0, s, keys_in, (int64_t)1, n, batch, offsets);
   ANNC_HIP_TRY(hipGetLastError());
   a.offsets = offsets;
-  a.perm = vals_out;
+  a.perm = vals_in;
   return launch_bag(a, s);
 }
 
@@ -2128,14 +2126,7 @@ int widen_i32(hipStream_t s, const int32_t* src, int64_t n, int64_t* dst) {
   return ANNC_OK;
 }
 
-size_t nonzero_scan_temp_bytes(int64_t count) {
-  size_t bytes = 0;
-  if (hipcub::DeviceScan::InclusiveSum(nullptr, bytes, (const int32_t*)nullptr, (int32_t*)nullptr,
-                                       (int)std::max<int64_t>(count, 1), (hipStream_t)0) !=
-      hipSuccess)
-    return 0;
-  return std::max<size_t>(bytes, 1);
-}
+size_t nonzero_scan_temp_bytes(int64_t count) { return scan_temp_bytes(count); }
 
 int nonzero_compact(hipStream_t s, const float* dense, int64_t count, int64_t dim,
                     const int64_t* seg_of_row, int one_d, int32_t* flags, int32_t* incl, void* tmp,
@@ -2145,7 +2136,9 @@ int nonzero_compact(hipStream_t s, const float* dense, int64_t count, int64_t di
   const dim3 grid((unsigned)ceil_div(count, kThreads));
   hipLaunchKernelGGL(nz_flag_kernel, grid, dim3(kThreads), 0, s, dense, count, flags);
   ANNC_HIP_TRY(hipGetLastError());
-  ANNC_HIP_TRY(hipcub::DeviceScan::InclusiveSum(tmp, tmp_bytes, flags, incl, (int)count, s));
+  ANNC_REQUIRE(tmp_bytes >= scan_temp_bytes(count), "scan scratch too small");
+  const int rc = inclusive_sum(s, flags, incl, count, tmp);
+  if (rc != ANNC_OK) return rc;
   if (out_idx) return nonzero_write(s, dense, count, dim, seg_of_row, one_d, flags, incl, cap,
                                     out_idx, out_val);
   return ANNC_OK;

@@ -17,11 +17,11 @@
 // v_mul_lo/v_mul_hi sequences, and `% num_buckets` uses a precomputed
 // invariant-divisor reciprocal instead of a 64-bit division loop.
 #include <hip/hip_runtime.h>
-#include <hipcub/hipcub.hpp>
 
 #include <algorithm>
 
 #include "common.h"
+#include "scan_sort.h"
 #include "embedding_impl.h"
 
 namespace annc {
@@ -1029,16 +1029,15 @@ int run_sparse_embedding(hipStream_t s, const int64_t* offsets, const int64_t* b
   hipLaunchKernelGGL(sparse_embedding_flags_kernel, grid, dim3(kThreads), 0, s, offsets, bucket, n,
                      keep);
   ANNC_HIP_TRY(hipGetLastError());
-  size_t temp_bytes = 0;
-  ANNC_HIP_TRY(hipcub::DeviceScan::ExclusiveSum(nullptr, temp_bytes, keep, pos, (int)n, s));
-  void* temp = stream_workspace(s, temp_bytes);
+  void* temp = stream_workspace(s, scan_temp_bytes(n));
   if (!temp) return set_error(ANNC_RESOURCE_EXHAUSTED, "workspace allocation failed");
-  ANNC_HIP_TRY(hipcub::DeviceScan::ExclusiveSum(temp, temp_bytes, keep, pos, (int)n, s));
+  int rc = exclusive_sum(s, keep, pos, n, temp);
+  if (rc != ANNC_OK) return rc;
   hipLaunchKernelGGL(sparse_embedding_scatter_kernel, grid, dim3(kThreads), 0, s, offsets, bucket,
                      keep, pos, n, indices, values, empty);
   ANNC_HIP_TRY(hipGetLastError());
   int32_t last[2];
-  const int rc = read_back(s, {{&last[0], pos + n - 1, sizeof(int32_t)},
+  rc = read_back(s, {{&last[0], pos + n - 1, sizeof(int32_t)},
                                {&last[1], keep + n - 1, sizeof(int32_t)}});
   if (rc != ANNC_OK) return rc;
   *num_values = (int64_t)last[0] + last[1];

@@ -127,6 +127,8 @@ SEG_ORDER_CASES = [
     ("mostly empty segments", 10000, 100),
     ("ids outside [0, batch) dropped", 1000, 30000),
     ("ids outside [0, batch) dropped, radix sort", 20000, 30000),
+    ("radix sort, 3 passes (18 key bits)", 2**17 + 5, 300_000),
+    ("radix sort, 4 passes (25 key bits)", 2**24 + 3, 300_000),
     ("sorted", 4096, 81857),
     ("two-level sort, 128 blocks", 4096, 131072),
     ("two-level sort, last block partial", 4096, 131073),
@@ -169,6 +171,21 @@ def test_device_segment_reduce_orders(what, batch, n, combiner):
         out = dev.segment_reduce(to_dev(data), to_dev(idx), to_dev(seg), batch, combiner,
                                  sorted_ids=True)
         np.testing.assert_array_equal(to_host(out), ref)
+
+
+def test_device_segment_reduce_radix_sort_long_scan():
+    """Radix-sort path over 2^26 + 123 positions: 16,385 blocks of 4096, so
+    the scan of the digit histograms (256 per block) spans 1025 tiles and
+    its tile-totals step walks two totals per thread; bit-exact against the
+    sequential loop."""
+    n, batch = 2**26 + 123, 70_000
+    note(f"device segment reduce: radix sort, long scan (batch {batch}, n {n})")
+    g = workloads.rng(77)
+    data = g.standard_normal((2000, 4)).astype(np.float32)
+    idx = g.integers(0, 2000, size=n, dtype=np.int64)
+    seg = g.integers(0, batch, size=n, dtype=np.int64)
+    out = dev.segment_reduce(to_dev(data), to_dev(idx), to_dev(seg), batch, 1)
+    np.testing.assert_array_equal(to_host(out), ora.segment_reduce(data, idx, seg, batch, 1))
 
 
 SORTED_CHUNK = 160  # positions per workgroup of the sorted-id kernel

@@ -140,9 +140,12 @@ def test_tf_embedding_with_hash_bucket_ops():
         np.testing.assert_array_equal(got, ora.dnn_embedding_with_hash_bucket(strs, weight[:600], 1000))
 
 
-def test_tf_sparse_embedding():
-    note("tf sparse embedding")
-    strs = [str(i).encode() for i in range(2000)] + [b""] * 3 + [b"\0x"]
+@pytest.mark.parametrize("count", [2000, 50_000])
+def test_tf_sparse_embedding(count):
+    """KPFusedSparseEmbedding against the oracle, bucket-0 quirk included;
+    50,000 ids make the compaction scan span 13 tiles of 4096."""
+    note(f"tf sparse embedding, {count} ids")
+    strs = [str(i).encode() for i in range(count)] + [b""] * 3 + [b"\0x"]
     got = tf_ops.kp_fused_sparse_embedding(strs, 7)
     ref = ora.sparse_embedding(strs, 7)
     for a, b in zip(got, ref):
