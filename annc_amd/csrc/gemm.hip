@@ -20,9 +20,13 @@
 //     ReLU (std::max(x, 0.f) semantics) or sigmoid before the single store.
 //   * Tiles are numbered so that each XCD (workgroup id mod 8) receives a
 //     contiguous run of tiles sharing A rows, keeping them in its own L2.
+//   * The packed pipeline also has a v_mfma_f32_16x16x4f32 form (16x16
+//     blocks), selected only by the ANNC_GEMM_PIPE tuning variable.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
+#include <cstdlib>
+#include <cstring>
 #include <type_traits>
 
 #include "common.h"
@@ -556,14 +560,23 @@ __device__ __forceinline__ int a_swizzle(int row) { return (row & 7) ^ ((row >> 
 }  // namespace pipe
 
 template <int WM, int WN, int BLK_M, int BLK_N, int S, int NACC, int KS, bool A16, bool BRM,
-          bool ZMAP>
+          bool ZMAP, bool MI16 = false>
 __global__ __launch_bounds__(64 * WM * WN * KS) void gemm_packed_pipe_kernel(GemmParams p) {
   static_assert(NACC == 1 || NACC == 2, "one or two accumulator chains");
   static_assert(KS == 1 || KS == 2, "one or two k groups");
+  // MI16: 16x16 accumulator blocks on v_mfma_f32_16x16x4f32 (one k group,
+  // packed B, K % 32 == 0).  A fragment step covers 16 k: lane l feeds k =
+  // 4*(l/16) + s at MFMA step s, so one 16-byte LDS read per operand block
+  // serves the 4 steps, from the same A and packed-B stage layouts.
+  static_assert(!MI16 || (KS == 1 && !BRM), "16x16 blocks: one k group, packed B");
+  constexpr int MB = MI16 ? 16 : 32;               // rows and columns of an MFMA block
+  constexpr int NR = MI16 ? 4 : 16;                // accumulator registers per block
+  using AccT = std::conditional_t<MI16, f32x4, f32x16>;
   constexpr int NT = WM * WN;                      // waves per k group
   constexpr int NW = NT * KS;
-  constexpr int NQ = 4 / KS;                       // 8-k quads per wave per k-block
-  constexpr int BM = WM * BLK_M * 32, BN = WN * BLK_N * 32;
+  constexpr int NQ = MI16 ? 2 : 4 / KS;            // fragment steps per wave per k-block
+  constexpr int BM = WM * BLK_M * MB, BN = WN * BLK_N * MB;
+  static_assert(BN % 32 == 0, "whole 32-column panels");
   constexpr int NA = BM / 8, NB = BN / 8, NBLK = NA + NB;  // 1 KiB blocks per stage
   static_assert(NBLK % NW == 0, "stage blocks split evenly over the waves");
   static_assert(S >= 3 && S <= 4, "3 or 4 stages: the next stage is published mid-stage");
@@ -618,10 +631,11 @@ __global__ __launch_bounds__(64 * WM * WN * KS) void gemm_packed_pipe_kernel(Gem
   const int panels = N >> 5;      // N % 32 == 0 on this path
 
   // bias of this lane's columns, fetched before the pipeline starts
+  const int fl = MI16 ? (lane & 15) : l32;  // this lane's row / column in an MFMA block
   float bias_v[BLK_N];
 #pragma unroll
   for (int j = 0; j < BLK_N; ++j) {
-    const int col = n0 + wn * BLK_N * 32 + j * 32 + l32;
+    const int col = n0 + (wn * BLK_N + j) * MB + fl;
     bias_v[j] = (p.bias && col < N) ? p.bias[col] : 0.0f;
   }
 
@@ -693,14 +707,14 @@ __global__ __launch_bounds__(64 * WM * WN * KS) void gemm_packed_pipe_kernel(Gem
   int a_off[BLK_M], a_swz[BLK_M];
 #pragma unroll
   for (int i = 0; i < BLK_M; ++i) {
-    const int trow = (wm * BLK_M + i) * 32 + l32;
+    const int trow = (wm * BLK_M + i) * MB + fl;
     a_off[i] = (trow >> 3) * 64 + (trow & 7) * 8;
     a_swz[i] = pipe::a_swizzle(trow);
   }
 
   // NACC = 2: even and odd k-steps accumulate into separate chains, so a wave
   // always has an independent MFMA to issue; the chains are added at the end
-  f32x16 acc[NACC][BLK_M][BLK_N];
+  AccT acc[NACC][BLK_M][BLK_N];
 #pragma unroll
   for (int c = 0; c < NACC; ++c)
 #pragma unroll
@@ -708,7 +722,7 @@ __global__ __launch_bounds__(64 * WM * WN * KS) void gemm_packed_pipe_kernel(Gem
 #pragma unroll
       for (int j = 0; j < BLK_N; ++j)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) acc[c][i][j][r] = 0.0f;
+        for (int r = 0; r < NR; ++r) acc[c][i][j][r] = 0.0f;
 
 #pragma unroll
   for (int s = 0; s < S - 1; ++s)
@@ -724,6 +738,19 @@ __global__ __launch_bounds__(64 * WM * WN * KS) void gemm_packed_pipe_kernel(Gem
     constexpr int HALF = QPS / 2;
     f32x4 af[2][BLK_M], bf[2][BLK_N];
     auto frag_at = [&](const f32x4* stage, int t, int buf) {
+      if constexpr (MI16) {
+        // 16-k step t: A chunk 4t + l/16 of row fl; packed B quad l/16,
+        // lanes 32t + 16*(block's half of its panel) + fl
+        const int sub = lane >> 4;
+#pragma unroll
+        for (int i = 0; i < BLK_M; ++i) af[buf][i] = stage[a_off[i] + ((4 * t + sub) ^ a_swz[i])];
+#pragma unroll
+        for (int j = 0; j < BLK_N; ++j) {
+          const int bj = wn * BLK_N + j;
+          bf[buf][j] = stage[(NA + (bj >> 1) * 4 + sub) * 64 + 32 * t + 16 * (bj & 1) + fl];
+        }
+        return;
+      }
       const int q = q0 + t;
 #pragma unroll
       for (int i = 0; i < BLK_M; ++i) af[buf][i] = stage[a_off[i] + ((4 * half + q) ^ a_swz[i])];
@@ -773,9 +800,14 @@ __global__ __launch_bounds__(64 * WM * WN * KS) void gemm_packed_pipe_kernel(Gem
 #pragma unroll
               for (int i = 0; i < BLK_M; ++i)
 #pragma unroll
-                for (int j = 0; j < BLK_N; ++j)
-                  acc[e % NACC][i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(
-                      af[b][i][e], bf[b][j][e], acc[e % NACC][i][j], 0, 0, 0);
+                for (int j = 0; j < BLK_N; ++j) {
+                  if constexpr (MI16)
+                    acc[e % NACC][i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(
+                        af[b][i][e], bf[b][j][e], acc[e % NACC][i][j], 0, 0, 0);
+                  else
+                    acc[e % NACC][i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(
+                        af[b][i][e], bf[b][j][e], acc[e % NACC][i][j], 0, 0, 0);
+                }
             // interleave the next quad's LDS reads with this quad's MFMAs
             constexpr int NDS = BLK_M + (BRM ? 4 : 1) * BLK_N, NMF = 4 * BLK_M * BLK_N;
             constexpr int NIL = NDS < NMF ? NDS : NMF;
@@ -802,7 +834,7 @@ __global__ __launch_bounds__(64 * WM * WN * KS) void gemm_packed_pipe_kernel(Gem
   }
 
   // K tail (K % 32 != 0): packed rows k >= 32*KT are row-major [K - 32*KT, N]
-  if (K & 31) {
+  if (!MI16 && (K & 31)) {
     const int kf = KT * 32;
     const int64_t tail_base = (int64_t)N * kf;
 #pragma unroll
@@ -832,9 +864,11 @@ __global__ __launch_bounds__(64 * WM * WN * KS) void gemm_packed_pipe_kernel(Gem
 #pragma unroll
         for (int i = 0; i < BLK_M; ++i)
 #pragma unroll
-          for (int j = 0; j < BLK_N; ++j)
-            acc[e % NACC][i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(
-                af[i][e], bf[j][e], acc[e % NACC][i][j], 0, 0, 0);
+          for (int j = 0; j < BLK_N; ++j) {
+            if constexpr (!MI16)
+              acc[e % NACC][i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(
+                  af[i][e], bf[j][e], acc[e % NACC][i][j], 0, 0, 0);
+          }
     }
   }
   if constexpr (NACC == 2) {
@@ -853,11 +887,14 @@ __global__ __launch_bounds__(64 * WM * WN * KS) void gemm_packed_pipe_kernel(Gem
     for (int i = 0; i < BLK_M; ++i) {
 #pragma unroll
       for (int j = 0; j < BLK_N; ++j) {
-        const int col = n0 + wn * BLK_N * 32 + j * 32 + l32;
+        const int col = n0 + (wn * BLK_N + j) * MB + fl;
         if (col >= N) continue;
 #pragma unroll
         for (int r = R0; r < R1; ++r) {
-          const int row = m0 + wm * BLK_M * 32 + i * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+          // 32x32 block: register r holds row 8*(r/4) + 4*(l/32) + r%4;
+          // 16x16 block: row 4*(l/16) + r
+          const int row = m0 + (wm * BLK_M + i) * MB +
+                          (MI16 ? 4 * (lane >> 4) + r : 8 * (r >> 2) + 4 * half + (r & 3));
           if (row >= M) continue;
           float v = acc[0][i][j][r];
           if (E) v += E[(int64_t)row * p.lde + col];
@@ -874,7 +911,7 @@ __global__ __launch_bounds__(64 * WM * WN * KS) void gemm_packed_pipe_kernel(Gem
   using I8 = std::integral_constant<int, 8>;
   using I16 = std::integral_constant<int, 16>;
   if constexpr (KS == 1) {
-    epilogue(I0{}, I16{});
+    epilogue(I0{}, std::integral_constant<int, NR>{});
   } else {
     // The two k groups hold partial sums of the same outputs.  Group g keeps
     // registers [8g, 8g+8) and hands the other eight to its partner through
@@ -1016,9 +1053,9 @@ int launch_tile(const GemmParams& p0, int64_t batch, hipStream_t stream) {
   return ANNC_OK;
 }
 
-template <int WM, int WN, int BMB, int BNB, int S, int NACC, int KS, bool BRM>
+template <int WM, int WN, int BMB, int BNB, int S, int NACC, int KS, bool BRM, bool MI16 = false>
 int launch_pipe(const GemmParams& p0, int64_t batch, hipStream_t stream) {
-  constexpr int BM = WM * BMB * 32, BN = WN * BNB * 32;
+  constexpr int BM = WM * BMB * (MI16 ? 16 : 32), BN = WN * BNB * (MI16 ? 16 : 32);
   GemmParams p = p0;
   p.tiles_m = (p.m + BM - 1) / BM;
   p.tiles_n = (p.n + BN - 1) / BN;
@@ -1028,18 +1065,18 @@ int launch_pipe(const GemmParams& p0, int64_t batch, hipStream_t stream) {
   const dim3 block(64 * WM * WN * KS);
   if (p.a_vec) {
     if (batch > 1)
-      hipLaunchKernelGGL((gemm_packed_pipe_kernel<WM, WN, BMB, BNB, S, NACC, KS, true, BRM, true>),
+      hipLaunchKernelGGL((gemm_packed_pipe_kernel<WM, WN, BMB, BNB, S, NACC, KS, true, BRM, true, MI16>),
                          grid, block, 0, stream, p);
     else
-      hipLaunchKernelGGL((gemm_packed_pipe_kernel<WM, WN, BMB, BNB, S, NACC, KS, true, BRM, false>),
+      hipLaunchKernelGGL((gemm_packed_pipe_kernel<WM, WN, BMB, BNB, S, NACC, KS, true, BRM, false, MI16>),
                          grid, block, 0, stream, p);
   } else {
     if (batch > 1)
-      hipLaunchKernelGGL((gemm_packed_pipe_kernel<WM, WN, BMB, BNB, S, NACC, KS, false, BRM, true>),
+      hipLaunchKernelGGL((gemm_packed_pipe_kernel<WM, WN, BMB, BNB, S, NACC, KS, false, BRM, true, MI16>),
                          grid, block, 0, stream, p);
     else
       hipLaunchKernelGGL(
-          (gemm_packed_pipe_kernel<WM, WN, BMB, BNB, S, NACC, KS, false, BRM, false>), grid,
+          (gemm_packed_pipe_kernel<WM, WN, BMB, BNB, S, NACC, KS, false, BRM, false, MI16>), grid,
           block, 0, stream, p);
   }
   ANNC_HIP_TRY(hipGetLastError());
@@ -1056,8 +1093,35 @@ int launch_pipe(const GemmParams& p0, int64_t batch, hipStream_t stream) {
 // a CU when there are at least two tiles per CU, hiding each one's ramp and
 // store phase under the other's MFMAs (measured: 8% faster at K = 256, 3% at
 // K = 512, 3% slower at K = 845).
+// ANNC_GEMM_PIPE selects 16x16-block tilings of the packed pipeline for
+// one-batch packed GEMMs with K % 32 == 0 (a tuning study; the default
+// tiling measured as fast or faster on every configs shape):
+//   "mi16"    128x64 tiles of 4 waves (64x32 per wave, one wave a SIMD),
+//             64x64 where 128x64 gives fewer than 256 tiles;
+//   "mi16w8"  128x64 tiles of 8 waves (32x32 per wave, two a SIMD),
+//             64x64 of 8 waves (16x32) likewise.
+// Read on every launch, so a process can compare the forms.
+int gemm_pipe_choice() {
+  const char* v = std::getenv("ANNC_GEMM_PIPE");
+  if (!v || !*v) return 0;
+  if (std::strcmp(v, "mi16") == 0) return 1;
+  if (std::strcmp(v, "mi16w8") == 0) return 2;
+  return 0;
+}
+
 template <bool BRM>
 int launch_pipe_tiles(const GemmParams& p, int64_t batch, hipStream_t stream) {
+  if constexpr (!BRM) {
+    const int choice = batch == 1 && (p.k & 31) == 0 ? gemm_pipe_choice() : 0;
+    if (choice) {
+      const bool big = ((int64_t)(p.m + 127) / 128) * ((p.n + 63) / 64) >= 256;
+      if (choice == 1)
+        return big ? launch_pipe<2, 2, 4, 2, 4, 1, 1, BRM, true>(p, batch, stream)
+                   : launch_pipe<2, 2, 2, 2, 4, 1, 1, BRM, true>(p, batch, stream);
+      return big ? launch_pipe<4, 2, 2, 2, 4, 1, 1, BRM, true>(p, batch, stream)
+                 : launch_pipe<4, 2, 1, 2, 4, 1, 1, BRM, true>(p, batch, stream);
+    }
+  }
   const int64_t cus = 256;
   auto tiles = [&](int bm, int bn) {
     return ((int64_t)(p.m + bm - 1) / bm) * ((p.n + bn - 1) / bn) * batch;

@@ -284,6 +284,26 @@ def test_config5_wide_deep_graph():
     np.testing.assert_array_equal(y2, y)
 
 
+@pytest.mark.parametrize("pipe", ["mi16", "mi16w8"])
+@pytest.mark.parametrize("m,n,k", [(4096, 512, 1024), (4096, 256, 512), (100, 96, 64),
+                                   (257, 160, 256), (4100, 64, 32)])
+def test_packed_gemm_16x16_blocks(pipe, m, n, k, monkeypatch):
+    """The 16x16-block forms of the packed pipeline (ANNC_GEMM_PIPE): k fed
+    as 4*(lane/16) + step from the 32x32 stage layouts, 16x16 accumulator
+    map in the epilogue; within the GEMM bound of OpenBLAS, edge tiles
+    included."""
+    note(f"packed GEMM, ANNC_GEMM_PIPE={pipe}, {m}x{n}x{k}")
+    g = workloads.rng(m + 3 * n + k)
+    a = g.standard_normal((m, k)).astype(np.float32)
+    b = (g.standard_normal((k, n)) / np.sqrt(k)).astype(np.float32)
+    bias = (g.standard_normal(n) * 0.1).astype(np.float32)
+    pw = dev.pack_weight(to_dev(b))
+    monkeypatch.setenv("ANNC_GEMM_PIPE", pipe)
+    out = to_host(dev.gemm(to_dev(a), pw, bias=to_dev(bias), epilogue=EPI_RELU))
+    ref = ora.dense_layer(a, b, bias, 1)
+    assert_gemm_close(out, ref, gemm_bound(a, b, np.broadcast_to(bias, ref.shape)))
+
+
 # ---------------------------------------------------------------- KPFusedBatchMatMulAddSigmoid
 import json  # noqa: E402
 import os  # noqa: E402
