@@ -316,8 +316,8 @@ def layout_matmul(model: Model) -> List[str]:
         if rhs is None or rhs not in model.variables:
             continue
         w = model.variables[rhs]
-        if w.ndim != 2 or _too_small(w):
-            continue
+        if not isinstance(w, np.ndarray) or w.ndim != 2 or _too_small(w):
+            continue  # (a bundle entry of a type the packer cannot read stays as it is)
         if nd.attrs.get("transpose_b") or nd.attrs.get("adj_y"):
             continue  # the packed format describes an untransposed [k, n] operand
         current = nd.attrs.get("rhs_format")

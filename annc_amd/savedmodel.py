@@ -36,7 +36,7 @@ from __future__ import annotations
 import os
 import struct
 from dataclasses import dataclass, field
-from typing import Dict, Iterable, List, Optional, Tuple
+from typing import Dict, Iterable, List, Optional, Tuple, Union
 
 import numpy as np
 
@@ -229,7 +229,22 @@ _DT_OF = {np.dtype(v): k for k, v in _NP_OF.items()}
 
 
 class DType(str):
-    """A `type` attr value ("DT_FLOAT"), kept apart from string attrs."""
+    """A `type` attr value ("DT_FLOAT"), kept apart from string attrs.
+    `enum` is its DataType number, kept for values this module has no name
+    for (float8, int4, the reference types 101+), which then round-trip as
+    "DT_<number>"."""
+
+    def __new__(cls, name: str, enum: Optional[int] = None):
+        obj = super().__new__(cls, name)
+        if enum is None:
+            if name in DTYPES:
+                enum = DTYPES[name]
+            elif name.startswith("DT_") and name[3:].isdigit():
+                enum = int(name[3:])
+            else:
+                raise ValueError(f"unknown DataType {name!r}")
+        obj.enum = int(enum)
+        return obj
 
 
 @dataclass
@@ -256,7 +271,7 @@ def decode_attr(buf: bytes):
         if num == 5 and wt == VARINT:
             return bool(v)
         if num == 6 and wt == VARINT:
-            return DType(DTYPE_NAMES.get(v, f"DT_{v}"))
+            return DType(DTYPE_NAMES.get(v, f"DT_{v}"), v)
     return RawAttr(buf)
 
 
@@ -265,7 +280,7 @@ def encode_attr(value) -> bytes:
     if isinstance(value, RawAttr):
         return value.data
     if isinstance(value, DType):
-        m.add(6, VARINT, DTYPES[str(value)])
+        m.add(6, VARINT, value.enum)
     elif isinstance(value, bool):
         m.add(5, VARINT, int(value))
     elif isinstance(value, int):
@@ -535,9 +550,25 @@ def bundle_paths(prefix: str) -> Tuple[str, str]:
     return prefix + ".index", prefix + ".data-00000-of-00001"
 
 
-def read_bundle(prefix: str) -> Dict[str, np.ndarray]:
+@dataclass
+class OpaqueTensor:
+    """A bundle entry this module does not decode (strings, resources,
+    quantized types): its BundleEntryProto and data bytes, written back
+    unchanged.  `dtype` is the DataType name, `shape` the dims."""
+    entry: bytes
+    raw: bytes
+    dtype: str
+    shape: Tuple[int, ...]
+
+    @property
+    def ndim(self) -> int:
+        return len(self.shape)
+
+
+def read_bundle(prefix: str) -> Dict[str, Union[np.ndarray, OpaqueTensor]]:
     """name -> array of every numeric tensor of a one-shard little-endian
-    bundle (checksums verified)."""
+    bundle (checksums verified); other tensors (DT_STRING lookup-table keys
+    of TF1 checkpoints and the like) come back as OpaqueTensor."""
     index_path, data_path = bundle_paths(prefix)
     with open(index_path, "rb") as f:
         entries = read_table(f.read())
@@ -556,8 +587,6 @@ def read_bundle(prefix: str) -> Dict[str, np.ndarray]:
             continue
         e = Msg.parse(val)
         dt = e.get(1, 0)
-        if dt not in _NP_OF:
-            raise ValueError(f"{key.decode()}: dtype {DTYPE_NAMES.get(dt, dt)} is not supported")
         if e.all(7):
             raise ValueError(f"{key.decode()}: sliced tensors are not supported")
         shape = shape_of(e.get(2, b""))
@@ -568,21 +597,38 @@ def read_bundle(prefix: str) -> Dict[str, np.ndarray]:
         crc = e.get(6)
         if crc is not None and unmask_crc(crc) != crc32c_fast(raw):
             raise ValueError(f"{key.decode()}: tensor checksum mismatch")
+        if dt not in _NP_OF:
+            out[key.decode()] = OpaqueTensor(bytes(val), bytes(raw),
+                                             DTYPE_NAMES.get(dt, f"DT_{dt}"), shape)
+            continue
         arr = np.frombuffer(raw, dtype=_NP_OF[dt]).reshape(shape)
         out[key.decode()] = arr.copy()
     return out
 
 
-def write_bundle(prefix: str, tensors: Dict[str, np.ndarray]) -> None:
-    """One shard, tensors in key order, each at an 8-byte aligned offset
-    (TensorFlow aligns nothing but any offset is valid; alignment keeps the
-    data shard easy to map)."""
+def write_bundle(prefix: str, tensors: Dict[str, Union[np.ndarray, OpaqueTensor]]) -> None:
+    """One shard, tensors in key order, each at the next offset of the data
+    shard; OpaqueTensor entries keep their proto and bytes, with the new
+    offset and size."""
     index_path, data_path = bundle_paths(prefix)
     os.makedirs(os.path.dirname(index_path) or ".", exist_ok=True)
     data = bytearray()
     items = []
     for name in sorted(tensors):
-        arr = np.asarray(tensors[name])  # (ascontiguousarray would make a scalar 1-D)
+        t = tensors[name]
+        if isinstance(t, OpaqueTensor):
+            fields = Msg.parse(t.entry).fields
+            off = len(data)
+            data += t.raw
+            place = []  # offset (4) and size (5) in field order; proto3 omits zeros
+            if off:
+                place.append((4, VARINT, off))
+            if t.raw:
+                place.append((5, VARINT, len(t.raw)))
+            e = Msg([f for f in fields if f[0] < 4] + place + [f for f in fields if f[0] > 5])
+            items.append((name.encode(), e.serialize()))
+            continue
+        arr = np.asarray(t)  # (ascontiguousarray would make a scalar 1-D)
         if not arr.flags.c_contiguous:
             arr = arr.copy(order="C")
         if arr.dtype not in _DT_OF:

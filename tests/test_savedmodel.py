@@ -122,6 +122,51 @@ def test_bundle_round_trip_and_checks(tmp_path):
         sm.read_bundle(prefix)
 
 
+def test_attr_unknown_datatype_round_trips():
+    """DataType values without a name here (24: a float8 type, 101: a
+    reference type) decode to DType("DT_<n>") and encode to the same bytes."""
+    for v in (24, 101):
+        raw = sm.Msg([(6, sm.VARINT, v)]).serialize()
+        d = sm.decode_attr(raw)
+        assert isinstance(d, sm.DType) and d == f"DT_{v}" and d.enum == v
+        assert sm.encode_attr(d) == raw
+    assert sm.DType("DT_FLOAT").enum == 1 and sm.DType("DT_RESOURCE").enum == 20
+    with pytest.raises(ValueError):
+        sm.DType("DT_NOT_A_TYPE")
+
+
+def test_bundle_keeps_string_entries(tmp_path):
+    """A DT_STRING entry (a TF1 lookup table's keys) reads as OpaqueTensor and
+    is written back byte for byte, its proto fields kept, beside re-encoded
+    numeric tensors."""
+    prefix = str(tmp_path / "variables" / "variables")
+    w = np.arange(12, dtype=np.float32).reshape(3, 4)
+    sm.write_bundle(prefix, {"w": w})
+    index = dict(sm.read_table(open(prefix + ".index", "rb").read()))
+    data = open(prefix + ".data-00000-of-00001", "rb").read()
+    # TF's string tensor layout: varint lengths, then the bytes; opaque here
+    raw = bytes([3, 5]) + b"abc" + b"hello"
+    off = len(data)
+    entry = sm.Msg([(1, sm.VARINT, 7), (2, sm.LEN, sm.shape_proto((2,))), (4, sm.VARINT, off),
+                    (5, sm.VARINT, len(raw)), (6, sm.FIXED32, sm.mask_crc(sm.crc32c(raw)))])
+    index[b"table/keys"] = entry.serialize()
+    open(prefix + ".index", "wb").write(sm.write_table(sorted(index.items())))
+    open(prefix + ".data-00000-of-00001", "wb").write(data + raw)
+    back = sm.read_bundle(prefix)
+    keys = back["table/keys"]
+    assert isinstance(keys, sm.OpaqueTensor) and keys.dtype == "DT_STRING"
+    assert keys.shape == (2,) and keys.raw == raw
+    np.testing.assert_array_equal(back["w"], w)
+    out = str(tmp_path / "out" / "variables")
+    sm.write_bundle(out, back)
+    again = sm.read_bundle(out)
+    assert again["table/keys"].raw == raw and again["table/keys"].shape == (2,)
+    e = sm.Msg.parse(dict(sm.read_table(open(out + ".index", "rb").read()))[b"table/keys"])
+    nums = [f[0] for f in e.fields]  # field order kept; offset 0 left out (proto3)
+    assert nums == sorted(nums) and 6 in nums and e.get(1) == 7 and e.get(5) == len(raw)
+    np.testing.assert_array_equal(again["w"], w)
+
+
 def test_saved_model_graph_round_trip(tmp_path):
     nodes = [sm.GraphNode("x", "Placeholder", [], {"dtype": sm.DType("DT_FLOAT")}),
              sm.GraphNode("w", "VariableV2", [], {"dtype": sm.DType("DT_FLOAT")}),
