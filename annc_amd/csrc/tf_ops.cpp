@@ -86,32 +86,10 @@ int embed_hash_bucket(const char* bytes, const int64_t* offsets, int64_t batch,
 namespace annc {
 namespace {
 
-// Phase-1 results of KPFusedSparseSegmentReduceNonzero, kept for the phase-2
-// call that follows on the same thread and device with the same operands
-// (as one TensorFlow Compute() makes them: count, allocate, write), so that
-// phase 2 only writes the listed values.  Buffers grow as needed and, like
-// the thread's pinned and staging buffers, are kept until the process ends
-// (releasing them at thread exit could run after the HIP runtime has shut
-// down).
-struct NzKey {
-  const void* data;
-  int data_rank;
-  int64_t rows, dim;
-  const void* indices;
-  int indices_is_64;
-  int64_t num_indices;
-  const void* slice;
-  int64_t slice_rows, slice_cols;
-  int32_t col;
-  int combiner;
-  bool operator==(const NzKey& o) const {
-    return data == o.data && data_rank == o.data_rank && rows == o.rows && dim == o.dim &&
-           indices == o.indices && indices_is_64 == o.indices_is_64 &&
-           num_indices == o.num_indices && slice == o.slice && slice_rows == o.slice_rows &&
-           slice_cols == o.slice_cols && col == o.col && combiner == o.combiner;
-  }
-};
-
+// Device scratch of KPFusedSparseSegmentReduceNonzero, per thread and
+// device.  Buffers grow as needed and, like the thread's pinned and staging
+// buffers, are kept until the process ends (releasing them at thread exit
+// could run after the HIP runtime has shut down).
 struct DeviceBuf {
   char* p = nullptr;
   size_t size = 0;
@@ -129,14 +107,10 @@ struct DeviceBuf {
   }
 };
 
-struct NzStash {
-  bool valid = false;
-  NzKey key{};
-  int64_t batch = 0, count = 0;
-  int32_t nnz = 0;
+struct NzScratch {
   DeviceBuf uniq_buf, dense_buf;  // segments by first appearance; dense, flags, incl, scan temp
 };
-thread_local std::map<int, NzStash> t_nz;
+thread_local std::map<int, NzScratch> t_nz;
 
 size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
@@ -253,39 +227,10 @@ int annc_kp_fused_sparse_segment_reduce_nonzero(
   if (!s) return set_error(ANNC_INTERNAL, "no HIP stream");
   int device = 0;
   ANNC_HIP_TRY(hipGetDevice(&device));
-  NzStash& nz = t_nz[device];
-  const NzKey key{data, data_rank, rows, dim, indices, indices_is_64, num_indices,
-                  slice_input, slice_dims[0], slice_dims[1], col, combiner};
-  if (write && nz.valid && nz.key == key) {
-    // phase 2 after phase 1 on the same operands: write what phase 1 listed
-    nz.valid = false;
-    if (output_shape) {
-      rc = write_i32(output_shape, static_cast<int32_t>(nz.batch));
-      if (rc == ANNC_OK && !one_d) rc = write_i32(output_shape + 1, static_cast<int32_t>(dim));
-      if (rc != ANNC_OK) return rc;
-    }
-    ANNC_REQUIRE(nz.nnz == cap, "output size %lld differs from the %lld nonzero values",
-                 (long long)cap, (long long)nz.nnz);
-    if (cap > 0) {
-      Staging st(s);
-      int32_t* d_out_idx = static_cast<int32_t*>(
-          st.out(output_indices, sizeof(int32_t) * cap * (one_d ? 1 : 2)));
-      float* d_out_val = static_cast<float*>(st.out(output_nonzero, sizeof(float) * cap));
-      if (st.status() != ANNC_OK) return st.status();
-      const float* dense = reinterpret_cast<const float*>(nz.dense_buf.p);
-      const size_t vb = align256(sizeof(float) * (size_t)nz.count);
-      const int32_t* flags = reinterpret_cast<const int32_t*>(nz.dense_buf.p + vb);
-      const int32_t* incl = reinterpret_cast<const int32_t*>(nz.dense_buf.p + 2 * vb);
-      rc = nonzero_write(s, dense, nz.count, dim, reinterpret_cast<const int64_t*>(nz.uniq_buf.p),
-                         one_d, flags, incl, cap, d_out_idx, d_out_val);
-      if (rc != ANNC_OK) return rc;
-      rc = st.finish();
-      if (rc != ANNC_OK) return rc;
-    }
-    *num_nonzero = nz.nnz;
-    return set_error(ANNC_OK, "");
-  }
-  nz.valid = false;
+  NzScratch& nz = t_nz[device];
+  // Phase 2 recomputes from the operands (they may have changed since phase
+  // 1); the result is deterministic, so an unchanged input gives phase 1's
+  // count.
   Staging st(s);
   const int64_t stride = slice_dims[1];
   const int64_t* d_slice = static_cast<const int64_t*>(
@@ -335,8 +280,7 @@ int annc_kp_fused_sparse_segment_reduce_nonzero(
   const float* d_data = static_cast<const float*>(st.in(data, sizeof(float) * rows * dim));
   const void* d_idx = st.in(indices, (indices_is_64 ? 8 : 4) * (size_t)num_indices);
   const int64_t count = nseg * dim;
-  // dense values, flags, their scan and the scan's temporary storage, kept
-  // for a phase-2 call
+  // dense values, flags, their scan and the scan's temporary storage
   const size_t vb = align256(sizeof(float) * (size_t)count);
   const size_t tmp_bytes = nonzero_scan_temp_bytes(count);
   char* db = nz.dense_buf.get(3 * vb + align256(std::max<size_t>(tmp_bytes, 1)));
@@ -379,13 +323,6 @@ int annc_kp_fused_sparse_segment_reduce_nonzero(
   if (write && cap > 0) {
     rc = st.finish();
     if (rc != ANNC_OK) return rc;
-  }
-  if (!write) {
-    nz.valid = true;
-    nz.key = key;
-    nz.batch = batch;
-    nz.count = count;
-    nz.nnz = nnz;
   }
   *num_nonzero = nnz;
   return set_error(ANNC_OK, "");

@@ -343,11 +343,8 @@ int annc_kp_fused_sparse_segment_reduce(const float* data, int data_rank, const 
  * *num_nonzero = the number of listed values.  Phase 2: *num_nonzero holds
  * that count on entry and output_indices int32 [count, 1] (1-D: segment) or
  * [count, 2] (2-D: segment, dim) and output_nonzero f32[count] are written.
- * A phase 2 that follows phase 1 on the same thread and device with the same
- * operands (addresses, shapes, begin column, combiner) writes the values
- * phase 1 listed instead of recomputing them, so the operands' contents must
- * not change between the two calls (as within one TF Compute()); any other
- * phase 2 recomputes.
+ * Phase 2 recomputes from its operands; it is refused (INVALID_ARGUMENT)
+ * when their count differs from *num_nonzero.
  * Errors: the reference OP_REQUIRES messages verbatim; indices outside the
  * data rows are reported (the reference reads them unchecked). */
 int annc_kp_fused_sparse_segment_reduce_nonzero(

@@ -498,17 +498,16 @@ def _nonzero_args(data, indices, slice_input, rows, dim, n, combiner, shape, nnz
             2, _lib.ptr(sdims), _lib.ptr(begin), 2, combiner, _lib.ptr(shape), _lib.ptr(nnz))
 
 
-@pytest.mark.parametrize("reuse", [True, False])
-def test_tf_segment_reduce_nonzero_short_phase2_buffer(reuse):
+@pytest.mark.parametrize("between", [False, True])
+def test_tf_segment_reduce_nonzero_short_phase2_buffer(between):
     """A phase-2 call whose buffers hold one value fewer than phase 1
     counted is refused with the count mismatch, and writes nothing past the
-    buffers it was given (a guard word after them keeps its value): both when
-    phase 2 takes phase 1's kept results (reuse) and when a phase 1 on other
-    operands came in between, so phase 2 recomputes and its write kernel
-    must stop at the buffer's end itself."""
+    buffers it was given (a guard word after them keeps its value; the write
+    kernel stops at the buffer's end itself), with or without a phase 1 on
+    other operands in between."""
     import ctypes
     from annc_amd import _lib
-    note(f"KPFusedSparseSegmentReduceNonzero short phase-2 buffer (reuse={reuse})")
+    note(f"KPFusedSparseSegmentReduceNonzero short phase-2 buffer (between={between})")
     g = workloads.rng(35)
     n, rows, dim = 500, 50, 4
     data = to_dev(g.standard_normal((rows, dim)).astype(np.float32))
@@ -526,7 +525,7 @@ def test_tf_segment_reduce_nonzero_short_phase2_buffer(reuse):
     _lib.check(lib.annc_kp_fused_sparse_segment_reduce_nonzero(*args, None, None))
     count = int(nnz[0])
     assert count > 1
-    if not reuse:  # phase 1 of other operands (the other combiner) in between
+    if between:  # phase 1 of other operands (the other combiner) in between
         keep, nnz2, shape2 = [], np.zeros(1, np.int64), np.zeros(2, np.int32)
         _lib.check(lib.annc_kp_fused_sparse_segment_reduce_nonzero(
             *_nonzero_args(data, indices, slice_input, rows, dim, n, 1, shape2, nnz2, keep),
@@ -546,9 +545,9 @@ def test_tf_segment_reduce_nonzero_short_phase2_buffer(reuse):
 
 
 def test_tf_segment_reduce_nonzero_phase2_after_other_operands():
-    """Phase 1 on A, phase 1 on B, phase 2 on A: the results kept from B's
-    phase 1 must not be written for A, so A's phase 2 recomputes and
-    matches the oracle; then phase 1 and 2 on B reuse B's results."""
+    """Phase 1 on A, phase 1 on B, phase 2 on A, then phase 1 and 2 on B and
+    phase 2 on B again: every phase 2 matches the oracle of its own
+    operands."""
     from annc_amd import _lib
     note("KPFusedSparseSegmentReduceNonzero phase 2 after other operands")
     g = workloads.rng(36)
@@ -568,7 +567,7 @@ def test_tf_segment_reduce_nonzero_phase2_after_other_operands():
         _lib.check(lib.annc_kp_fused_sparse_segment_reduce_nonzero(
             *_nonzero_args(dd, di, ds, rows, dim, n, 0, shape, nnz, keep), None, None))
         counts.append(int(nnz[0]))
-    for k in (0, 1, 1):  # phase 2 on A (recomputed), phase 2 on B (reused), B again
+    for k in (0, 1, 1):  # phase 2 on A, phase 1 + 2 on B, phase 2 on B again
         data, idx, seg, dd, di, ds = cases[k]
         if k == 1:
             _lib.check(lib.annc_kp_fused_sparse_segment_reduce_nonzero(
@@ -584,6 +583,38 @@ def test_tf_segment_reduce_nonzero_phase2_after_other_operands():
         np.testing.assert_array_equal(shape, want[0])
         np.testing.assert_array_equal(to_host(out_idx), want[1])
         np.testing.assert_array_equal(to_host(out_val), want[2])
+
+
+def test_tf_segment_reduce_nonzero_operands_changed_between_phases():
+    """Phase 1, then the data and indices change in place (same addresses,
+    shapes and nonzero count), then phase 2: phase 2 lists the new values."""
+    from annc_amd import _lib
+    note("KPFusedSparseSegmentReduceNonzero operands changed in place between phases")
+    g = workloads.rng(37)
+    n, rows, dim = 2000, 100, 4
+    data = g.standard_normal((rows, dim)).astype(np.float32) + 3.0  # no zero sums
+    idx = g.integers(0, rows, size=n).astype(np.int32)
+    seg = g.integers(0, 50, size=n).astype(np.int64)
+    dd, di = to_dev(data), to_dev(idx)
+    ds = to_dev(np.stack([np.zeros(n, np.int64), seg], axis=1))
+    lib, keep = _lib.lib(), []
+    shape, nnz = np.zeros(2, np.int32), np.zeros(1, np.int64)
+    _lib.check(lib.annc_kp_fused_sparse_segment_reduce_nonzero(
+        *_nonzero_args(dd, di, ds, rows, dim, n, 1, shape, nnz, keep), None, None))
+    count = int(nnz[0])
+    data2 = data * 2.0 + 1.0
+    idx2 = idx[::-1].copy()
+    dd.copy_(to_dev(data2))
+    di.copy_(to_dev(idx2))
+    want = ora.segment_reduce_nonzero(data2, idx2, seg, 1)
+    assert want[1].shape[0] == count
+    out_idx = torch.full((count, 2), -1, dtype=torch.int32, device=device())
+    out_val = torch.full((count,), -1.0, dtype=torch.float32, device=device())
+    _lib.check(lib.annc_kp_fused_sparse_segment_reduce_nonzero(
+        *_nonzero_args(dd, di, ds, rows, dim, n, 1, shape, nnz, keep),
+        _lib.ptr(out_idx), _lib.ptr(out_val)))
+    np.testing.assert_array_equal(to_host(out_idx), want[1])
+    np.testing.assert_array_equal(to_host(out_val), want[2])
 
 
 def test_tf_segment_reduce_nonzero_index_out_of_range():
