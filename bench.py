@@ -282,6 +282,30 @@ def make_case(name: str, device, inp: Inputs) -> Case:
                     f"bag_kernel_config3_{'mean' if comb else 'sum'}", launches=200,
                     nnz=nnz, unique_rows=uniq,
                     unique_row_bytes=8 * nnz + 8 * (bags + 1) + 4 * dim * uniq + 4 * dim * bags)
+    if name in ("bag_phase_empty", "bag_phase_hotrow"):
+        # the configs[2] bag kernel on inputs that end its dependent chain
+        # early: every bag empty (launch, offsets read, zero rows stored), or
+        # every id naming row 0 (launch, offsets, ids, rows that all hit one
+        # line of L2, store); beside bag_sum (rows from L2 / MALL) and
+        # bag_sum_cold (rows from HBM) they split the kernel's time by hop
+        w = inp.get("config3")
+        table = t(w.table)
+        bags, dim = w.offsets.size - 1, w.table.shape[1]
+        out = torch.empty((bags, dim), dtype=torch.float32, device=device)
+        if name == "bag_phase_empty":
+            offs = torch.zeros(bags + 1, dtype=torch.int64, device=device)
+            ids = t(w.ids[:1])
+            return Case(name, lambda i: dev.embedding_bag(table, ids, offs, 0, out=out),
+                        8 * (bags + 1) + 4 * dim * bags, "hbm",
+                        "configs[2] bag kernel, every bag empty: launch, offsets, zero rows "
+                        "stored", "bag_kernel_config3_phases", launches=200)
+        offs = t(w.offsets)
+        ids = torch.zeros(int(w.offsets[-1]), dtype=torch.int64, device=device)
+        return Case(name, lambda i: dev.embedding_bag(table, ids, offs, 0, out=out),
+                    _bag_bytes(int(w.offsets[-1]), bags, dim), "hbm",
+                    "configs[2] bag kernel, configs[2] offsets, every id = row 0: launch, "
+                    "offsets, ids, rows from one L2 line, store", "bag_kernel_config3_phases",
+                    launches=200)
     if name in ("hashed", "hashed_cold", "hashed_nohash"):
         w = inp.get("config4")
         ids, offs = t(w.ids), t(w.offsets)
@@ -439,8 +463,9 @@ def make_case(name: str, device, inp: Inputs) -> Case:
 
 
 CASES = ("tower", "widedeep", "gemm_l1", "gemm_l2", "gemm_l3", "gemm_small", "gemm_e2e_l1", "batch_matmul",
-         "bag_sum", "bag_mean", "bag_sum_cold", "hashed", "hashed_cold", "hashed_nohash",
-         "hashed_dim32", "sparse_embedding2", "pooling", "segment_reduce_sorted",
+         "bag_sum", "bag_mean", "bag_sum_cold", "bag_phase_empty", "bag_phase_hotrow", "hashed",
+         "hashed_cold", "hashed_nohash", "hashed_dim32", "sparse_embedding2", "pooling",
+         "segment_reduce_sorted",
          "segment_reduce_any", "hash_bucket", "copy", "bag_stream", "torch_mm_l1",
          "gather_probe", "gather_probe_cold")
 # the cases reported under `components` (gemm_l1 is the roofline, copy the calibration)
