@@ -96,8 +96,6 @@ _PROTOTYPES = {
                                               _i64, _c_void_p]),
     "annc_hip_unique_gather": (_i32, [_c_void_p, _c_void_p, _i64, _i64, _c_void_p, _i64, _i64,
                                       _c_void_p, _c_void_p, _c_void_p, _c_void_p]),
-    "annc_hip_probe_random_rows": (_i32, [_c_void_p, _c_void_p, _i64, _i64, _i64, _i64,
-                                          _c_void_p]),
     "annc_kp_fused_gather": (_i32, [_c_void_p, _i32, _c_void_p, _c_void_p, _i32, _c_void_p,
                                     _c_void_p, _i64, _c_void_p, _c_void_p, _c_void_p, _c_void_p]),
     "annc_kp_fused_batch_matmul_add_sigmoid": (_i32, [_c_void_p, _i32, _c_void_p, _c_void_p,

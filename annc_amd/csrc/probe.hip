@@ -7,10 +7,13 @@
 // fabric for rows of up to 128 bytes) when nothing else limits the kernel:
 // the ceiling against which the embedding-bag kernels' random gathers are
 // compared.  Every thread writes one sum, so no load is dead.
+//
+// Built into its own library, libannc_probe.so (bench.py loads it), and not
+// part of the operator library or its header.  Returns 0, or 3 for
+// arguments it refuses, or 13 when the launch fails.
 #include <hip/hip_runtime.h>
 
-#include "annc_hip.h"
-#include "common.h"
+#include <cstdint>
 
 namespace annc {
 namespace {
@@ -45,16 +48,15 @@ __global__ __launch_bounds__(kThreads) void probe_random_rows_kernel(const float
 }  // namespace
 }  // namespace annc
 
-extern "C" int annc_hip_probe_random_rows(void* stream, const float* table, int64_t rows,
-                                          int64_t dim, int64_t blocks, int64_t rows_per_group,
-                                          float* out) {
+extern "C" int annc_probe_random_rows(void* stream, const float* table, int64_t rows,
+                                      int64_t dim, int64_t blocks, int64_t rows_per_group,
+                                      float* out) {
   using namespace annc;
-  ANNC_REQUIRE(table && out, "null pointer");
-  ANNC_REQUIRE(rows >= 1 && rows < (int64_t(1) << 32), "rows must be in [1, 2^32)");
-  ANNC_REQUIRE(dim == 16 || dim == 32 || dim == 64, "dim must be 16, 32 or 64");
-  ANNC_REQUIRE(blocks >= 1 && blocks < (int64_t(1) << 31), "bad block count");
-  ANNC_REQUIRE(rows_per_group >= 8 && rows_per_group % 8 == 0 && rows_per_group < (1 << 30),
-               "rows_per_group must be a positive multiple of 8");
+  if (!table || !out) return 3;
+  if (rows < 1 || rows >= (int64_t(1) << 32)) return 3;
+  if (dim != 16 && dim != 32 && dim != 64) return 3;
+  if (blocks < 1 || blocks >= (int64_t(1) << 31)) return 3;
+  if (rows_per_group < 8 || rows_per_group % 8 != 0 || rows_per_group >= (1 << 30)) return 3;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int iters = static_cast<int>(rows_per_group);
   auto go = [&](auto kernel) {
@@ -67,6 +69,5 @@ extern "C" int annc_hip_probe_random_rows(void* stream, const float* table, int6
     go(probe_random_rows_kernel<8, 8>);
   else
     go(probe_random_rows_kernel<16, 8>);
-  ANNC_HIP_TRY(hipGetLastError());
-  return set_error(ANNC_OK, "");
+  return hipGetLastError() == hipSuccess ? 0 : 13;
 }

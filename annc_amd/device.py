@@ -159,19 +159,6 @@ def segment_reduce(data: torch.Tensor, indices: torch.Tensor, segment_ids: torch
     return out
 
 
-def probe_random_rows(table: torch.Tensor, blocks: int, rows_per_group: int,
-                      out: torch.Tensor, stream=None) -> None:
-    """Measurement kernel: random row gathers from `table` [rows, dim]
-    (dim 16/32/64) at their steady-state rate; `out` holds blocks*256
-    floats.  blocks * 256 / (dim/4) * rows_per_group rows per launch."""
-    _require_cuda(table, out)
-    rows, dim = table.shape
-    if out.numel() < blocks * 256:
-        raise ValueError("out must hold blocks * 256 floats")
-    check(_lib.lib().annc_hip_probe_random_rows(stream_ptr(stream), ptr(table), rows, dim, blocks,
-                                                rows_per_group, ptr(out)))
-
-
 def unique_gather(table: torch.Tensor, keys: torch.Tensor, col: int = 0, stream=None):
     """KPFusedGather engine on device tensors: keys [N, C] (or [N]) int64,
     column `col`.  Returns (unique int64[U], indices int32[N], rows [U, dim])

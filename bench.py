@@ -142,6 +142,33 @@ def read_profile(profile: str) -> dict:
     return out
 
 
+def probe_random_rows(table, blocks: int, rows_per_group: int, out) -> None:
+    """The random-row probe of libannc_probe.so (a measurement kernel built
+    beside the operator library, not part of it): random row gathers from
+    `table` [rows, dim] (dim 16/32/64) at their steady-state rate; `out`
+    holds blocks*256 floats; blocks * 256 / (dim/4) * rows_per_group rows per
+    launch, on torch's current stream."""
+    import ctypes
+    import torch
+    global _PROBE
+    if "_PROBE" not in globals():
+        path = os.path.join(ROOT, "annc_amd", "lib", "libannc_probe.so")
+        if not os.path.exists(path):
+            raise RuntimeError(f"{path} is not built (make -C annc_amd/csrc)")
+        _PROBE = ctypes.CDLL(path)
+        _PROBE.annc_probe_random_rows.restype = ctypes.c_int
+        _PROBE.annc_probe_random_rows.argtypes = [ctypes.c_void_p, ctypes.c_void_p] + \
+            [ctypes.c_int64] * 4 + [ctypes.c_void_p]
+    rows, dim = table.shape
+    if out.numel() < blocks * 256:
+        raise ValueError("out must hold blocks * 256 floats")
+    rc = _PROBE.annc_probe_random_rows(torch.cuda.current_stream().cuda_stream, table.data_ptr(),
+                                       rows, dim, blocks, rows_per_group, out.data_ptr())
+    if rc != 0:
+        raise ValueError(f"annc_probe_random_rows refused its arguments (status {rc}): dim 16, "
+                         "32 or 64, rows_per_group a positive multiple of 8")
+
+
 # ---------------------------------------------------------------- cases
 class Inputs:
     """Benchmark inputs, generated once per process (seed 0)."""
@@ -446,7 +473,7 @@ def make_case(name: str, device, inp: Inputs) -> Case:
         blocks, per = 2048, 40
         out = torch.empty(blocks * 256, dtype=torch.float32, device=device)
         n_rows = blocks * 64 * per
-        return Case(name, lambda i: dev.probe_random_rows(table, blocks, per, out),
+        return Case(name, lambda i: probe_random_rows(table, blocks, per, out),
                     64 * n_rows, "hbm",
                     f"random-row probe: {n_rows} rows of 64 B at uniform random positions of a "
                     f"[{rows_n} x 16] table ({rows_n * 64 / 1e6:.0f} MB), 8 in flight per 4-lane "

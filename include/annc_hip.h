@@ -411,18 +411,6 @@ int annc_kp_fused_sparse_embedding(const char* bytes, const int64_t* offsets, in
                                    int64_t* output_values, uint8_t* empty_row_indicator,
                                    int64_t* output_shape, int64_t* num_values);
 
-/* ------------------------------------------------------------------------ */
-/* Measurement (no counterpart in the reference: a diagnostic for the       */
-/* benchmark, not an operator).                                             */
-/* ------------------------------------------------------------------------ */
-/* Random row gathers at their steady-state rate: `blocks` workgroups of 256
- * lanes; every group of dim/4 lanes reads rows_per_group rows of
- * table[rows, dim] at uniformly random positions, 8 in flight, with no
- * dependent index loads; out receives one float per lane (blocks * 256).
- * dim 16, 32 or 64; rows_per_group a multiple of 8.  Device pointers,
- * asynchronous on `stream`. */
-int annc_hip_probe_random_rows(void* stream, const float* table, int64_t rows, int64_t dim,
-                               int64_t blocks, int64_t rows_per_group, float* out);
 
 #ifdef __cplusplus
 }  /* extern "C" */

@@ -795,13 +795,14 @@ def test_random_row_probe_reads_what_it_counts(dim):
     """The measurement kernel behind bench.py's gather_probe cases: every lane
     sums rows_per_group 16-byte chunks of a table of ones, so each lane's
     output is exactly 4 * rows_per_group (and the grid covers `out`)."""
+    import bench
     note(f"random-row probe, dim {dim}")
     table = torch.ones((5000, dim), dtype=torch.float32, device=device())
     out = torch.full((3 * 256,), -1.0, dtype=torch.float32, device=device())
-    dev.probe_random_rows(table, 3, 24, out)
+    bench.probe_random_rows(table, 3, 24, out)
     np.testing.assert_array_equal(to_host(out), np.full(3 * 256, 96.0, np.float32))
-    with pytest.raises(Exception, match="multiple of 8"):
-        dev.probe_random_rows(table, 3, 12, out)
+    with pytest.raises(ValueError, match="multiple of 8"):
+        bench.probe_random_rows(table, 3, 12, out)
 
 
 def test_tf_ops_from_concurrent_threads():
