@@ -586,7 +586,7 @@ def bench_tower(args, device, inp: Inputs):
     achieved = k1_flops / (k1_ms * 1e-3) / 1e12
     prof = read_profile("gemm_layer1_4096x512x1024")
     roofline = {
-        "kernel": "gemm_packed_pipe_kernel<4,2,1,1,4,2,1,true,false,false> (layer 1: 4096x512x1024 packed B + bias + ReLU)",
+        "kernel": "gemm_packed_pipe_kernel<4,2,1,1,4,2,1,true,false,false,false> (layer 1: 4096x512x1024 packed B + bias + ReLU)",
         "bound": "mfma",
         "achieved": round(achieved, 3),
         "peak": FP32_MFMA_PEAK_TFLOPS,
