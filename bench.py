@@ -653,7 +653,7 @@ def bench_nonzero(device, inp: Inputs):
     """KPFusedSparseSegmentReduceNonzero on configs[2] in TF form (positions
     shuffled, segment ids in column 1 of slice_input), device tensors, mean:
     median wall time of the two-phase op (phase 1 counts the nonzeros and
-    reads the count back; phase 2 writes the values phase 1 kept),
+    reads the count back; phase 2 recomputes and writes the listed values),
     and of phase 1 alone."""
     import ctypes
     import numpy as np
@@ -692,7 +692,8 @@ def bench_nonzero(device, inp: Inputs):
                         f"{int(vals.numel())} nonzero values listed",
             "two_phase_wall_us_median": round(statistics.median(ts) * 1e6, 1),
             "phase1_wall_us_median": round(statistics.median(t1) * 1e6, 1),
-            "note": "each phase synchronises; phase 2 writes the values phase 1 kept"}
+            "note": "each phase synchronises; phase 2 recomputes from its operands and writes "
+                    "the values"}
 
 
 def bench_config5(device, inp: Inputs, steps: int):
