@@ -127,6 +127,7 @@ SEG_ORDER_CASES = [
     ("mostly empty segments", 10000, 100),
     ("ids outside [0, batch) dropped", 1000, 30000),
     ("ids outside [0, batch) dropped, radix sort", 20000, 30000),
+    ("radix sort, 16 key bits exactly (2 passes), ids outside [0, batch) dropped", 2**16 - 1, 200_000),
     ("radix sort, 3 passes (18 key bits)", 2**17 + 5, 300_000),
     ("radix sort, 4 passes (25 key bits)", 2**24 + 3, 300_000),
     ("sorted", 4096, 81857),

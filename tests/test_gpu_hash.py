@@ -140,10 +140,11 @@ def test_tf_embedding_with_hash_bucket_ops():
         np.testing.assert_array_equal(got, ora.dnn_embedding_with_hash_bucket(strs, weight[:600], 1000))
 
 
-@pytest.mark.parametrize("count", [2000, 50_000])
+@pytest.mark.parametrize("count", [0, 2000, 4092, 50_000])
 def test_tf_sparse_embedding(count):
     """KPFusedSparseEmbedding against the oracle, bucket-0 quirk included;
-    50,000 ids make the compaction scan span 13 tiles of 4096."""
+    the compaction scan over 4 ids, 2004, exactly one tile of 4096, and
+    50,004 (13 tiles)."""
     note(f"tf sparse embedding, {count} ids")
     strs = [str(i).encode() for i in range(count)] + [b""] * 3 + [b"\0x"]
     got = tf_ops.kp_fused_sparse_embedding(strs, 7)
