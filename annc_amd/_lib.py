@@ -76,6 +76,10 @@ _PROTOTYPES = {
                              _c_void_p, _i64, _i64,
                              _c_void_p, _i32,
                              _c_void_p, _i64, _i64]),
+    "annc_hip_dense_score": (_i32, [_c_void_p, _i64, _i64, _i64, _c_void_p, _i64,
+                                    _c_void_p, _c_void_p, _i32,
+                                    _c_void_p, _c_void_p, _i32,
+                                    _c_void_p, _i64, _c_void_p, _i64]),
     "annc_hip_embedding_bag": (_i32, [_c_void_p, _c_void_p, _i64, _i64, _c_void_p, _i32,
                                       _c_void_p, _i64, _i32, _c_void_p, _i64]),
     "annc_hip_segment_reduce": (_i32, [_c_void_p, _c_void_p, _i64, _i64, _c_void_p, _i32,

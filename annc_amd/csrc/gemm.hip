@@ -1175,6 +1175,168 @@ int launch_gemm(const GemmParams& p, int64_t batch, hipStream_t stream) {
   return launch_tile<2, 2, 1, 1, PACKED>(p, batch, stream);
 }
 
+// ---------------------------------------------------------------------------
+// Tower tail: a dense layer on packed weights (K -> N, bias, activation)
+// and the N -> 1 scoring layer after it, in one kernel.
+//   * A workgroup owns 16 rows and all N columns, so a row's scoring dot
+//     needs no other workgroup: no atomics, no second launch, and every
+//     row's sums run in one fixed order.  M = 4096 gives 256 workgroups.
+//   * NW = N/16 waves; wave w computes the 16-column block w on
+//     v_mfma_f32_16x16x4f32.  A 16-k step feeds k = 4*(l/16) + s to lane l
+//     at MFMA step s, so one 16-byte read per operand covers 4 steps.
+//   * The 16 rows of A sit in LDS whole (row stride K + 4 floats: the 16
+//     rows of a fragment read start 4 banks apart), written a round at a
+//     time: a round is N k-columns of the 16 rows, one float4 per thread,
+//     loaded into registers one round ahead, then one barrier.
+//   * B streams from L2 straight into registers, two k-blocks ahead, with
+//     buffer loads: each lane's float4 of the packed format (layout_pack.h)
+//     is the operand of 4 MFMA steps.  Every workgroup reads all of B
+//     (K*N*4 bytes), twice the operand bytes of a 64x64-tiled layer, and on
+//     the 4096x256x512 layer the loop is bound by that stream: global loads
+//     instead of buffer loads took 12.1 us against 10.8 us, and deeper
+//     prefetch (3 to 6 blocks) was slower as well.
+//   * Workgroups of one XCD start at different rounds (rotating the k
+//     order), so that XCD's L2 serves different B blocks at a time.
+//   * Epilogue: bias and activation per element (optionally stored as the
+//     hidden layer), times the score weight, summed over the wave's 16
+//     columns by DPP and then over the waves in wave order through LDS;
+//     score bias and activation last.
+constexpr int kScoreRows = 16;
+constexpr int kScoreMaxK = 2048;
+
+template <int NW, int KMAX>
+__global__ __launch_bounds__(64 * NW) void dense_score_kernel(
+    const float* __restrict__ A, int64_t lda, int M, int K, const float* __restrict__ B,
+    const float* __restrict__ bias, int epilogue, const float* __restrict__ w_score,
+    const float* __restrict__ bias_score, int score_epilogue, float* __restrict__ H,
+    int64_t ldh, float* __restrict__ out, int64_t ldo) {
+  constexpr int N = 16 * NW;
+  constexpr int T = 64 * NW;   // threads
+  constexpr int RK = N;        // k-columns per round: T float4s over 16 rows
+  constexpr int BPR = RK / 32; // 32-k blocks per round
+  constexpr int TPR = T / 16;  // threads per row in a round
+  static_assert(BPR % 2 == 0, "two-block B ring");
+  __shared__ __attribute__((aligned(16))) float a_lds[kScoreRows * (KMAX + 4)];
+  __shared__ float red[NW][kScoreRows];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lane >> 4, c = lane & 15;
+  const int m0 = blockIdx.x * kScoreRows;
+  const int RS = K + 4;
+  const int KT = K >> 5;
+  const int R = K / RK;
+  // visit round r is round (r + ro) % R; ro differs between workgroups of
+  // one XCD (workgroups are dealt to the 8 XCDs round-robin)
+  const int ro = (int)((blockIdx.x >> 3) % (unsigned)R);
+
+  // this thread's A float4 of every round: row arow_t, k-chunk ac4
+  const int arow_t = tid / TPR, ac4 = tid % TPR;
+  const float* a_src = A + (int64_t)min(m0 + arow_t, M - 1) * lda + 4 * ac4;
+  float* a_dst = a_lds + arow_t * RS + 4 * ac4;
+
+  // B: wave w's 16 columns are half (w & 1) of 32-column panel w/2; lane
+  // (g, c) reads the float4 of quad g, lane 16*(w & 1) + c, 16-k half h
+  // 128h floats further (layout_pack.h)
+  const __amdgpu_buffer_rsrc_t brs =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(B), 0, K * N * 4, 0x00020000);
+  const int b_off = ((wave >> 1) * KT * 1024 + 256 * g + 4 * (16 * (wave & 1) + c)) * 4;
+  auto load_b = [&](int t, int h) {
+    return __builtin_bit_cast(
+        f32x4, __builtin_amdgcn_raw_buffer_load_b128(brs, b_off + (t * 1024 + 128 * h) * 4, 0, 0));
+  };
+
+  int ar = ro;  // round being visited
+  f32x4 a_next = *reinterpret_cast<const f32x4*>(a_src + ar * RK);
+  f32x4 bq[2][2];
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    bq[s][0] = load_b(ar * BPR + s, 0);
+    bq[s][1] = load_b(ar * BPR + s, 1);
+  }
+  f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  const float* a_frag = a_lds + c * RS + 4 * g;
+  for (int r = 0; r < R; ++r) {
+    const int an = (ar + 1 == R) ? 0 : ar + 1;  // next round visited
+    *reinterpret_cast<f32x4*>(a_dst + ar * RK) = a_next;
+    if (r + 1 < R) a_next = *reinterpret_cast<const f32x4*>(a_src + an * RK);
+    __syncthreads();
+#pragma unroll
+    for (int tb = 0; tb < BPR; ++tb) {
+      const int t = ar * BPR + tb;
+      const f32x4 a0 = *reinterpret_cast<const f32x4*>(a_frag + 32 * t);
+      const f32x4 a1 = *reinterpret_cast<const f32x4*>(a_frag + 32 * t + 16);
+      const int s = tb & 1;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a0[e], bq[s][0][e], acc, 0, 0, 0);
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a1[e], bq[s][1][e], acc, 0, 0, 0);
+      // refill this slot with the block visited two blocks later
+      if (tb + 2 < BPR) {
+        bq[s][0] = load_b(t + 2, 0);
+        bq[s][1] = load_b(t + 2, 1);
+      } else if (r + 1 < R) {
+        const int tn = an * BPR + tb + 2 - BPR;
+        bq[s][0] = load_b(tn, 0);
+        bq[s][1] = load_b(tn, 1);
+      }
+    }
+    ar = an;
+  }
+
+  // rows 4g .. 4g+3, column 16*wave + c of this wave's block
+  const int col = 16 * wave + c;
+  const float bj = bias ? bias[col] : 0.0f;
+  const float wj = w_score[col];
+  float part[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const float v = apply_epilogue(acc[r] + bj, epilogue);
+    const int row = m0 + 4 * g + r;
+    if (H && row < M) __builtin_nontemporal_store(v, H + (int64_t)row * ldh + col);
+    float sum = v * wj;
+    sum = dpp_add<0x128>(sum);  // row_ror:8
+    sum = dpp_add<0x124>(sum);  // row_ror:4
+    sum = dpp_add<0x04E>(sum);  // quad_perm [2,3,0,1]
+    sum = dpp_add<0x0B1>(sum);  // quad_perm [1,0,3,2]
+    part[r] = sum;
+  }
+  if (c == 0) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) red[wave][4 * g + r] = part[r];
+  }
+  __syncthreads();
+  if (wave == 0 && lane < kScoreRows) {
+    float sum = 0.0f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) sum += red[w][lane];
+    if (bias_score) sum += bias_score[0];
+    const int row = m0 + lane;
+    if (row < M) out[(int64_t)row * ldo] = apply_epilogue(sum, score_epilogue);
+  }
+}
+
+template <int NW>
+void launch_dense_score(hipStream_t s, int kmax, dim3 grid, const float* a, int64_t lda, int m,
+                        int k, const float* b, const float* bias, int epilogue,
+                        const float* w_score, const float* bias_score, int score_epilogue,
+                        float* hidden, int64_t ldh, float* out, int64_t ldo) {
+  const dim3 block(64 * NW);
+#define ANNC_SCORE_LAUNCH(KMAX)                                                                 \
+  hipLaunchKernelGGL((dense_score_kernel<NW, KMAX>), grid, block, 0, s, a, lda, m, k, b, bias, \
+                     epilogue, w_score, bias_score, score_epilogue, hidden, ldh, out, ldo)
+  if (kmax <= 512)
+    ANNC_SCORE_LAUNCH(512);
+  else if (kmax <= 1024)
+    ANNC_SCORE_LAUNCH(1024);
+  else
+    ANNC_SCORE_LAUNCH(kScoreMaxK);
+#undef ANNC_SCORE_LAUNCH
+}
+
 }  // namespace
 
 int launch_broadcast3(hipStream_t s, const float* src, int64_t s0, int64_t s1, int64_t s2,
@@ -1286,6 +1448,47 @@ int annc_hip_layout_matmul_pack_rhs(void* stream, int64_t k, int64_t n, const fl
   if (total == 0) return set_error(ANNC_OK, "");
   hipLaunchKernelGGL(pack_rhs_kernel, dim3((unsigned)ceil_div(total, 256)), dim3(256), 0,
                      static_cast<hipStream_t>(stream), src, dst, k, n);
+  ANNC_HIP_TRY(hipGetLastError());
+  return set_error(ANNC_OK, "");
+}
+
+int annc_hip_dense_score(void* stream, int64_t m, int64_t n, int64_t k, const float* a,
+                         int64_t lda, const float* b_packed, const float* bias, int epilogue,
+                         const float* w_score, const float* bias_score, int score_epilogue,
+                         float* hidden, int64_t ldh, float* out, int64_t ldo) {
+  using namespace annc;
+  auto aligned16 = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
+  ANNC_REQUIRE(m >= 0 && m < (1ll << 31) - kScoreRows, "bad row count");
+  ANNC_REQUIRE(n == 64 || n == 128 || n == 256, "dense_score: n must be 64, 128 or 256");
+  ANNC_REQUIRE(k >= n && k <= kScoreMaxK && k % n == 0,
+               "dense_score: k must be a multiple of n, at most %d", kScoreMaxK);
+  ANNC_REQUIRE((epilogue & ~(ANNC_EPI_RELU | ANNC_EPI_SIGMOID)) == 0 &&
+                   (score_epilogue & ~(ANNC_EPI_RELU | ANNC_EPI_SIGMOID)) == 0,
+               "unknown epilogue bits");
+  if (m == 0) return set_error(ANNC_OK, "");
+  ANNC_REQUIRE(a != nullptr && b_packed != nullptr && w_score != nullptr && out != nullptr,
+               "null operand");
+  ANNC_REQUIRE(lda >= k && lda % 4 == 0 && aligned16(a), "A rows must be 16-byte aligned");
+  ANNC_REQUIRE(aligned16(b_packed), "packed B must be 16-byte aligned");
+  ANNC_REQUIRE(ldo >= 1, "bad output stride");
+  ANNC_REQUIRE(hidden == nullptr || ldh >= n, "ldh < n");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 grid((unsigned)ceil_div(m, kScoreRows));
+  const int mi = (int)m, ki = (int)k, kmax = (int)k;
+  switch (n) {
+    case 64:
+      launch_dense_score<4>(s, kmax, grid, a, lda, mi, ki, b_packed, bias, epilogue, w_score,
+                            bias_score, score_epilogue, hidden, ldh, out, ldo);
+      break;
+    case 128:
+      launch_dense_score<8>(s, kmax, grid, a, lda, mi, ki, b_packed, bias, epilogue, w_score,
+                            bias_score, score_epilogue, hidden, ldh, out, ldo);
+      break;
+    default:
+      launch_dense_score<16>(s, kmax, grid, a, lda, mi, ki, b_packed, bias, epilogue, w_score,
+                             bias_score, score_epilogue, hidden, ldh, out, ldo);
+      break;
+  }
   ANNC_HIP_TRY(hipGetLastError());
   return set_error(ANNC_OK, "");
 }

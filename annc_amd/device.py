@@ -120,6 +120,62 @@ def gemm(a: torch.Tensor, b, *, addend: torch.Tensor | None = None,
     return out
 
 
+DENSE_SCORE_WIDTHS = (64, 128, 256)
+DENSE_SCORE_MAX_K = 2048
+
+
+def dense_score_fits(k: int, n: int) -> bool:
+    """Whether annc_hip_dense_score takes a hidden layer of shape [k, n]."""
+    return n in DENSE_SCORE_WIDTHS and n <= k <= DENSE_SCORE_MAX_K and k % n == 0
+
+
+def dense_score(a: torch.Tensor, weight: PackedWeight, score_weight: torch.Tensor, *,
+                bias: torch.Tensor | None = None, epilogue: int = _lib.EPI_RELU,
+                score_bias: torch.Tensor | None = None, score_epilogue: int = _lib.EPI_SIGMOID,
+                hidden: torch.Tensor | None = None, out: torch.Tensor | None = None,
+                stream=None) -> torch.Tensor:
+    """Tower tail in one kernel: out = score_epi(epi(a @ W + bias) @ w + score_bias).
+
+    a: [M, K] (rows 16-byte aligned); weight: packed [K, N] with N in
+    DENSE_SCORE_WIDTHS and K a multiple of N; score_weight: N floats (a
+    [N, 1] weight).  `hidden` ([M, N]) receives epi(a @ W + bias) when given.
+    Returns out, [M, 1]."""
+    if not isinstance(weight, PackedWeight):
+        raise ValueError("dense_score takes a packed weight")
+    _require_cuda(a, weight.data, score_weight, bias, score_bias, hidden, out)
+    if a.dtype != torch.float32 or a.dim() != 2:
+        raise ValueError("a must be a 2-D float32 tensor")
+    m, k = a.shape
+    n = weight.n
+    if weight.k != k:
+        raise ValueError(f"packed weight has k={weight.k}, a has k={k}")
+    if not dense_score_fits(k, n):
+        raise ValueError(f"dense_score takes n in {DENSE_SCORE_WIDTHS} and k a multiple of n "
+                         f"up to {DENSE_SCORE_MAX_K}, not k={k}, n={n}")
+    lda = _row_major_2d(a, "a")
+    sw = score_weight.reshape(-1)
+    if sw.numel() != n or not sw.is_contiguous() or sw.dtype != torch.float32:
+        raise ValueError("score_weight must hold n contiguous float32 values")
+    for name, v, size in (("bias", bias, n), ("score_bias", score_bias, 1)):
+        if v is not None and (v.numel() != size or not v.is_contiguous()):
+            raise ValueError(f"{name} must be a contiguous vector of {size}")
+    ldh = 0
+    if hidden is not None:
+        if tuple(hidden.shape) != (m, n):
+            raise ValueError("hidden must be [m, n]")
+        ldh = _row_major_2d(hidden, "hidden")
+    if out is None:
+        out = torch.empty((m, 1), dtype=torch.float32, device=a.device)
+    if out.dim() != 2 or tuple(out.shape) != (m, 1):
+        raise ValueError("out must be [m, 1]")
+    ldo = out.stride(0)
+    check(_lib.lib().annc_hip_dense_score(stream_ptr(stream), m, n, k, ptr(a), lda,
+                                          ptr(weight.data), ptr(bias), epilogue,
+                                          ptr(sw), ptr(score_bias), score_epilogue,
+                                          ptr(hidden), ldh, ptr(out), ldo))
+    return out
+
+
 def embedding_bag(table: torch.Tensor, ids: torch.Tensor, offsets: torch.Tensor,
                   combiner: int = _lib.COMBINER_SUM, out: torch.Tensor | None = None,
                   stream=None) -> torch.Tensor:

@@ -60,12 +60,20 @@ class DenseLayer:
 
 
 class MLPTower:
-    """relu(x W1 + b1) ... -> sigmoid(h Wl + bl) with pre-packed weights."""
+    """relu(x W1 + b1) ... -> sigmoid(h Wl + bl) with pre-packed weights.
+
+    With `fuse_score` (the default) a tower whose last layer has one output
+    runs its last two layers as one kernel (annc_hip_dense_score) when the
+    shapes allow: the scoring dot reads the hidden layer from registers, and
+    that hidden layer reaches memory only with `keep_hidden`.  Every other
+    layer, and the tail when it does not fit, is one GEMM launch."""
 
     def __init__(self, weights: Sequence[np.ndarray], biases: Sequence[np.ndarray],
                  device: torch.device | str = "cuda", packed: bool = True,
-                 final_activation: int = _lib.EPI_SIGMOID):
+                 final_activation: int = _lib.EPI_SIGMOID, fuse_score: bool = True,
+                 keep_hidden: bool = False):
         self.device = torch.device(device)
+        self.keep_hidden = keep_hidden
         self.layers: list[DenseLayer] = []
         for i, (w, b) in enumerate(zip(weights, biases)):
             wt = torch.as_tensor(np.ascontiguousarray(w, dtype=np.float32)).to(self.device)
@@ -75,6 +83,10 @@ class MLPTower:
             bt = torch.as_tensor(np.ascontiguousarray(b, dtype=np.float32)).to(self.device)
             self.layers.append(DenseLayer(wt, bt, act))
         self._buffers: dict[int, list[torch.Tensor]] = {}
+        self.fused_tail = False
+        if fuse_score and packed and len(self.layers) >= 2:
+            hid, last = self.layers[-2].weight, self.layers[-1].weight
+            self.fused_tail = last.n == 1 and dev.dense_score_fits(hid.k, hid.n)
 
     @property
     def widths(self) -> list[int]:
@@ -120,11 +132,25 @@ class MLPTower:
         """x: [batch, k0] (any row stride).  Returns the final [batch, 1] buffer."""
         bufs = self.buffers(x.shape[0])
         h = x
-        for layer, out in zip(self.layers, bufs):
+        plain = len(self.layers) - (2 if self.fused_tail else 0)
+        for layer, out in zip(self.layers[:plain], bufs):
             dev.gemm(h, layer.weight, bias=layer.bias, epilogue=layer.activation, out=out,
                      stream=stream)
             h = out
-        return h
+        if plain == len(self.layers):
+            return h
+        if h.data_ptr() % 16 or h.stride(0) % 4:  # the fused tail reads float4 rows
+            for layer, out in zip(self.layers[plain:], bufs[plain:]):
+                dev.gemm(h, layer.weight, bias=layer.bias, epilogue=layer.activation, out=out,
+                         stream=stream)
+                h = out
+            return h
+        hid, last = self.layers[-2], self.layers[-1]
+        return dev.dense_score(h, hid.weight, last.weight.data, bias=hid.bias,
+                               epilogue=hid.activation, score_bias=last.bias,
+                               score_epilogue=last.activation,
+                               hidden=bufs[-2] if self.keep_hidden else None, out=bufs[-1],
+                               stream=stream)
 
     __call__ = forward
 

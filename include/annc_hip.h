@@ -208,6 +208,26 @@ int annc_hip_gemm(void* stream, int64_t batch, int64_t m, int64_t n, int64_t k,
                   const float* bias, int epilogue,
                   float* c, int64_t ldc, int64_t stride_c);
 
+/* Tower tail in one kernel: the last hidden layer on a packed weight and the
+ * N -> 1 scoring layer after it,
+ *   h      = epi( A . B + bias )                       [m, n]
+ *   out[i] = score_epi( sum_j h[i, j] * w_score[j] + bias_score[0] )
+ * summed over j in a fixed order.  No single counterpart in the reference:
+ * there the hidden layer is a __layout_matmul custom call with XLA's bias
+ * and ReLU fusion (gemm_rewriter.cc:136-159), and the n -> 1 dot stays an
+ * XLA dot (its N = 1 fails the >= 12 rule, gemm_rewriter.cc:29-38) with
+ * bias and logistic fused by XLA.  Here neither h nor a second launch goes
+ * through memory: hidden may be NULL; when given (ldh >= n), h is stored as
+ * well.  Requirements: n = 64, 128 or 256; k a multiple of n, at most 2048;
+ * B in annc_layout_matmul_pack_rhs order, 16-byte aligned; A rows 16-byte
+ * aligned (lda % 4 == 0); w_score holds n floats; bias and bias_score may be
+ * NULL.  Otherwise ANNC_INVALID_ARGUMENT, and nothing is launched.  All
+ * device pointers. */
+int annc_hip_dense_score(void* stream, int64_t m, int64_t n, int64_t k, const float* a,
+                         int64_t lda, const float* b_packed, const float* bias, int epilogue,
+                         const float* w_score, const float* bias_score, int score_epilogue,
+                         float* hidden, int64_t ldh, float* out, int64_t ldo);
+
 /* ------------------------------------------------------------------------ */
 /* Embedding bags and segment reduction (all device pointers)                */
 /* ------------------------------------------------------------------------ */

@@ -248,14 +248,26 @@ def _check_tower_layers(tower, x_host, hidden, y, weights, biases, lda=None):
 
 
 def test_config2_mlp_tower():
+    """The configs[1] tower as the benchmark runs it (layer 1 as a GEMM, layers
+    2 and 3 as one dense_score kernel) and with every layer a GEMM launch:
+    each layer against the oracle, the fused tail's hidden layer stored or
+    not giving the same bits."""
     note("config2 MLP tower")
     w = workloads.config2(seed=0)
-    tower = MLPTower(w.weights, w.biases, device=device(), packed=True)
     x = to_dev(w.x)
-    y = to_host(tower(x))
-    bufs = [to_host(b) for b in tower.buffers(x.shape[0])]
-    _check_tower_layers(tower, w.x, bufs[:-1], bufs[-1], w.weights, w.biases)
-    np.testing.assert_allclose(y, ora.mlp_tower(w.x, w.weights, w.biases), rtol=1e-3, atol=1e-5)
+    ref = ora.mlp_tower(w.x, w.weights, w.biases)
+    ys = {}
+    for fuse in (True, False):
+        tower = MLPTower(w.weights, w.biases, device=device(), packed=True, fuse_score=fuse,
+                         keep_hidden=True)
+        assert tower.fused_tail == fuse
+        ys[fuse] = to_host(tower(x)).copy()
+        bufs = [to_host(b) for b in tower.buffers(x.shape[0])]
+        _check_tower_layers(tower, w.x, bufs[:-1], bufs[-1], w.weights, w.biases)
+        np.testing.assert_allclose(ys[fuse], ref, rtol=1e-3, atol=1e-5)
+    bench_tower = MLPTower(w.weights, w.biases, device=device(), packed=True)
+    assert bench_tower.fused_tail and not bench_tower.keep_hidden
+    np.testing.assert_array_equal(to_host(bench_tower(x)), ys[True])
 
 
 def test_config5_wide_deep_graph():
@@ -264,6 +276,8 @@ def test_config5_wide_deep_graph():
     h = w.hashed
     cfg = WideDeepConfig()
     graph = WideDeepGraph(cfg, [to_dev(t) for t in h.tables], w.weights, w.biases, device=device())
+    assert graph.tower.fused_tail  # 512 -> 256 -> 1 as one dense_score kernel
+    graph.tower.keep_hidden = True  # the 256-wide layer stored too, for the per-layer check
     y = to_host(graph(to_dev(h.ids), to_dev(h.offsets), to_dev(w.dense))).copy()
     emb = ora.hashed_embedding_bags(h.tables, h.num_buckets, h.ids, h.offsets, h.batch, 1, threads=8)
     x = np.concatenate([emb, w.dense], axis=1)
@@ -282,6 +296,71 @@ def test_config5_wide_deep_graph():
     y2 = to_host(graph(to_dev(h.ids), to_dev(h.offsets), view))
     np.testing.assert_array_equal(to_host(graph.concat_buffer(h.batch))[:, :x.shape[1]], x)
     np.testing.assert_array_equal(y2, y)
+    # as served: the fused tail without the hidden store, same bits
+    graph.tower.keep_hidden = False
+    y3 = to_host(graph(to_dev(h.ids), to_dev(h.offsets), view))
+    np.testing.assert_array_equal(y3, y)
+
+
+DENSE_SCORE_CASES = [
+    # m, k, n, hidden epilogue, score epilogue, biases
+    (4096, 512, 256, 1, 2, True),    # configs[1] / configs[4] tail
+    (1000, 256, 256, 1, 2, True),    # one round, partial last workgroup
+    (4099, 2048, 256, 1, 2, True),   # largest K, 8 rounds
+    (17, 512, 128, 2, 0, False),     # 8 waves, no biases, sigmoid hidden
+    (300, 1024, 64, 0, 1, True),     # 4 waves, 16 rounds
+    (1, 64, 64, 1, 2, True),         # one row
+    (4096, 768, 256, 1, 2, True),    # 3 rounds: rotation by 0, 1, 2
+]
+
+
+@pytest.mark.parametrize("m,k,n,epi,sepi,with_bias", DENSE_SCORE_CASES)
+def test_dense_score(m, k, n, epi, sepi, with_bias):
+    """annc_hip_dense_score: the hidden layer against the oracle's sgemm
+    (GEMM bound), the score against the oracle's dense layer fed with the
+    GPU's hidden layer (rtol 1e-4); the score is the same bits with and
+    without the hidden store and with a strided output column."""
+    note(f"dense_score {m}x{k} . [{k}x{n}] epi {epi} -> [{n}x1] epi {sepi} bias {with_bias}")
+    g = workloads.rng(m + 7 * k + n)
+    a = np.maximum(g.standard_normal((m, k)), 0).astype(np.float32)
+    w = (g.standard_normal((k, n)) / np.sqrt(k)).astype(np.float32)
+    ws = (g.standard_normal((n, 1)) / np.sqrt(n)).astype(np.float32)
+    b = (g.standard_normal(n) * 0.1).astype(np.float32) if with_bias else None
+    bs = np.array([0.25], dtype=np.float32) if with_bias else None
+    pw = dev.pack_weight(to_dev(w))
+    hid = torch.full((m, n), float("nan"), device=device())
+    out = torch.full((m, 1), float("nan"), device=device())
+    dev.dense_score(to_dev(a), pw, to_dev(ws), bias=None if b is None else to_dev(b),
+                    epilogue=epi, score_bias=None if bs is None else to_dev(bs),
+                    score_epilogue=sepi, hidden=hid, out=out)
+    h = to_host(hid)
+    href = ora.dense_layer(a, w, b, epi)
+    bias_e = None if b is None else np.broadcast_to(b, href.shape)
+    assert_gemm_close(h, href, gemm_bound(a, w, bias_e))
+    y = to_host(out).copy()
+    np.testing.assert_allclose(y, ora.dense_layer(h, ws, bs, sepi), rtol=1e-4, atol=1e-6)
+    wide = torch.full((m, 3), float("nan"), device=device())
+    dev.dense_score(to_dev(a), pw, to_dev(ws), bias=None if b is None else to_dev(b),
+                    epilogue=epi, score_bias=None if bs is None else to_dev(bs),
+                    score_epilogue=sepi, out=wide[:, 1:2])
+    cols = to_host(wide)
+    np.testing.assert_array_equal(cols[:, 1:2], y)
+    assert np.isnan(cols[:, 0]).all() and np.isnan(cols[:, 2]).all()
+
+
+def test_dense_score_consecutive_calls_of_different_sizes():
+    """Two calls in a row on one stream, the second smaller: nothing carries
+    over between launches (the kernel keeps no state outside its LDS)."""
+    note("dense_score 4096 then 40 rows")
+    g = workloads.rng(11)
+    w = (g.standard_normal((512, 256)) / 23.0).astype(np.float32)
+    ws = (g.standard_normal((256, 1)) / 16.0).astype(np.float32)
+    pw = dev.pack_weight(to_dev(w))
+    for m in (4096, 40):
+        a = np.maximum(g.standard_normal((m, 512)), 0).astype(np.float32)
+        y = to_host(dev.dense_score(to_dev(a), pw, to_dev(ws)))
+        h = np.maximum(ora.dense_layer(a, w, None, 0), 0)
+        np.testing.assert_allclose(y, ora.dense_layer(h, ws, None, 2), rtol=1e-4, atol=1e-6)
 
 
 @pytest.mark.parametrize("pipe", ["mi16", "mi16w8"])

@@ -215,6 +215,24 @@ def test_unique_gather_rejects_key_counts_past_the_table_limit(n):
     assert b"at most 2^29" in lib.annc_hip_last_error()
 
 
+@pytest.mark.parametrize("m,n,k,why", [(64, 96, 192, b"n must be"), (64, 256, 100, b"multiple of n"),
+                                       (64, 256, 4096, b"multiple of n"), (64, 128, 64, b"multiple of n"),
+                                       (-1, 256, 512, b"bad row count")])
+def test_dense_score_rejects_unsupported_shapes(m, n, k, why):
+    """annc_hip_dense_score checks its shape before any launch or pointer
+    access; the tower falls back to one GEMM per layer for such shapes."""
+    import ctypes
+    from annc_amd import device as dev
+    lib = _lib.lib()
+    dummy = ctypes.c_void_p(16)
+    rc = lib.annc_hip_dense_score(None, m, n, k, dummy, k, dummy, None, 1, dummy, None, 2, None, 0,
+                                  dummy, 1)
+    assert rc == _lib.INVALID_ARGUMENT
+    assert why in lib.annc_hip_last_error()
+    assert dev.dense_score_fits(k, n) == (m < 0)
+    assert dev.dense_score_fits(512, 256) and dev.dense_score_fits(2048, 64)
+
+
 def test_shape_info_encoding():
     # hlo_util.h:14-21 -- dims then minor_to_major; row-major [512,256] -> {512,256,1,0}
     assert xla.shape_info((512, 256)).tolist() == [512, 256, 1, 0]
