@@ -3,8 +3,10 @@
 
 Headline (`value`): BASELINE.json configs[1], the layout_matmul MLP tower
 1024-512-256-1 at batch 4096 in fp32, as whole-tower TFLOP/s.  One step =
-one forward of the tower (3 kernels, bias/ReLU/sigmoid fused) launched on
-one stream on device-resident inputs, after `--settle-ms` of untimed steps
+one forward of the tower launched on one stream on device-resident inputs:
+layer 1 as the packed-weight GEMM with bias and ReLU fused, layers 2 and 3 as
+one kernel (annc_hip_dense_score: the 512->256 layer with bias and ReLU and
+the 256->1 sigmoid head, per 16-row workgroup), after `--settle-ms` of untimed steps
 and `--warmup` more; a HIP-graph replay per step is reported beside it.
 
 `roofline` is the dominant kernel (layer 1, 4096x512x1024 packed-weight
@@ -239,7 +241,23 @@ def make_case(name: str, device, inp: Inputs) -> Case:
         tower = MLPTower(w.weights, w.biases, device=device, packed=True)
         x = t(w.x)
         return Case(name, lambda i: tower(x), float(tower.flops(x.shape[0])), "mfma",
-                    "configs[1] step: the 3-layer tower forward (3 kernels)", "tower_config2_step")
+                    "configs[1] step: the 3-layer tower forward (layer-1 GEMM, then the fused "
+                    "512->256->1 tail: 2 kernels)", "tower_config2_step")
+    if name == "tower_tail":
+        # configs[1] layers 2 and 3 as the tower runs them: one dense_score
+        # kernel, the 256-wide hidden layer kept in registers
+        w = inp.get("config2")
+        x = torch.relu(t(w.x)[:, :w.weights[1].shape[0]]).contiguous()
+        wt = dev.pack_weight(t(w.weights[1]))
+        bias, ws, bs = t(w.biases[1]), t(w.weights[2]), t(w.biases[2])
+        out = torch.empty((x.shape[0], 1), dtype=torch.float32, device=device)
+        m, k, n = x.shape[0], wt.k, wt.n
+        return Case(name, lambda i: dev.dense_score(x, wt, ws, bias=bias, epilogue=EPI_RELU,
+                                                    score_bias=bs, score_epilogue=EPI_SIGMOID,
+                                                    out=out),
+                    2.0 * m * n * k + 2.0 * m * n, "mfma",
+                    f"configs[1] layers 2+3: [{m}x{k}] . packed [{k}x{n}] + bias, ReLU, "
+                    f". [{n}x1] + bias, sigmoid (one kernel)", "dense_score_tail_4096x512x256")
     if name == "widedeep":
         from annc_amd.rec_graph import WideDeepConfig, WideDeepGraph
         w = inp.get("config5")
@@ -251,7 +269,8 @@ def make_case(name: str, device, inp: Inputs) -> Case:
         dense.copy_(t(w.dense))
         return Case(name, lambda i: graph(ids, offs, dense), float(h.batch), "samples",
                     "configs[4] step: hashed bags into the concat buffer, 3 GEMMs + bias + ReLU, "
-                    "GEMV + sigmoid (5 kernels)", "widedeep_config5_step", launches=20,
+                    "the 512->256->1 tail as one dense_score kernel (4 kernels)",
+                    "widedeep_config5_step", launches=20,
                     gemm_flops=graph.flops(h.batch))
     if name == "gemm_small":
         w = inp.get("config1")
@@ -489,14 +508,14 @@ def make_case(name: str, device, inp: Inputs) -> Case:
     raise ValueError(f"unknown case {name!r}; choose from {CASES}")
 
 
-CASES = ("tower", "widedeep", "gemm_l1", "gemm_l2", "gemm_l3", "gemm_small", "gemm_e2e_l1", "batch_matmul",
+CASES = ("tower", "widedeep", "gemm_l1", "tower_tail", "gemm_l2", "gemm_l3", "gemm_small", "gemm_e2e_l1", "batch_matmul",
          "bag_sum", "bag_mean", "bag_sum_cold", "bag_phase_empty", "bag_phase_hotrow", "hashed",
          "hashed_cold", "hashed_nohash", "hashed_dim32", "sparse_embedding2", "pooling",
          "segment_reduce_sorted",
          "segment_reduce_any", "hash_bucket", "copy", "bag_stream", "torch_mm_l1",
          "gather_probe", "gather_probe_cold")
 # the cases reported under `components` (gemm_l1 is the roofline, copy the calibration)
-COMPONENT_CASES = ("gemm_small", "gemm_l2", "gemm_l3", "gemm_e2e_l1", "batch_matmul",
+COMPONENT_CASES = ("gemm_small", "tower_tail", "gemm_l2", "gemm_l3", "gemm_e2e_l1", "batch_matmul",
                    "bag_sum", "bag_mean", "bag_sum_cold", "hashed", "hashed_cold",
                    "hashed_nohash", "hashed_dim32", "sparse_embedding2", "pooling",
                    "segment_reduce_sorted", "segment_reduce_any", "hash_bucket",
@@ -559,13 +578,13 @@ def bench_tower(args, device, inp: Inputs):
     x = torch.from_numpy(w.x).to(device)
     batch = x.shape[0]
     flops = tower.flops(batch)
-    # One step = the 3-layer forward launched on one stream (3 kernels).
-    # Untimed steps run for `settle_ms` first, then the `warmup` ones: after
-    # start-up the clocks need some ms of load before they settle (5 warm-up
-    # steps alone left the tower at 59.5 us/step, against 52.9 after 300 ms
-    # on the same box).  A HIP-graph replay per step is timed too: each graph
-    # launch adds a few us of boundary on the box, more than the host needs
-    # to enqueue 3 kernels.
+    # One step = the 3-layer forward launched on one stream (the layer-1 GEMM
+    # and the fused 512->256->1 tail, 2 kernels).  Untimed steps run for
+    # `settle_ms` first, then the `warmup` ones: after start-up the clocks
+    # need some ms of load before they settle (5 warm-up steps alone left the
+    # tower at 59.5 us/step, against 52.9 after 300 ms on the same box).  A
+    # HIP-graph replay per step is timed too: each graph launch adds a few us
+    # of boundary on the box, more than the host needs to enqueue 2 kernels.
     settle = settle_steps(lambda: tower(x), args.settle_ms)
     ms, wall = time_steps(lambda: tower(x), args.steps, args.warmup)
     log(f"tower: {ms * 1e3:.1f} us/step ({wall * 1e6:.1f} us wall) after {args.settle_ms:.0f} ms "
@@ -959,7 +978,8 @@ def main() -> int:
         "config": {"workload": "configs[1]: layout_matmul MLP tower 1024-512-256-1, fp32, "
                                "batch 4096, pre-packed weights, bias+ReLU fused, sigmoid out",
                    "batch": tower["batch"], "flops_per_step": tower["flops"],
-                   "step": "one 3-layer forward (3 kernels) launched on one stream",
+                   "step": "one 3-layer forward launched on one stream: the layer-1 GEMM "
+                           "and the fused 512->256->1 tail (2 kernels)",
                    "settle_ms": args.settle_ms, "settle_steps": tower["settle_steps"]},
         "roofline": tower["roofline"],
         "cpu_baseline": cpu,
