@@ -7,7 +7,7 @@ import torch
 
 from annc_amd import EPI_NONE, EPI_RELU, EPI_SIGMOID, _lib, workloads, xla
 from annc_amd import device as dev
-from annc_amd.rec_graph import MLPTower, WideDeepConfig, WideDeepGraph
+from annc_amd.rec_graph import CapturedGraph, MLPTower, WideDeepConfig, WideDeepGraph
 from oracle import ora
 from tests.gpu_util import assert_gemm_close, device, gemm_bound, note, to_dev, to_host
 
@@ -268,6 +268,26 @@ def test_config2_mlp_tower():
     bench_tower = MLPTower(w.weights, w.biases, device=device(), packed=True)
     assert bench_tower.fused_tail and not bench_tower.keep_hidden
     np.testing.assert_array_equal(to_host(bench_tower(x)), ys[True])
+
+
+@pytest.mark.parametrize("fuse", [True, False])
+def test_config2_tower_graph_replays(fuse):
+    """The benchmark's graph form of the tower: a captured forward replayed
+    three times, with eager forwards of other inputs and synchronisations
+    between the replays, gives the eager result bit for bit every time."""
+    note(f"config2 tower as a HIP graph, fused tail {fuse}")
+    w = workloads.config2(seed=0)
+    tower = MLPTower(w.weights, w.biases, device=device(), packed=True, fuse_score=fuse)
+    x = to_dev(w.x)
+    eager = to_host(tower(x)).copy()
+    graph = CapturedGraph(tower, x)
+    other = to_dev(workloads.config2(seed=1).x)
+    for r in range(3):
+        y = to_host(graph.replay()).copy()
+        np.testing.assert_array_equal(y, eager, err_msg=f"replay {r}")
+        y_other = to_host(tower(other)).copy()  # eager work on the same buffers
+        assert not np.array_equal(y_other, eager)
+        torch.cuda.synchronize()
 
 
 def test_config5_wide_deep_graph():
