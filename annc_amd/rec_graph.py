@@ -170,9 +170,10 @@ class WideDeepGraph:
     """Hashed categorical fields + dense features -> concat -> MLP -> sigmoid.
 
     The concat buffer is [batch, F*dim + num_dense] with its row padded to a
-    multiple of 4 floats so every row starts 16-byte aligned; the embedding
-    kernel writes its columns in place and the first GEMM reads the first
-    F*dim + num_dense columns through the padded leading dimension.
+    multiple of 32 floats; the embedding kernel writes its columns in place.
+    The padding columns stay zero, and the first layer's weight is packed
+    with as many zero rows, so the first GEMM reads whole rows and runs
+    whole 32-deep k-blocks (no K tail; the zero terms change no sum).
     Column order: field 0 .. field F-1 embeddings, then the dense features.
     """
 
@@ -183,8 +184,15 @@ class WideDeepGraph:
         self.device = torch.device(device)
         self.tables = [t.to(self.device).contiguous() for t in tables]
         self.concat_width = cfg.num_fields * cfg.dim + cfg.num_dense
-        self.ld = (self.concat_width + 3) // 4 * 4
-        self.tower = MLPTower(weights, biases, device=self.device, packed=True)
+        self.ld = (self.concat_width + 31) // 32 * 32
+        w0 = np.asarray(weights[0], dtype=np.float32)
+        if w0.shape[0] != self.concat_width:
+            raise ValueError(f"first weight has {w0.shape[0]} rows, the concat {self.concat_width}")
+        w0_padded = np.zeros((self.ld, w0.shape[1]), dtype=np.float32)
+        w0_padded[:self.concat_width] = w0
+        self._shapes = [tuple(np.shape(w)) for w in weights]
+        self.tower = MLPTower([w0_padded] + list(weights[1:]), biases, device=self.device,
+                              packed=True)
         self._concat: dict[int, torch.Tensor] = {}
 
     def concat_buffer(self, batch: int) -> torch.Tensor:
@@ -195,7 +203,8 @@ class WideDeepGraph:
         return buf
 
     def flops(self, batch: int) -> int:
-        return self.tower.flops(batch)
+        """The model's GEMM flops (the first layer at its own K, not the padded one)."""
+        return sum(2 * batch * k * n for k, n in self._shapes)
 
     def dense_view(self, batch: int) -> torch.Tensor:
         """The dense-feature columns of the concat buffer ([batch, num_dense],
@@ -217,7 +226,6 @@ class WideDeepGraph:
         if not (dense.data_ptr() == view.data_ptr() and dense.stride() == view.stride()
                 and dense.shape == view.shape):
             view.copy_(dense)
-        x = buf[:, :self.concat_width]
-        return self.tower.forward(x, stream=stream)
+        return self.tower.forward(buf, stream=stream)
 
     __call__ = forward

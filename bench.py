@@ -268,7 +268,7 @@ def make_case(name: str, device, inp: Inputs) -> Case:
         dense = graph.dense_view(h.batch)
         dense.copy_(t(w.dense))
         return Case(name, lambda i: graph(ids, offs, dense), float(h.batch), "samples",
-                    "configs[4] step: hashed bags into the concat buffer, 3 GEMMs + bias + ReLU, "
+                    "configs[4] step: hashed bags into the concat buffer, 2 GEMMs + bias + ReLU, "
                     "the 512->256->1 tail as one dense_score kernel (4 kernels)",
                     "widedeep_config5_step", launches=20,
                     gemm_flops=graph.flops(h.batch))

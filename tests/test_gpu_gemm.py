@@ -304,7 +304,7 @@ def test_config5_wide_deep_graph():
     concat = to_host(graph.concat_buffer(h.batch))[:, :x.shape[1]]
     np.testing.assert_array_equal(concat, x)  # embeddings bit-exact, dense copied
     # the four GEMM layers at full size, each against the oracle fed with the
-    # GPU's previous layer: 4096x845 (concat rows, stride 848) -> 1024 -> 512
+    # GPU's previous layer: 4096x845 (concat rows, padded to 864 with zero columns and zero weight rows) -> 1024 -> 512
     # -> 256 at the GEMM bound, then the 256 -> 1 sigmoid head
     bufs = [to_host(b) for b in graph.tower.buffers(h.batch)]
     _check_tower_layers(graph.tower, x, bufs[:-1], bufs[-1], w.weights, w.biases)
