@@ -1184,10 +1184,11 @@ int launch_gemm(const GemmParams& p, int64_t batch, hipStream_t stream) {
 //   * NW = N/16 waves; wave w computes the 16-column block w on
 //     v_mfma_f32_16x16x4f32.  A 16-k step feeds k = 4*(l/16) + s to lane l
 //     at MFMA step s, so one 16-byte read per operand covers 4 steps.
-//   * The 16 rows of A sit in LDS whole (row stride K + 4 floats: the 16
-//     rows of a fragment read start 4 banks apart), written a round at a
-//     time: a round is N k-columns of the 16 rows, one float4 per thread,
-//     loaded into registers one round ahead, then one barrier.
+//   * The 16 rows of A sit in LDS whole, written a round at a time: a round
+//     is N k-columns of the 16 rows, one float4 per thread, loaded into
+//     registers one round ahead, then one barrier.  Row stride K + 8
+//     floats: with K + 4 the fragment reads (16 rows, 4 k-chunks) counted
+//     0.5 M cycles of LDS bank conflicts per launch, with K + 8 none.
 //   * B streams from L2 straight into registers, two k-blocks ahead, with
 //     buffer loads: each lane's float4 of the packed format (layout_pack.h)
 //     is the operand of 4 MFMA steps.  Every workgroup reads all of B
@@ -1216,7 +1217,7 @@ __global__ __launch_bounds__(64 * NW) void dense_score_kernel(
   constexpr int BPR = RK / 32; // 32-k blocks per round
   constexpr int TPR = T / 16;  // threads per row in a round
   static_assert(BPR % 2 == 0, "two-block B ring");
-  __shared__ __attribute__((aligned(16))) float a_lds[kScoreRows * (KMAX + 4)];
+  __shared__ __attribute__((aligned(16))) float a_lds[kScoreRows * (KMAX + 8)];
   __shared__ float red[NW][kScoreRows];
 
   const int tid = threadIdx.x;
@@ -1224,7 +1225,7 @@ __global__ __launch_bounds__(64 * NW) void dense_score_kernel(
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 4, c = lane & 15;
   const int m0 = blockIdx.x * kScoreRows;
-  const int RS = K + 4;
+  const int RS = K + 8;
   const int KT = K >> 5;
   const int R = K / RK;
   // visit round r is round (r + ro) % R; ro differs between workgroups of
