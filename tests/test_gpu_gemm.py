@@ -348,12 +348,14 @@ def test_dense_score(m, k, n, epi, sepi, with_bias):
     b = (g.standard_normal(n) * 0.1).astype(np.float32) if with_bias else None
     bs = np.array([0.25], dtype=np.float32) if with_bias else None
     pw = dev.pack_weight(to_dev(w))
-    hid = torch.full((m, n), float("nan"), device=device())
+    hid_buf = torch.full((m, n + 8), float("nan"), device=device())  # ldh = n + 8
+    hid = hid_buf[:, :n]
     out = torch.full((m, 1), float("nan"), device=device())
     dev.dense_score(to_dev(a), pw, to_dev(ws), bias=None if b is None else to_dev(b),
                     epilogue=epi, score_bias=None if bs is None else to_dev(bs),
                     score_epilogue=sepi, hidden=hid, out=out)
-    h = to_host(hid)
+    h = to_host(hid).copy()
+    assert np.isnan(to_host(hid_buf)[:, n:]).all()  # the row padding is not written
     href = ora.dense_layer(a, w, b, epi)
     bias_e = None if b is None else np.broadcast_to(b, href.shape)
     assert_gemm_close(h, href, gemm_bound(a, w, bias_e))
