@@ -1248,6 +1248,14 @@ __global__ __launch_bounds__(64 * NW) void dense_score_kernel(
         f32x4, __builtin_amdgcn_raw_buffer_load_b128(brs, b_off + (t * 1024 + 128 * h) * 4, 0, 0));
   };
 
+  // epilogue operands of this lane's column 16*wave + c, fetched before the
+  // loop rather than after it (11.07 against 11.20 us per launch at
+  // 4096x512x256)
+  const int col = 16 * wave + c;
+  const float bj = bias ? bias[col] : 0.0f;
+  const float wj = w_score[col];
+  const float b_score = bias_score ? bias_score[0] : 0.0f;
+
   int ar = ro;  // round being visited
   f32x4 a_next = *reinterpret_cast<const f32x4*>(a_src + ar * RK);
   f32x4 bq[2][2];
@@ -1288,10 +1296,7 @@ __global__ __launch_bounds__(64 * NW) void dense_score_kernel(
     ar = an;
   }
 
-  // rows 4g .. 4g+3, column 16*wave + c of this wave's block
-  const int col = 16 * wave + c;
-  const float bj = bias ? bias[col] : 0.0f;
-  const float wj = w_score[col];
+  // rows 4g .. 4g+3, column col of this wave's block
   float part[4];
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
@@ -1314,7 +1319,7 @@ __global__ __launch_bounds__(64 * NW) void dense_score_kernel(
     float sum = 0.0f;
 #pragma unroll
     for (int w = 0; w < NW; ++w) sum += red[w][lane];
-    if (bias_score) sum += bias_score[0];
+    if (bias_score) sum += b_score;
     const int row = m0 + lane;
     if (row < M) out[(int64_t)row * ldo] = apply_epilogue(sum, score_epilogue);
   }
