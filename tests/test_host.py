@@ -233,6 +233,13 @@ def test_dense_score_rejects_unsupported_shapes(m, n, k, why):
     assert dev.dense_score_fits(512, 256) and dev.dense_score_fits(2048, 64)
 
 
+def test_dense_score_zero_rows_is_a_no_op():
+    """m = 0 returns OK before any pointer is looked at or any launch."""
+    lib = _lib.lib()
+    assert lib.annc_hip_dense_score(None, 0, 256, 512, None, 512, None, None, 1, None, None, 2,
+                                    None, 0, None, 1) == _lib.OK
+
+
 def test_shape_info_encoding():
     # hlo_util.h:14-21 -- dims then minor_to_major; row-major [512,256] -> {512,256,1,0}
     assert xla.shape_info((512, 256)).tolist() == [512, 256, 1, 0]
