@@ -331,6 +331,9 @@ DENSE_SCORE_CASES = [
     (300, 1024, 64, 0, 1, True),     # 4 waves, 16 rounds
     (1, 64, 64, 1, 2, True),         # one row
     (4096, 768, 256, 1, 2, True),    # 3 rounds: rotation by 0, 1, 2
+    (128, 2048, 64, 1, 2, True),     # 4 waves, 32 rounds, largest K
+    (200, 1024, 128, 1, 2, False),   # 8 waves, 8 rounds
+    (64, 1536, 128, 1, 0, True),     # 8 waves, 12 rounds (K buffer of 2048)
 ]
 
 
