@@ -397,7 +397,7 @@ def make_case(name: str, device, inp: Inputs) -> Case:
         nf = len(w.tables)
         tables = [t(x) for x in w.tables]
         k0 = nf * w.dim + 13
-        buf = torch.zeros((w.batch, (k0 + 3) // 4 * 4), dtype=torch.float32, device=device)
+        buf = torch.zeros((w.batch, (k0 + 31) // 32 * 32), dtype=torch.float32, device=device)
         out = buf[:, :nf * w.dim]
         nnz = int(w.offsets[-1])
         alg = 8 * nnz + 8 * (nf * w.batch + 1) + 4 * w.dim * nnz + 4 * w.batch * nf * w.dim
@@ -406,7 +406,7 @@ def make_case(name: str, device, inp: Inputs) -> Case:
                                                               out=out),
                     alg, "hbm",
                     "configs[4] hashed fields: 26 x batch 4096, Zipf ids, bags 1-5, tables "
-                    "[1e5x32], mean, written into the [4096x848] concat buffer",
+                    "[1e5x32], mean, written into the [4096x864] concat buffer",
                     "hashed_bags_lds_config5_dim32", nnz=nnz)
     if name in ("sparse_embedding2", "pooling"):
         w = inp.get("config3")
