@@ -270,6 +270,26 @@ def test_config2_mlp_tower():
     np.testing.assert_array_equal(to_host(bench_tower(x)), ys[True])
 
 
+@pytest.mark.parametrize("widths,offset", [((512, 256, 1), 1), ((512, 256, 1), 4), ((512, 96, 1), 0)])
+def test_tower_tail_fallbacks(widths, offset):
+    """Towers whose tail the fused kernel does not take run it as two GEMM
+    launches: an input whose rows are not 16-byte aligned (column offset 1)
+    and a hidden width outside 64/128/256; an aligned offset (4) keeps the
+    fused kernel.  Each against the oracle."""
+    note(f"tower {widths}, input column offset {offset}")
+    g = workloads.rng(sum(widths) + offset)
+    m = 300
+    ws = [workloads.glorot_uniform(g, a, b) for a, b in zip(widths[:-1], widths[1:])]
+    bs = [(g.standard_normal(b) * 0.01).astype(np.float32) for b in widths[1:]]
+    xbuf = g.standard_normal((m, widths[0] + 8)).astype(np.float32)
+    x = xbuf[:, offset:offset + widths[0]]
+    tower = MLPTower(ws, bs, device=device(), packed=True)
+    assert tower.fused_tail == (widths[1] in (64, 128, 256))
+    y = to_host(tower(to_dev(xbuf)[:, offset:offset + widths[0]]))
+    np.testing.assert_allclose(y, ora.mlp_tower(np.ascontiguousarray(x), ws, bs), rtol=1e-4,
+                               atol=1e-6)
+
+
 @pytest.mark.parametrize("fuse", [True, False])
 def test_config2_tower_graph_replays(fuse):
     """The benchmark's graph form of the tower: a captured forward replayed
