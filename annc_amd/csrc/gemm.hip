@@ -373,9 +373,13 @@ __global__ __launch_bounds__(kThreads) void gemv_rows_kernel(GemmParams p) {
 // guarded block afterwards.  The W partial blocks meet in LDS and wave v
 // adds registers 4v..4v+3 over w = 0..W-1 in that order before the fused
 // epilogue.
-template <int W, bool AVEC>
+template <int W, bool AVEC, bool PACKED = false>
 __global__ __launch_bounds__(64 * W) void gemm_small_kernel(GemmParams p) {
   static_assert(W == 4 || W == 8, "4 or 8 waves");
+  // PACKED: B in the layout_matmul format with N % 32 == 0 (no tail
+  // columns): a k-block of the workgroup's 32-column panel is 1 KiB whose
+  // quad q holds, at float4 `lane`, this lane's B operand of MFMA steps
+  // 4q..4q+3 -- the same values, in the same order, as the row-major loads
   __shared__ float red[W][16][64];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -391,6 +395,10 @@ __global__ __launch_bounds__(64 * W) void gemm_small_kernel(GemmParams p) {
   const float* __restrict__ arow = p.a + z * p.stride_a + (int64_t)min(m0 + l32, M - 1) * p.lda;
   const float* __restrict__ bcol = p.b + z * p.stride_b + min(col, N - 1);
   const int64_t ldb = p.ldb;
+  // PACKED: this lane's float4 in the panel's k-block 0, and the row-major
+  // K-tail rows [K - 32*KF, N] that follow the full blocks
+  const float* __restrict__ bpan = p.b + z * p.stride_b + (int64_t)(n0 >> 5) * KF * 1024 + 4 * lane;
+  const float* __restrict__ btail = p.b + z * p.stride_b + (int64_t)N * KF * 32 + min(col, N - 1);
   // the addend of the four output registers this wave finishes (wave & 3),
   // fetched before the k-loop; without an addend the loads re-read C and are
   // ignored, so no wave branches around them
@@ -417,8 +425,14 @@ __global__ __launch_bounds__(64 * W) void gemm_small_kernel(GemmParams p) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) af[buf][q][e] = arow[kb + 4 * q + e];
       }
+      if constexpr (PACKED) {
+        const f32x4 bq = *reinterpret_cast<const f32x4*>(bpan + (int64_t)kt * 1024 + 256 * q);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) bf[buf][4 * q + e] = bcol[(int64_t)(kb + 4 * q + e) * ldb];
+        for (int e = 0; e < 4; ++e) bf[buf][4 * q + e] = bq[e];
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) bf[buf][4 * q + e] = bcol[(int64_t)(kb + 4 * q + e) * ldb];
+      }
     }
   };
   f32x16 acc[2];
@@ -459,7 +473,10 @@ __global__ __launch_bounds__(64 * W) void gemm_small_kernel(GemmParams p) {
       for (int e = 0; e < 4; ++e) {
         const int k = kb + 4 * q + e;
         af[0][q][e] = k < K ? arow[k] : 0.0f;
-        bf[0][4 * q + e] = k < K ? bcol[(int64_t)k * ldb] : 0.0f;
+        if constexpr (PACKED)
+          bf[0][4 * q + e] = k < K ? btail[(int64_t)(k - KF * 32) * N] : 0.0f;
+        else
+          bf[0][4 * q + e] = k < K ? bcol[(int64_t)k * ldb] : 0.0f;
       }
     mma(0);
   }
@@ -1146,16 +1163,16 @@ int launch_packed_pipe(const GemmParams& p, int64_t batch, hipStream_t stream,
                     : launch_pipe_tiles<false>(p, batch, stream);
 }
 
-template <int W>
+template <int W, bool PACKED = false>
 int launch_small(const GemmParams& p0, int64_t batch, hipStream_t stream) {
   GemmParams p = p0;
   p.tiles_m = (p.m + 31) / 32;
   p.tiles_n = (p.n + 31) / 32;
   dim3 grid(p.tiles_m * p.tiles_n, 1, (unsigned)batch);
   if (p.a_vec)
-    hipLaunchKernelGGL((gemm_small_kernel<W, true>), grid, dim3(64 * W), 0, stream, p);
+    hipLaunchKernelGGL((gemm_small_kernel<W, true, PACKED>), grid, dim3(64 * W), 0, stream, p);
   else
-    hipLaunchKernelGGL((gemm_small_kernel<W, false>), grid, dim3(64 * W), 0, stream, p);
+    hipLaunchKernelGGL((gemm_small_kernel<W, false, PACKED>), grid, dim3(64 * W), 0, stream, p);
   ANNC_HIP_TRY(hipGetLastError());
   return ANNC_OK;
 }
@@ -1412,7 +1429,15 @@ int annc_hip_gemm(void* stream, int64_t batch, int64_t m, int64_t n, int64_t k, 
   }
   if (b_packed) {
     ANNC_REQUIRE(aligned16(b) && stride_b % 4 == 0, "packed B must be 16-byte aligned");
-    if (n % 32 == 0) return launch_packed_pipe(p, batch, s);
+    if (n % 32 == 0) {
+      // Too few 64x64 tiles to occupy the chip (small batches): 32x32 blocks
+      // with K split over four waves, as for row-major B, whose results these
+      // equal bit for bit.  At 16-256 rows of configs[1]'s layer 1 this takes
+      // about 8 us against 19 us in the pipelined kernel, whose few
+      // workgroups each stream the whole K.
+      if (ceil_div(m, 64) * ceil_div(n, 64) * batch < 128) return launch_small<4, true>(p, batch, s);
+      return launch_packed_pipe(p, batch, s);
+    }
     return launch_gemm<true>(p, batch, s);
   }
   // Large row-major-B GEMMs (the __matmul* and __batch_matmul custom calls,

@@ -509,6 +509,29 @@ def test_row_major_b_packed_per_call(batch, m, n, k, ldb_pad):
     np.testing.assert_array_equal(got, pre)
 
 
+@pytest.mark.parametrize("batch,m,n,k", [(1, 1, 512, 1024), (1, 16, 512, 1024), (1, 256, 256, 512),
+                                         (1, 100, 96, 64), (1, 33, 256, 845), (1, 7, 32, 20),
+                                         (3, 40, 64, 96), (1, 512, 512, 1024)])
+def test_packed_small_batches(batch, m, n, k):
+    """Packed GEMMs with too few 64x64 tiles for the chip (small batches) run
+    the small kernel: within the GEMM bound of OpenBLAS, and bit-identical to
+    the same GEMM on row-major B, which takes the same kernel (K tails and
+    K < 32 included)."""
+    note(f"packed small batch b={batch} {m}x{n}x{k}")
+    g = workloads.rng(7 * m + n + k + batch)
+    a = g.standard_normal((batch, m, k)).astype(np.float32)
+    b = (g.standard_normal((batch, k, n)) / np.sqrt(k)).astype(np.float32)
+    bias = (g.standard_normal(n) * 0.1).astype(np.float32)
+    da, dbias = to_dev(a), to_dev(bias)
+    for z in range(batch):
+        pw = dev.pack_weight(to_dev(b[z]))
+        got = to_host(dev.gemm(da[z], pw, bias=dbias, epilogue=EPI_RELU))
+        ref = ora.dense_layer(a[z], b[z], bias, 1)
+        assert_gemm_close(got, ref, gemm_bound(a[z], b[z], np.broadcast_to(bias, ref.shape)))
+        rm = to_host(dev.gemm(da[z], to_dev(b[z]), bias=dbias, epilogue=EPI_RELU))
+        np.testing.assert_array_equal(got, rm)
+
+
 @pytest.mark.parametrize("m,n,k,col0", [(2048, 512, 256, 1), (8192, 64, 333, 3)])
 def test_pipeline_misaligned_a_base(m, n, k, col0):
     """A starting mid-row of a wider buffer (base not 16-byte aligned, lda a
