@@ -1143,6 +1143,14 @@ int launch_pipe_tiles(const GemmParams& p, int64_t batch, hipStream_t stream) {
   auto tiles = [&](int bm, int bn) {
     return ((int64_t)(p.m + bm - 1) / bm) * ((p.n + bn - 1) / bn) * batch;
   };
+  // 64x32 tiles, each k-block split over two wave pairs (one wave a SIMD,
+  // 48 KiB of LDS, so three workgroups share a CU): where they fill the chip
+  // in one round while 64x64 tiles would leave half of it idle (768-1024 rows
+  // of a 1024->512 layer: 12.4 us against 19.6), and where up to three of
+  // them per CU all run at once while 64x64 tiles would need a second round
+  // (3072 rows of 1024->512: 31.0 us against 36.0 in 128x64 tiles)
+  if (tiles(64, 32) <= cus || (tiles(64, 64) > cus && tiles(64, 32) <= 3 * cus))
+    return launch_pipe<2, 1, 1, 1, 4, 1, 2, BRM>(p, batch, stream);
   auto cost = [&](int bm, int bn) { return ceil_div(tiles(bm, bn), cus) * bm * bn; };
   const int64_t c128 = cost(128, 128), c128x64 = cost(128, 64), c64 = cost(64, 64);
   // 64x64 tiles leave one wave per SIMD; split each k-block over two wave
@@ -1184,9 +1192,11 @@ int launch_gemm(const GemmParams& p, int64_t batch, hipStream_t stream) {
   auto tiles = [&](int bm, int bn) {
     return ((int64_t)(p.m + bm - 1) / bm) * ((p.n + bn - 1) / bn) * batch;
   };
-  // Too few 64x64 tiles to occupy the chip: 32x32 blocks with K split over
-  // four waves (eight measured slower at every K)
-  if (!PACKED && tiles(64, 64) < cus / 2) return launch_small<4>(p, batch, stream);
+  // Too few 64x64 tiles to occupy the chip, or one round of 32x32 blocks:
+  // 32x32 blocks with K split over four waves (eight measured slower at
+  // every K)
+  if (!PACKED && (tiles(64, 64) < cus / 2 || tiles(32, 32) <= cus))
+    return launch_small<4>(p, batch, stream);
   if (tiles(128, 128) >= cus) return launch_tile<2, 2, 2, 2, PACKED>(p, batch, stream);
   if (tiles(64, 128) >= cus) return launch_tile<2, 2, 1, 2, PACKED>(p, batch, stream);
   return launch_tile<2, 2, 1, 1, PACKED>(p, batch, stream);
@@ -1430,12 +1440,12 @@ int annc_hip_gemm(void* stream, int64_t batch, int64_t m, int64_t n, int64_t k, 
   if (b_packed) {
     ANNC_REQUIRE(aligned16(b) && stride_b % 4 == 0, "packed B must be 16-byte aligned");
     if (n % 32 == 0) {
-      // Too few 64x64 tiles to occupy the chip (small batches): 32x32 blocks
-      // with K split over four waves, as for row-major B, whose results these
-      // equal bit for bit.  At 16-256 rows of configs[1]'s layer 1 this takes
-      // about 8 us against 19 us in the pipelined kernel, whose few
-      // workgroups each stream the whole K.
-      if (ceil_div(m, 64) * ceil_div(n, 64) * batch < 128) return launch_small<4, true>(p, batch, s);
+      // At most one round of 32x32 blocks (small batches): 32x32 blocks with
+      // K split over four waves, as for row-major B, whose results these
+      // equal bit for bit.  At 1-512 rows of configs[1]'s layer 1 this takes
+      // 6-8 us against 19 us in the pipelined kernel, whose few workgroups
+      // each stream the whole K.
+      if (ceil_div(m, 32) * ceil_div(n, 32) * batch <= 256) return launch_small<4, true>(p, batch, s);
       return launch_packed_pipe(p, batch, s);
     }
     return launch_gemm<true>(p, batch, s);
@@ -1445,11 +1455,14 @@ int annc_hip_gemm(void* stream, int64_t batch, int64_t m, int64_t n, int64_t k, 
   // faster than the row-major kernel on the tower shapes: in place when B's
   // rows are 16-byte aligned, else after packing B into the stream workspace
   // (8*K*N bytes moved).
+  // Up to one round of 32x32 blocks runs the small kernel (launch_gemm), as
+  // for packed B.
   const int64_t tiles64 = ceil_div(m, 64) * ceil_div(n, 64) * batch;
+  const int64_t tiles32 = ceil_div(m, 32) * ceil_div(n, 32) * batch;
   const int64_t packed_bytes = batch * k * n * static_cast<int64_t>(sizeof(float));
-  const bool pipe_shape = n % 32 == 0 && k >= 32 && tiles64 >= 128;
+  const bool pipe_shape = n % 32 == 0 && k >= 32 && tiles32 > 256;
   if (pipe_shape && p.b_vec) return launch_packed_pipe(p, batch, s, /*b_rowmajor=*/true);
-  if (pipe_shape && m >= 512 && packed_bytes <= (int64_t(1) << 31)) {
+  if (pipe_shape && tiles64 >= 128 && m >= 512 && packed_bytes <= (int64_t(1) << 31)) {
     float* bp = static_cast<float*>(stream_workspace(s, static_cast<size_t>(packed_bytes)));
     if (bp) {
       // Panels per workgroup: the widest that still gives >= 512 workgroups.

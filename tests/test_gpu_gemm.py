@@ -532,6 +532,29 @@ def test_packed_small_batches(batch, m, n, k):
         np.testing.assert_array_equal(got, rm)
 
 
+@pytest.mark.parametrize("m,n,k,col0", [(768, 512, 1024, 0), (1024, 512, 1024, 0),
+                                        (3072, 512, 1024, 0), (1536, 1024, 864, 0),
+                                        (1200, 256, 100, 0), (1536, 256, 512, 1),
+                                        (4000, 288, 845, 3)])
+def test_packed_mid_batches(m, n, k, col0):
+    """Batches between one round of 32x32 blocks and two rounds of 64x64
+    tiles run 64x32 tiles of the pipelined kernel (16- and 4-byte A DMAs, K
+    tails): within the GEMM bound of OpenBLAS, and bit-identical to the same
+    GEMM on row-major B."""
+    note(f"packed mid batch {m}x{n}x{k} col0={col0}")
+    g = workloads.rng(5 * m + n + k + col0)
+    buf = g.standard_normal((m, k + 4)).astype(np.float32)
+    a = np.ascontiguousarray(buf[:, col0:col0 + k])
+    b = (g.standard_normal((k, n)) / np.sqrt(k)).astype(np.float32)
+    bias = (g.standard_normal(n) * 0.1).astype(np.float32)
+    da, dbias = to_dev(buf)[:, col0:col0 + k], to_dev(bias)
+    got = to_host(dev.gemm(da, dev.pack_weight(to_dev(b)), bias=dbias, epilogue=EPI_RELU))
+    ref = ora.dense_layer(a, b, bias, 1)
+    assert_gemm_close(got, ref, gemm_bound(a, b, np.broadcast_to(bias, ref.shape)))
+    rm = to_host(dev.gemm(da, to_dev(b), bias=dbias, epilogue=EPI_RELU))
+    np.testing.assert_array_equal(got, rm)
+
+
 @pytest.mark.parametrize("m,n,k,col0", [(2048, 512, 256, 1), (8192, 64, 333, 3)])
 def test_pipeline_misaligned_a_base(m, n, k, col0):
     """A starting mid-row of a wider buffer (base not 16-byte aligned, lda a
