@@ -915,6 +915,40 @@ def profile_case(name: str, launches: int, graph: bool, device) -> dict:
     return info
 
 
+# (N, K) of the configs[4] tower's three GEMM layers (its 845-wide concat padded to
+# 864; 1024->512 and 512->256 are also configs[1]'s), and the batch sizes swept
+SWEEP_LAYERS = ((1024, 864), (512, 1024), (256, 512))
+SWEEP_ROWS = (1, 64, 256, 512, 768, 1024, 1536, 2048, 3072, 4096, 8192)
+
+
+def gemm_sweep(device) -> None:
+    """One JSON line per (layer, rows): the GEMM with bias and ReLU on packed
+    and on row-major B, and torch.mm (hipBLASLt, no epilogue) on the same
+    operands; best of 3 graphs of 20 launches each, in us."""
+    import torch
+    from annc_amd import EPI_RELU
+    from annc_amd import device as dev
+    g = torch.Generator().manual_seed(0)
+
+    def best(fn):
+        return min(graph_time_ms(lambda i: fn(), 20, 10) for _ in range(3)) * 1e3
+
+    for n, k in SWEEP_LAYERS:
+        w = (torch.randn(k, n, generator=g) * 0.03).to(device)
+        pw = dev.pack_weight(w)
+        bias = torch.zeros(n, device=device)
+        for m in SWEEP_ROWS:
+            x = torch.randn(m, k, generator=g).to(device)
+            out = torch.empty(m, n, device=device)
+            t_packed = best(lambda: dev.gemm(x, pw, bias=bias, epilogue=EPI_RELU, out=out))
+            t_rm = best(lambda: dev.gemm(x, w, bias=bias, epilogue=EPI_RELU, out=out))
+            t_mm = best(lambda: torch.mm(x, w, out=out))
+            print(json.dumps({"m": m, "n": n, "k": k, "packed_us": round(t_packed, 2),
+                              "rowmajor_us": round(t_rm, 2), "torch_mm_us": round(t_mm, 2),
+                              "packed_tflops": round(2 * m * n * k / t_packed / 1e6, 1)}),
+                  flush=True)
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -932,6 +966,8 @@ def main() -> int:
                          "--graph, else 20)")
     ap.add_argument("--graph", action="store_true",
                     help="profiling mode: launch through a replayed HIP graph")
+    ap.add_argument("--gemm-sweep", action="store_true",
+                    help="time the tower's GEMM layers across batch sizes (one JSON line each)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build targets one GPU; --gpus must be 1 (GEMMs "
@@ -946,6 +982,9 @@ def main() -> int:
     torch.cuda.set_device(device)
     if args.kernel:
         print(json.dumps(profile_case(args.kernel, args.launches, args.graph, device)), flush=True)
+        return 0
+    if args.gemm_sweep:
+        gemm_sweep(device)
         return 0
 
     inp = Inputs()
