@@ -1153,6 +1153,13 @@ int launch_pipe_tiles(const GemmParams& p, int64_t batch, hipStream_t stream) {
     return launch_pipe<2, 1, 1, 1, 4, 1, 2, BRM>(p, batch, stream);
   auto cost = [&](int bm, int bn) { return ceil_div(tiles(bm, bn), cus) * bm * bn; };
   const int64_t c128 = cost(128, 128), c128x64 = cost(128, 64), c64 = cost(64, 64);
+  // 256x128 tiles (8 waves of 64x64, 3 stages of 48 KiB: one workgroup a
+  // CU) for K > 512 where they cost no more CU rounds of area than the
+  // smaller tiles, i.e. from 8192 rows of a 1024-column layer: half the
+  // operand bytes per MFMA of 128x128, 1.5-2% faster at 8192-16384 rows
+  const int64_t c256 = cost(256, 128);
+  if (p.k > 512 && c256 <= c128 && c256 <= c128x64 && c256 <= c64)
+    return launch_pipe<4, 2, 2, 2, 3, 1, 1, BRM>(p, batch, stream);
   // 64x64 tiles leave one wave per SIMD; split each k-block over two wave
   // groups so every SIMD runs two
   if (c64 < c128x64 && c64 < c128) return launch_pipe<2, 2, 1, 1, 4, 1, 2, BRM>(p, batch, stream);

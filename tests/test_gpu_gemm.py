@@ -77,9 +77,10 @@ def test_layout_matmul_packed(m, n, k):
 
 
 # Packed B with N % 32 == 0 runs the LDS-DMA pipelined kernel: each of its
-# tile configurations (128x128, 128x64 in 4 or 3 stages, 64x64, chosen from
-# the tile area the busiest CU computes, and K), partial M and N tiles, a K tail with and without full
-# k-blocks, padded lda, addend and sigmoid; A rows that are not 16-byte
+# tile configurations (256x128, 128x128, 128x64 in 4 or 3 stages, 64x64,
+# chosen from the tile area the busiest CU computes, and K; 64x32 is covered
+# by test_packed_mid_batches), partial M and N tiles, a K tail with and
+# without full k-blocks, padded lda, addend and sigmoid; A rows that are not 16-byte
 # aligned (lda % 4 != 0) take the 4-byte DMA variant.
 PIPE_CASES = [
     (4096, 1024, 845, 845, "128x128 tiles, unaligned A rows (4-byte DMA)"),
@@ -104,6 +105,9 @@ PIPE_CASES = [
     (4096, 512, 160, 160, "128x64 tiles, 5 k-blocks"),
     (4096, 512, 64, 67, "128x64 tiles, 2 k-blocks, unaligned A"),
     (4096, 256, 224, 224, "64x64 split-K tiles, 7 k-blocks"),
+    (8192, 1024, 845, 845, "256x128 tiles, unaligned A rows (4-byte DMA), K tail"),
+    (8192, 1024, 1024, 1028, "256x128 tiles, padded lda"),
+    (8192, 1024, 544, 544, "256x128 tiles, 17 k-blocks"),
 ]
 
 
@@ -474,7 +478,8 @@ def test_batch_matmul_add_sigmoid_broadcasts(bias_shape, rhs_batched):
                                                  (3, 1024, 256, 200, 0), (1, 8192, 64, 33, 7),
                                                  (2, 4000, 96, 64, 32), (32, 512, 256, 256, 0),
                                                  (64, 512, 160, 101, 4), (70, 512, 224, 64, 3),
-                                                 (64, 256, 128, 256, 0), (4, 2048, 320, 845, 0)])
+                                                 (64, 256, 128, 256, 0), (4, 2048, 320, 845, 0),
+                                                 (2, 4096, 1024, 1024, 0), (1, 8192, 1024, 845, 3)])
 def test_row_major_b_packed_per_call(batch, m, n, k, ldb_pad):
     """Large row-major-B GEMMs run the pipelined kernel, on B read in place or
     packed into the stream workspace: within tolerance of OpenBLAS, and
