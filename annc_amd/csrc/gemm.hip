@@ -749,11 +749,16 @@ __global__ __launch_bounds__(64 * WM * WN * KS) void gemm_packed_pipe_kernel(Gem
     // DMAs of stage kb+1 and meets the others; stage kb+S-1 then refills the
     // slot of stage kb-1, which no wave reads any more.  So stage kb+1 is
     // published half a stage before it is needed, and the fragments of its
-    // first quad are read during the last MFMAs of stage kb: the MFMA pipes
+    // first quads are read during the last MFMAs of stage kb: the MFMA pipes
     // see no barrier or LDS-latency gap at the stage boundary.
     constexpr int QPS = NQ;  // 8-k quads per wave per stage (4, or 2 with two k groups)
     constexpr int HALF = QPS / 2;
-    f32x4 af[2][BLK_M], bf[2][BLK_N];
+    // fragment reads run LA quads ahead of the MFMAs, in NFB buffers: two
+    // with four quads a stage (reads of stage kb+1 start after the
+    // mid-stage barrier that publishes it), one with two
+    constexpr int LA = QPS == 4 ? 2 : 1;
+    constexpr int NFB = LA == 2 ? 4 : 2;
+    f32x4 af[NFB][BLK_M], bf[NFB][BLK_N];
     auto frag_at = [&](const f32x4* stage, int t, int buf) {
       if constexpr (MI16) {
         // 16-k step t: A chunk 4t + l/16 of row fl; packed B quad l/16,
@@ -795,6 +800,7 @@ __global__ __launch_bounds__(64 * WM * WN * KS) void gemm_packed_pipe_kernel(Gem
         pipe::wait_vmcnt<0>();
       pipe::barrier_only();
       frag_at(&lds[0][0], 0, 0);
+      if constexpr (LA == 2) frag_at(&lds[0][0], 1, 1);
     }
     for (int kb0 = 0; kb0 < KB; kb0 += S) {
 #pragma unroll
@@ -805,13 +811,21 @@ __global__ __launch_bounds__(64 * WM * WN * KS) void gemm_packed_pipe_kernel(Gem
           const f32x4* nxt = &lds[(u + 1) % S][0];
 #pragma unroll
           for (int t = 0; t < QPS; ++t) {
-            const int b = t & 1;
-            // next quad's fragments; after the last stage this reads a stale
-            // slot whose values are never used (no branch around the reads)
-            if (t + 1 < QPS)
-              frag_at(cur, t + 1, b ^ 1);
-            else
-              frag_at(nxt, 0, b ^ 1);
+            const int b = LA == 2 ? t : (t & 1);
+            // fragments LA quads ahead; after the last stage this reads a
+            // stale slot whose values are never used (no branch around the
+            // reads)
+            if constexpr (LA == 2) {
+              if (t + 2 < QPS)
+                frag_at(cur, t + 2, (t + 2) & 3);
+              else
+                frag_at(nxt, t + 2 - QPS, (t + 2) & 3);
+            } else {
+              if (t + 1 < QPS)
+                frag_at(cur, t + 1, b ^ 1);
+              else
+                frag_at(nxt, 0, b ^ 1);
+            }
 #pragma unroll
             for (int e = 0; e < 4; ++e)
 #pragma unroll
