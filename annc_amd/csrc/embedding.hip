@@ -1427,9 +1427,13 @@ __global__ __launch_bounds__(64) void seg_range_wave_kernel(
     if (bad) atomicOr(status, 1);
   };
 
-  // the common case: at most two blocks and four entries per lane; each
-  // lane copies its own entries (no block map)
-  auto gather_direct = [&]() {
+  // The common case: at most two blocks and four entries per lane.  Each
+  // lane loads its own entries (no block map) and keeps them in registers;
+  // the list order is lane-major, so an entry's rank within its segment is
+  // the entries of that segment in lower lanes (four ballot sets, one per
+  // register slot) plus those in lower slots of its own lane.  Only the
+  // ranked row ids go to LDS.
+  auto rank_direct = [&]() {
     const uint32_t c0 = cnt[0];
     const uint32_t src0 = static_cast<uint32_t>(min(lane * per, nblk - 1)) * kRwBlock + s0[0];
     const uint32_t src1 = per > 1 ? static_cast<uint32_t>(min(lane * per + 1, nblk - 1)) * kRwBlock + s0[1]
@@ -1447,22 +1451,42 @@ __global__ __launch_bounds__(64) void seg_range_wave_kernel(
       r[j] = sorted_row[e[j]];
       sg[j] = sorted_seg[e[j]];
     }
+    uint32_t ls[4];
+    bool ok[4];
+    Step st[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      if (static_cast<uint32_t>(j) < mine) {
-        list_row[first + j] = r[j];
-        list_seg[first + j] = static_cast<uint8_t>(sg[j] - lo);
+      ok[j] = static_cast<uint32_t>(j) < mine;
+      ls[j] = ok[j] ? static_cast<uint32_t>(sg[j] - lo) : 0u;
+      st[j] = step_ballots(ls[j], ok[j]);
+    }
+    uint32_t c_lane = 0;  // entries of segment `lane`
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      c_lane += static_cast<uint32_t>(__popcll(seg_mask(st[j], static_cast<uint32_t>(lane))));
+    const uint32_t cur = seg_starts(c_lane);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      uint32_t rank = 0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        rank += static_cast<uint32_t>(__popcll(seg_mask(st[i], ls[j]) & lt));
+        if (i < j) rank += (ok[i] && ls[i] == ls[j]) ? 1u : 0u;
       }
+      const uint32_t base = static_cast<uint32_t>(__shfl(static_cast<int>(cur), static_cast<int>(ls[j]), 64));
+      if (ok[j] && base + rank < static_cast<uint32_t>(kRwCap)) lrow[base + rank] = r[j];
     }
     __syncthreads();
   };
 
   uint32_t c_s = 0;
   if (total <= static_cast<uint32_t>(kRwCap)) {
-    if (per <= 2 && __ballot(mine > 4) == 0)
-      gather_direct();
-    else
-      gather(0, total);
+    if (per <= 2 && __ballot(mine > 4) == 0) {
+      rank_direct();
+      reduce(LdsIds{lrow}, 0u);
+      return;
+    }
+    gather(0, total);
     count_pass(total, &c_s);
     uint32_t cur_s = seg_starts(c_s);
     write_pass(total, &cur_s, true);
