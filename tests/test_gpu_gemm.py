@@ -479,13 +479,16 @@ def test_batch_matmul_add_sigmoid_broadcasts(bias_shape, rhs_batched):
                                                  (2, 4000, 96, 64, 32), (32, 512, 256, 256, 0),
                                                  (64, 512, 160, 101, 4), (70, 512, 224, 64, 3),
                                                  (64, 256, 128, 256, 0), (4, 2048, 320, 845, 0),
-                                                 (2, 4096, 1024, 1024, 0), (1, 8192, 1024, 845, 3)])
+                                                 (2, 4096, 1024, 1024, 0), (1, 8192, 1024, 845, 3),
+                                                 (3, 40, 64, 96, 0), (4, 33, 96, 845, 5)])
 def test_row_major_b_packed_per_call(batch, m, n, k, ldb_pad):
     """Large row-major-B GEMMs run the pipelined kernel, on B read in place or
     packed into the stream workspace: within tolerance of OpenBLAS, and
     bit-identical to the same GEMM on weights packed ahead of time (so the
     in-place reads and the per-call packing both equal the layout_matmul
-    packer, K tails and strided B included, and the pipelined kernel ran)."""
+    packer, K tails and strided B included, and the pipelined kernel ran).
+    Batches of at most 256 32x32 blocks run the small kernel on both forms
+    (batched packed B included), bit-identical likewise."""
     note(f"row-major B packed per call b={batch} {m}x{n}x{k} ldb+{ldb_pad}")
     g = workloads.rng(m + n + k + batch)
     a = g.standard_normal((batch, m, k)).astype(np.float32)
