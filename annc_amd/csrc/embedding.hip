@@ -367,8 +367,9 @@ int launch_bag_idx(const BagArgs& a, hipStream_t s) {
 // ---------------------------------------------------------------------------
 // Positions per workgroup (at most kThreads): 160 keeps a chunk's segments
 // (20 positions each in configs[2]) within the 16 lane groups of a
-// workgroup, so none takes a second turn (128 to 160 measure alike; 256
-// gives the chunks with more than 16 segments a second turn).
+// workgroup, so none takes a second turn (256 gives the chunks with more
+// than 16 segments a second turn).  configs[2], us per launch: 64 positions
+// 5.25, 96 5.38, 128 4.64, 160 4.45, 192 4.65.
 constexpr int kSsChunk = 160;
 
 template <typename IdxT, int G, int VEC, bool MEAN, bool BUF, int P = kSsChunk>
