@@ -24,7 +24,9 @@
 //     blocks), selected only by the ANNC_GEMM_PIPE tuning variable.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
+#include <cstdint>
 #include <cstdlib>
 #include <cstring>
 #include <type_traits>
@@ -577,7 +579,7 @@ __device__ __forceinline__ int a_swizzle(int row) { return (row & 7) ^ ((row >> 
 }  // namespace pipe
 
 template <int WM, int WN, int BLK_M, int BLK_N, int S, int NACC, int KS, bool A16, bool BRM,
-          bool ZMAP, bool MI16 = false>
+          bool ZMAP, bool MI16 = false, bool NTAIL = false>
 __global__ __launch_bounds__(64 * WM * WN * KS) void gemm_packed_pipe_kernel(GemmParams p) {
   static_assert(NACC == 1 || NACC == 2, "one or two accumulator chains");
   static_assert(KS == 1 || KS == 2, "one or two k groups");
@@ -586,6 +588,12 @@ __global__ __launch_bounds__(64 * WM * WN * KS) void gemm_packed_pipe_kernel(Gem
   // 4*(l/16) + s at MFMA step s, so one 16-byte LDS read per operand block
   // serves the 4 steps, from the same A and packed-B stage layouts.
   static_assert(!MI16 || (KS == 1 && !BRM), "16x16 blocks: one k group, packed B");
+  // NTAIL: N % 32 != 0.  The last, partial 32-column panel loads its B
+  // blocks with four 4-byte DMAs each, from the packed format's N-tail
+  // region (row-major [K, N % 32] after the full panels) or from the
+  // row-major B rows, each lane's column clamped to N - 1 (columns past N
+  // are computed and never stored).
+  static_assert(!NTAIL || !MI16, "N tail: 32x32 blocks");
   constexpr int MB = MI16 ? 16 : 32;               // rows and columns of an MFMA block
   constexpr int NR = MI16 ? 4 : 16;                // accumulator registers per block
   using AccT = std::conditional_t<MI16, f32x4, f32x16>;
@@ -645,7 +653,9 @@ __global__ __launch_bounds__(64 * WM * WN * KS) void gemm_packed_pipe_kernel(Gem
   const int M = p.m, N = p.n, K = p.k;
   const int KT = K >> 5;          // full k-blocks
   const int KB = KT;              // stages
-  const int panels = N >> 5;      // N % 32 == 0 on this path
+  const int panels = N >> 5;      // full 32-column panels
+  const int npan = NTAIL ? (N + 31) >> 5 : panels;
+  const int nt = N - 32 * panels;  // NTAIL: columns of the partial panel
 
   // bias of this lane's columns, fetched before the pipeline starts
   const int fl = MI16 ? (lane & 15) : l32;  // this lane's row / column in an MFMA block
@@ -672,7 +682,7 @@ __global__ __launch_bounds__(64 * WM * WN * KS) void gemm_packed_pipe_kernel(Gem
       step[i] = 32;
     } else {
       const int bb = b - NA;
-      const int pn = min((n0 >> 5) + (bb >> 2), panels - 1);
+      const int pn = min((n0 >> 5) + (bb >> 2), npan - 1);
       if constexpr (BRM) {
         // Row-major B: block bb&3 of a panel's stage holds the 128-byte row
         // segments of LDS slots 8*(bb&3) .. +7, slot s holding k = s/2 +
@@ -684,6 +694,40 @@ __global__ __launch_bounds__(64 * WM * WN * KS) void gemm_packed_pipe_kernel(Gem
       } else {
         src[i] = B + (int64_t)pn * KT * 1024 + (bb & 3) * 256 + lane * 4;
         step[i] = 1024;
+      }
+    }
+  }
+  // NTAIL: 4-byte DMA sources of the partial panel's B blocks.  Instruction
+  // j of block i fills LDS floats [64j, 64j+64) of its 1 KiB block: lane l
+  // writes float 64j + l.  Packed: that float is lane L = 16j + l/4, step
+  // e = l%4 of quad q = bb&3, i.e. k = 16*(L/32) + 4q + e, n = L%32 of the
+  // k-block.  Row-major: slot 8q + 2j + l/32 (row k = slot/2 + 16*(slot%2)),
+  // column l%32.
+  bool tpart[LPW];
+  const float* tsrc[NTAIL ? LPW : 1][4];
+  int64_t tstep = 0;
+#pragma unroll
+  for (int i = 0; i < LPW; ++i) {
+    const int b = wave + NW * i;
+    tpart[i] = false;
+    if constexpr (NTAIL) {
+      const int bb = b - NA;
+      const int pn = min((n0 >> 5) + (bb >> 2), npan - 1);
+      tpart[i] = b >= NA && pn == panels;
+      const int q = bb & 3;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if constexpr (BRM) {
+          const int slot = 8 * q + 2 * j + (lane >> 5);
+          const int kr = (slot >> 1) + 16 * (slot & 1);
+          tsrc[i][j] = B + (int64_t)kr * p.ldb + min(32 * panels + (lane & 31), N - 1);
+          tstep = 32 * p.ldb;
+        } else {
+          const int L = 16 * j + (lane >> 2);
+          const int kk = 16 * (L >> 5) + 4 * q + (lane & 3);
+          tsrc[i][j] = B + (int64_t)32 * panels * K + (int64_t)kk * nt + min(L & 31, nt - 1);
+          tstep = (int64_t)32 * nt;
+        }
       }
     }
   }
@@ -712,6 +756,12 @@ __global__ __launch_bounds__(64 * WM * WN * KS) void gemm_packed_pipe_kernel(Gem
 #pragma unroll
         for (int j = 0; j < 4; ++j)
           pipe::dma4(src4[A16 ? 0 : i][j] + (int64_t)kb * 32, dst[i] + slot * kStageBytes + 256 * j);
+      } else if (NTAIL && tpart[i]) {
+        // (a wave issues 3 more DMAs per stage here than the vmcnt waits
+        // count: they then wait for more than they need, never for less)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          pipe::dma4(tsrc[NTAIL ? i : 0][j] + (int64_t)kb * tstep, dst[i] + slot * kStageBytes + 256 * j);
       } else {
         pipe::dma16(src[i] + (int64_t)kb * step[i], dst[i] + slot * kStageBytes);
       }
@@ -864,10 +914,13 @@ __global__ __launch_bounds__(64 * WM * WN * KS) void gemm_packed_pipe_kernel(Gem
     }
   }
 
-  // K tail (K % 32 != 0): packed rows k >= 32*KT are row-major [K - 32*KT, N]
+  // K tail (K % 32 != 0): packed rows k >= 32*KT of the full panels are
+  // row-major [K - 32*KT, nf] (nf = 32*panels); the partial panel's are rows
+  // of its row-major [K, N - nf] region
   if (!MI16 && (K & 31)) {
     const int kf = KT * 32;
-    const int64_t tail_base = (int64_t)N * kf;
+    const int64_t nf = (int64_t)32 * panels;
+    const int64_t tail_base = nf * kf;
 #pragma unroll
     for (int qi = 0; qi < NQ; ++qi) {
       const int q = q0 + qi;
@@ -886,8 +939,10 @@ __global__ __launch_bounds__(64 * WM * WN * KS) void gemm_packed_pipe_kernel(Gem
           const int col = n0 + (wn * BLK_N + j) * 32 + l32;
           if constexpr (BRM)
             bf[j][e] = (kin && col < N) ? B[(int64_t)(kf + kk) * p.ldb + col] : 0.0f;
+          else if (NTAIL && col >= nf)
+            bf[j][e] = (kin && col < N) ? B[nf * K + (int64_t)(kf + kk) * nt + (col - nf)] : 0.0f;
           else
-            bf[j][e] = (kin && col < N) ? B[tail_base + (int64_t)kk * N + col] : 0.0f;
+            bf[j][e] = (kin && col < N) ? B[tail_base + (int64_t)kk * nf + col] : 0.0f;
         }
       }
 #pragma unroll
@@ -1084,7 +1139,8 @@ int launch_tile(const GemmParams& p0, int64_t batch, hipStream_t stream) {
   return ANNC_OK;
 }
 
-template <int WM, int WN, int BMB, int BNB, int S, int NACC, int KS, bool BRM, bool MI16 = false>
+template <int WM, int WN, int BMB, int BNB, int S, int NACC, int KS, bool BRM, bool MI16 = false,
+          bool NTAIL = false>
 int launch_pipe(const GemmParams& p0, int64_t batch, hipStream_t stream) {
   constexpr int BM = WM * BMB * (MI16 ? 16 : 32), BN = WN * BNB * (MI16 ? 16 : 32);
   GemmParams p = p0;
@@ -1096,26 +1152,27 @@ int launch_pipe(const GemmParams& p0, int64_t batch, hipStream_t stream) {
   const dim3 block(64 * WM * WN * KS);
   if (p.a_vec) {
     if (batch > 1)
-      hipLaunchKernelGGL((gemm_packed_pipe_kernel<WM, WN, BMB, BNB, S, NACC, KS, true, BRM, true, MI16>),
+      hipLaunchKernelGGL((gemm_packed_pipe_kernel<WM, WN, BMB, BNB, S, NACC, KS, true, BRM, true, MI16, NTAIL>),
                          grid, block, 0, stream, p);
     else
-      hipLaunchKernelGGL((gemm_packed_pipe_kernel<WM, WN, BMB, BNB, S, NACC, KS, true, BRM, false, MI16>),
+      hipLaunchKernelGGL((gemm_packed_pipe_kernel<WM, WN, BMB, BNB, S, NACC, KS, true, BRM, false, MI16, NTAIL>),
                          grid, block, 0, stream, p);
   } else {
     if (batch > 1)
-      hipLaunchKernelGGL((gemm_packed_pipe_kernel<WM, WN, BMB, BNB, S, NACC, KS, false, BRM, true, MI16>),
+      hipLaunchKernelGGL((gemm_packed_pipe_kernel<WM, WN, BMB, BNB, S, NACC, KS, false, BRM, true, MI16, NTAIL>),
                          grid, block, 0, stream, p);
     else
       hipLaunchKernelGGL(
-          (gemm_packed_pipe_kernel<WM, WN, BMB, BNB, S, NACC, KS, false, BRM, false, MI16>), grid,
+          (gemm_packed_pipe_kernel<WM, WN, BMB, BNB, S, NACC, KS, false, BRM, false, MI16, NTAIL>), grid,
           block, 0, stream, p);
   }
   ANNC_HIP_TRY(hipGetLastError());
   return ANNC_OK;
 }
 
-// Packed B with N % 32 == 0: the LDS-DMA pipeline (16-byte DMAs for A rows
-// that are 16-byte aligned, 4-byte DMAs otherwise), 32 k per stage.
+// Packed B with N % 32 == 0 (or, with NTAIL, a partial last panel): the
+// LDS-DMA pipeline (16-byte DMAs for A rows that are 16-byte aligned, 4-byte
+// DMAs otherwise), 32 k per stage.
 // Tile choice: the one whose busiest CU (256 on MI355X) computes the least
 // tile area, ceil(tiles / 256) * BM * BN, so that a 1.25-round grid does not
 // pay for two full rounds of large tiles.  On a tie between 128x128 and
@@ -1140,9 +1197,9 @@ int gemm_pipe_choice() {
   return 0;
 }
 
-template <bool BRM>
+template <bool BRM, bool NT>
 int launch_pipe_tiles(const GemmParams& p, int64_t batch, hipStream_t stream) {
-  if constexpr (!BRM) {
+  if constexpr (!BRM && !NT) {
     const int choice = batch == 1 && (p.k & 31) == 0 ? gemm_pipe_choice() : 0;
     if (choice) {
       const bool big = ((int64_t)(p.m + 127) / 128) * ((p.n + 63) / 64) >= 256;
@@ -1164,7 +1221,7 @@ int launch_pipe_tiles(const GemmParams& p, int64_t batch, hipStream_t stream) {
   // them per CU all run at once while 64x64 tiles would need a second round
   // (3072 rows of 1024->512: 31.0 us against 36.0 in 128x64 tiles)
   if (tiles(64, 32) <= cus || (tiles(64, 64) > cus && tiles(64, 32) <= 3 * cus))
-    return launch_pipe<2, 1, 1, 1, 4, 1, 2, BRM>(p, batch, stream);
+    return launch_pipe<2, 1, 1, 1, 4, 1, 2, BRM, false, NT>(p, batch, stream);
   auto cost = [&](int bm, int bn) { return ceil_div(tiles(bm, bn), cus) * bm * bn; };
   const int64_t c128 = cost(128, 128), c128x64 = cost(128, 64), c64 = cost(64, 64);
   // 256x128 tiles (8 waves of 64x64, 3 stages of 48 KiB: one workgroup a
@@ -1173,23 +1230,27 @@ int launch_pipe_tiles(const GemmParams& p, int64_t batch, hipStream_t stream) {
   // operand bytes per MFMA of 128x128, 1.5-2% faster at 8192-16384 rows
   const int64_t c256 = cost(256, 128);
   if (p.k > 512 && c256 <= c128 && c256 <= c128x64 && c256 <= c64)
-    return launch_pipe<4, 2, 2, 2, 3, 1, 1, BRM>(p, batch, stream);
+    return launch_pipe<4, 2, 2, 2, 3, 1, 1, BRM, false, NT>(p, batch, stream);
   // 64x64 tiles leave one wave per SIMD; split each k-block over two wave
   // groups so every SIMD runs two
-  if (c64 < c128x64 && c64 < c128) return launch_pipe<2, 2, 1, 1, 4, 1, 2, BRM>(p, batch, stream);
+  if (c64 < c128x64 && c64 < c128) return launch_pipe<2, 2, 1, 1, 4, 1, 2, BRM, false, NT>(p, batch, stream);
   if (c128 < c128x64 || (c128 == c128x64 && p.k > 512))
-    return p.a_vec ? launch_pipe<4, 2, 1, 2, 4, 1, 1, BRM>(p, batch, stream)
-                   : launch_pipe<4, 2, 1, 2, 3, 1, 1, BRM>(p, batch, stream);
-  if (tiles(128, 64) >= 2 * cus) return launch_pipe<4, 2, 1, 1, 3, 2, 1, BRM>(p, batch, stream);
-  return launch_pipe<4, 2, 1, 1, 4, 2, 1, BRM>(p, batch, stream);
+    return p.a_vec ? launch_pipe<4, 2, 1, 2, 4, 1, 1, BRM, false, NT>(p, batch, stream)
+                   : launch_pipe<4, 2, 1, 2, 3, 1, 1, BRM, false, NT>(p, batch, stream);
+  if (tiles(128, 64) >= 2 * cus) return launch_pipe<4, 2, 1, 1, 3, 2, 1, BRM, false, NT>(p, batch, stream);
+  return launch_pipe<4, 2, 1, 1, 4, 2, 1, BRM, false, NT>(p, batch, stream);
 }
 
 // b_rowmajor: B is row-major with 16-byte aligned rows (p.b_vec), read in
 // place; otherwise B is in the layout_matmul packed format.
 int launch_packed_pipe(const GemmParams& p, int64_t batch, hipStream_t stream,
                        bool b_rowmajor = false) {
-  return b_rowmajor ? launch_pipe_tiles<true>(p, batch, stream)
-                    : launch_pipe_tiles<false>(p, batch, stream);
+  const bool nt = (p.n & 31) != 0;
+  if (nt)
+    return b_rowmajor ? launch_pipe_tiles<true, true>(p, batch, stream)
+                      : launch_pipe_tiles<false, true>(p, batch, stream);
+  return b_rowmajor ? launch_pipe_tiles<true, false>(p, batch, stream)
+                    : launch_pipe_tiles<false, false>(p, batch, stream);
 }
 
 template <int W, bool PACKED = false>
@@ -1221,6 +1282,39 @@ int launch_gemm(const GemmParams& p, int64_t batch, hipStream_t stream) {
   if (tiles(128, 128) >= cus) return launch_tile<2, 2, 2, 2, PACKED>(p, batch, stream);
   if (tiles(64, 128) >= cus) return launch_tile<2, 2, 1, 2, PACKED>(p, batch, stream);
   return launch_tile<2, 2, 1, 1, PACKED>(p, batch, stream);
+}
+
+// N <= 4: 16 lanes per row (row-major or dense B)
+int launch_gemv(const GemmParams& p, int64_t batch, hipStream_t s) {
+  dim3 grid((unsigned)ceil_div(p.m, kThreads / 16), 1, (unsigned)batch);
+  switch (p.n) {
+    case 1: hipLaunchKernelGGL(gemv_rows_kernel<1>, grid, dim3(kThreads), 0, s, p); break;
+    case 2: hipLaunchKernelGGL(gemv_rows_kernel<2>, grid, dim3(kThreads), 0, s, p); break;
+    case 3: hipLaunchKernelGGL(gemv_rows_kernel<3>, grid, dim3(kThreads), 0, s, p); break;
+    default: hipLaunchKernelGGL(gemv_rows_kernel<4>, grid, dim3(kThreads), 0, s, p); break;
+  }
+  ANNC_HIP_TRY(hipGetLastError());
+  return ANNC_OK;
+}
+
+// Columns [nf, N) of a GEMM whose first nf = N & ~31 columns ran through the
+// pipelined kernel: B's tail columns as a row-major [K, N - nf] block at
+// b_tail (row stride ldb_tail; batches stride_b apart), and C, the addend
+// and the bias from column nf on.  N - nf <= 4 runs the GEMV kernel, wider
+// tails the small kernel (one 32-column block).
+int launch_n_tail(const GemmParams& p, int64_t nf, const float* b_tail, int64_t ldb_tail,
+                  int64_t batch, hipStream_t s) {
+  auto aligned16 = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
+  GemmParams t = p;
+  t.n = p.n - static_cast<int>(nf);
+  t.b = b_tail;
+  t.ldb = ldb_tail;
+  t.c = p.c + nf;
+  if (p.e) t.e = p.e + nf;
+  if (p.bias) t.bias = p.bias + nf;
+  t.b_vec = ldb_tail % 4 == 0 && p.stride_b % 4 == 0 && aligned16(b_tail);
+  t.b_dense = ldb_tail == t.n && p.stride_b % 4 == 0 && aligned16(b_tail);
+  return t.n <= 4 ? launch_gemv(t, batch, s) : launch_small<4>(t, batch, s);
 }
 
 // ---------------------------------------------------------------------------
@@ -1448,16 +1542,34 @@ int annc_hip_gemm(void* stream, int64_t batch, int64_t m, int64_t n, int64_t k, 
   p.b_dense = (p.ldb == n) && (stride_b % 4 == 0) && aligned16(b);
 
   if (n <= 4) {
-    dim3 grid((unsigned)ceil_div(m, kThreads / 16), 1, (unsigned)batch);
-    switch (n) {
-      case 1: hipLaunchKernelGGL(gemv_rows_kernel<1>, grid, dim3(kThreads), 0, s, p); break;
-      case 2: hipLaunchKernelGGL(gemv_rows_kernel<2>, grid, dim3(kThreads), 0, s, p); break;
-      case 3: hipLaunchKernelGGL(gemv_rows_kernel<3>, grid, dim3(kThreads), 0, s, p); break;
-      default: hipLaunchKernelGGL(gemv_rows_kernel<4>, grid, dim3(kThreads), 0, s, p); break;
-    }
-    ANNC_HIP_TRY(hipGetLastError());
-    return set_error(ANNC_OK, "");
+    const int rc = launch_gemv(p, batch, s);
+    return set_error(rc, rc == ANNC_OK ? "" : "GEMV launch failed");
   }
+  // N % 32 != 0 with more than one round of 32x32 blocks in its full
+  // 32-column panels: the pipelined kernel with a partial last panel (B
+  // packed, or row-major with 16-byte aligned rows) where the extra column
+  // of tiles costs no more CU rounds (one_launch), else the full panels
+  // pipelined (row-major B without aligned rows packed per call first) and
+  // then the N % 32 tail columns through a small kernel; instead of the tile
+  // kernel over all of N.  4096x1000x1024: 122 us -> 78 (two launches) or
+  // 73 (one); 4096x520x1024: 123 -> 46 (two; one launch needs a 5th CU
+  // round of tiles: 62).
+  const int64_t nf = n & ~int64_t(31);
+  const bool split_n = n % 32 != 0 && nf > 0 && k >= 32 &&
+                       ceil_div(m, 32) * (nf / 32) * batch > 256;
+  // the pipelined kernel's busiest-CU tile area over nn columns, the least
+  // over the tilings its launcher picks from
+  auto round_area = [&](int64_t nn) {
+    static constexpr int kShapes[5][2] = {{256, 128}, {128, 128}, {128, 64}, {64, 64}, {64, 32}};
+    int64_t best = INT64_MAX;
+    for (const auto& sh : kShapes) {
+      if (sh[0] == 256 && k <= 512) continue;
+      const int64_t t = ceil_div(m, sh[0]) * ceil_div(nn, sh[1]) * batch;
+      best = std::min<int64_t>(best, ceil_div(t, 256) * sh[0] * sh[1]);
+    }
+    return best;
+  };
+  const bool one_launch = split_n && round_area(n) <= round_area(nf);
   if (b_packed) {
     ANNC_REQUIRE(aligned16(b) && stride_b % 4 == 0, "packed B must be 16-byte aligned");
     if (n % 32 == 0) {
@@ -1469,6 +1581,18 @@ int annc_hip_gemm(void* stream, int64_t batch, int64_t m, int64_t n, int64_t k, 
       if (ceil_div(m, 32) * ceil_div(n, 32) * batch <= 256) return launch_small<4, true>(p, batch, s);
       return launch_packed_pipe(p, batch, s);
     }
+    if (split_n) {
+      // one launch: the partial last panel from the format's row-major
+      // N-tail region; two: the format's first nf*K floats are the packed
+      // [K, nf] matrix of the full panels, and the N-tail region follows
+      if (one_launch) return launch_packed_pipe(p, batch, s);
+      GemmParams q = p;
+      q.n = static_cast<int>(nf);
+      q.ldb = nf;
+      const int rc = launch_packed_pipe(q, batch, s);
+      if (rc != ANNC_OK) return set_error(rc, "GEMM launch failed");
+      return launch_n_tail(p, nf, b + nf * k, n - nf, batch, s);
+    }
     return launch_gemm<true>(p, batch, s);
   }
   // Large row-major-B GEMMs (the __matmul* and __batch_matmul custom calls,
@@ -1477,28 +1601,39 @@ int annc_hip_gemm(void* stream, int64_t batch, int64_t m, int64_t n, int64_t k, 
   // rows are 16-byte aligned, else after packing B into the stream workspace
   // (8*K*N bytes moved).
   // Up to one round of 32x32 blocks runs the small kernel (launch_gemm), as
-  // for packed B.
-  const int64_t tiles64 = ceil_div(m, 64) * ceil_div(n, 64) * batch;
+  // for packed B.  N % 32 != 0 (split_n): the first nm = nf columns as below,
+  // then the tail columns.
   const int64_t tiles32 = ceil_div(m, 32) * ceil_div(n, 32) * batch;
-  const int64_t packed_bytes = batch * k * n * static_cast<int64_t>(sizeof(float));
-  const bool pipe_shape = n % 32 == 0 && k >= 32 && tiles32 > 256;
-  if (pipe_shape && p.b_vec) return launch_packed_pipe(p, batch, s, /*b_rowmajor=*/true);
-  if (pipe_shape && tiles64 >= 128 && m >= 512 && packed_bytes <= (int64_t(1) << 31)) {
-    float* bp = static_cast<float*>(stream_workspace(s, static_cast<size_t>(packed_bytes)));
-    if (bp) {
-      // Panels per workgroup: the widest that still gives >= 512 workgroups.
-      const int64_t kcols = (k >> 5) + ((k & 31) ? 1 : 0), panels = n >> 5;
-      int ppw = 4;
-      while (ppw > 1 && kcols * ceil_div(panels, ppw) * batch < 512) ppw >>= 1;
-      const dim3 grid((unsigned)kcols, (unsigned)ceil_div(panels, ppw), (unsigned)batch);
-      hipLaunchKernelGGL(pack_rhs_rowmajor_kernel, grid, dim3(256), 0, s, b, ldb, stride_b, bp,
-                         (int)k, (int)n, ppw);
-      ANNC_HIP_TRY(hipGetLastError());
-      GemmParams q = p;
-      q.b = bp;
-      q.ldb = n;
-      q.stride_b = k * n;
-      return launch_packed_pipe(q, batch, s);
+  const bool whole = n % 32 == 0 && k >= 32 && tiles32 > 256;
+  if (whole || split_n) {
+    if (p.b_vec && (whole || one_launch))
+      return launch_packed_pipe(p, batch, s, /*b_rowmajor=*/true);
+    const int64_t nm = whole ? n : nf;  // columns through the pipelined kernel
+    GemmParams q = p;
+    q.n = static_cast<int>(nm);
+    auto then_tail = [&](int rc) -> int {
+      if (rc != ANNC_OK || nm == n) return rc;
+      return launch_n_tail(p, nm, b + nm, ldb, batch, s);
+    };
+    if (p.b_vec) return then_tail(launch_packed_pipe(q, batch, s, /*b_rowmajor=*/true));
+    const int64_t tiles64 = ceil_div(m, 64) * ceil_div(nm, 64) * batch;
+    const int64_t packed_bytes = batch * k * nm * static_cast<int64_t>(sizeof(float));
+    if (tiles64 >= 128 && m >= 512 && packed_bytes <= (int64_t(1) << 31)) {
+      float* bp = static_cast<float*>(stream_workspace(s, static_cast<size_t>(packed_bytes)));
+      if (bp) {
+        // Panels per workgroup: the widest that still gives >= 512 workgroups.
+        const int64_t kcols = (k >> 5) + ((k & 31) ? 1 : 0), panels = nm >> 5;
+        int ppw = 4;
+        while (ppw > 1 && kcols * ceil_div(panels, ppw) * batch < 512) ppw >>= 1;
+        const dim3 grid((unsigned)kcols, (unsigned)ceil_div(panels, ppw), (unsigned)batch);
+        hipLaunchKernelGGL(pack_rhs_rowmajor_kernel, grid, dim3(256), 0, s, b, ldb, stride_b, bp,
+                           (int)k, (int)nm, ppw);
+        ANNC_HIP_TRY(hipGetLastError());
+        q.b = bp;
+        q.ldb = nm;
+        q.stride_b = k * nm;
+        return then_tail(launch_packed_pipe(q, batch, s));
+      }
     }
   }
   return launch_gemm<false>(p, batch, s);

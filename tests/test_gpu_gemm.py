@@ -563,6 +563,58 @@ def test_packed_mid_batches(m, n, k, col0):
     np.testing.assert_array_equal(got, rm)
 
 
+# N % 32 != 0 with more than one round of 32x32 blocks in the full panels:
+# the pipelined kernel with a partial last panel (packed B, and row-major B
+# with 16-byte aligned rows), or, for other row-major B, the full panels
+# pipelined and the tail columns through the small kernel (N % 32 > 4) or
+# the GEMV kernel (N % 32 <= 4).
+N_TAIL_CASES = [
+    (1, 4096, 1000, 1024, "8 tail columns"),
+    (1, 4096, 515, 845, "3 tail columns; row-major rows unaligned (pack + GEMV tail), K tail"),
+    (1, 2048, 300, 845, "12 tail columns, K tail"),
+    (3, 1024, 100, 64, "batched, 4 tail columns"),
+    (1, 8200, 33, 256, "one full panel, 1 tail column (row-major: pack + GEMV tail)"),
+    (2, 777, 620, 100, "batched, partial M tile, 12 tail columns, K tail"),
+    (1, 4096, 1001, 40, "unaligned rows (pack + small tail), 1 k-block + K tail"),
+    (1, 8192, 1000, 864, "256x128 tiles with a partial panel"),
+    (1, 1200, 340, 512, "64x32 tiles with a partial panel"),
+]
+
+
+@pytest.mark.parametrize("batch,m,n,k,what", N_TAIL_CASES)
+def test_n_tail_split(batch, m, n, k, what):
+    """Within the GEMM bound of OpenBLAS with bias and ReLU, and with an
+    addend and sigmoid; packed B and row-major B with 16-byte aligned rows
+    (the same kernel) bit-identical."""
+    note(f"N-tail split b={batch} {m}x{n}x{k}: {what}")
+    g = workloads.rng(3 * m + n + k + batch)
+    a = g.standard_normal((batch, m, k)).astype(np.float32)
+    w = (g.standard_normal((batch, k, n)) / np.sqrt(k)).astype(np.float32)
+    bias = (g.standard_normal(n) * 0.1).astype(np.float32)
+    e = g.standard_normal((batch, m, n)).astype(np.float32)
+    da, dbias, de = to_dev(a), to_dev(bias), to_dev(e)
+    for z in range(batch):
+        pw = dev.pack_weight(to_dev(w[z]))
+        got = to_host(dev.gemm(da[z], pw, bias=dbias, epilogue=EPI_RELU))
+        ref = ora.dense_layer(a[z], w[z], bias, 1)
+        assert_gemm_close(got, ref, gemm_bound(a[z], w[z], np.broadcast_to(bias, ref.shape)))
+        sg = to_host(dev.gemm(da[z], pw, addend=de[z], epilogue=EPI_SIGMOID))
+        lin = ora.matmul_add(e[z], a[z], w[z])
+        np.testing.assert_allclose(sg, 1.0 / (1.0 + np.exp(-lin.astype(np.float64))), rtol=1e-4,
+                                   atol=1e-5)
+        if batch == 1:
+            rm = to_host(dev.gemm(da[z], to_dev(w[z]), bias=dbias, epilogue=EPI_RELU))
+            if n % 4 == 0:
+                np.testing.assert_array_equal(got, rm)
+            else:
+                assert_gemm_close(rm, ref, gemm_bound(a[z], w[z], np.broadcast_to(bias, ref.shape)))
+    if batch > 1:  # one batched row-major call: the same per-batch results
+        got_b = to_host(dev.gemm(da, to_dev(w), bias=dbias, epilogue=EPI_RELU))
+        for z in range(batch):
+            ref = ora.dense_layer(a[z], w[z], bias, 1)
+            assert_gemm_close(got_b[z], ref, gemm_bound(a[z], w[z], np.broadcast_to(bias, ref.shape)))
+
+
 @pytest.mark.parametrize("m,n,k,col0", [(2048, 512, 256, 1), (8192, 64, 333, 3)])
 def test_pipeline_misaligned_a_base(m, n, k, col0):
     """A starting mid-row of a wider buffer (base not 16-byte aligned, lda a
