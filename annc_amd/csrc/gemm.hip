@@ -378,10 +378,12 @@ __global__ __launch_bounds__(kThreads) void gemv_rows_kernel(GemmParams p) {
 template <int W, bool AVEC, bool PACKED = false>
 __global__ __launch_bounds__(64 * W) void gemm_small_kernel(GemmParams p) {
   static_assert(W == 4 || W == 8, "4 or 8 waves");
-  // PACKED: B in the layout_matmul format with N % 32 == 0 (no tail
-  // columns): a k-block of the workgroup's 32-column panel is 1 KiB whose
-  // quad q holds, at float4 `lane`, this lane's B operand of MFMA steps
-  // 4q..4q+3 -- the same values, in the same order, as the row-major loads
+  // PACKED: B in the layout_matmul format: a k-block of the workgroup's
+  // full 32-column panel is 1 KiB whose quad q holds, at float4 `lane`, this
+  // lane's B operand of MFMA steps 4q..4q+3 -- the same values, in the same
+  // order, as the row-major loads.  The partial last panel of N % 32 != 0
+  // (tpan) reads the format's row-major [K, N % 32] N-tail region as
+  // row-major B.
   __shared__ float red[W][16][64];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -395,12 +397,17 @@ __global__ __launch_bounds__(64 * W) void gemm_small_kernel(GemmParams p) {
   const int col = n0 + l32;
   const bool col_ok = col < N;
   const float* __restrict__ arow = p.a + z * p.stride_a + (int64_t)min(m0 + l32, M - 1) * p.lda;
-  const float* __restrict__ bcol = p.b + z * p.stride_b + min(col, N - 1);
-  const int64_t ldb = p.ldb;
+  const int nf = N & ~31;
+  const bool tpan = PACKED && n0 >= nf;  // the partial panel (wave-uniform)
+  const int nt = N - nf;
+  const float* __restrict__ bcol =
+      tpan ? p.b + z * p.stride_b + (int64_t)nf * K + min(col - nf, nt - 1)
+           : p.b + z * p.stride_b + min(col, N - 1);
+  const int64_t ldb = tpan ? nt : p.ldb;
   // PACKED: this lane's float4 in the panel's k-block 0, and the row-major
-  // K-tail rows [K - 32*KF, N] that follow the full blocks
+  // K-tail rows [K - 32*KF, nf] of the full panels that follow the blocks
   const float* __restrict__ bpan = p.b + z * p.stride_b + (int64_t)(n0 >> 5) * KF * 1024 + 4 * lane;
-  const float* __restrict__ btail = p.b + z * p.stride_b + (int64_t)N * KF * 32 + min(col, N - 1);
+  const float* __restrict__ btail = p.b + z * p.stride_b + (int64_t)nf * KF * 32 + min(col, nf - 1);
   // the addend of the four output registers this wave finishes (wave & 3),
   // fetched before the k-loop; without an addend the loads re-read C and are
   // ignored, so no wave branches around them
@@ -427,7 +434,7 @@ __global__ __launch_bounds__(64 * W) void gemm_small_kernel(GemmParams p) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) af[buf][q][e] = arow[kb + 4 * q + e];
       }
-      if constexpr (PACKED) {
+      if (PACKED && !tpan) {
         const f32x4 bq = *reinterpret_cast<const f32x4*>(bpan + (int64_t)kt * 1024 + 256 * q);
 #pragma unroll
         for (int e = 0; e < 4; ++e) bf[buf][4 * q + e] = bq[e];
@@ -475,8 +482,8 @@ __global__ __launch_bounds__(64 * W) void gemm_small_kernel(GemmParams p) {
       for (int e = 0; e < 4; ++e) {
         const int k = kb + 4 * q + e;
         af[0][q][e] = k < K ? arow[k] : 0.0f;
-        if constexpr (PACKED)
-          bf[0][4 * q + e] = k < K ? btail[(int64_t)(k - KF * 32) * N] : 0.0f;
+        if (PACKED && !tpan)
+          bf[0][4 * q + e] = k < K ? btail[(int64_t)(k - KF * 32) * nf] : 0.0f;
         else
           bf[0][4 * q + e] = k < K ? bcol[(int64_t)k * ldb] : 0.0f;
       }
@@ -1510,6 +1517,11 @@ int annc_hip_gemm(void* stream, int64_t batch, int64_t m, int64_t n, int64_t k, 
   ANNC_REQUIRE(m < (1ll << 31) && n < (1ll << 31) && k < (1ll << 31) && batch < 65536,
                "GEMM dimension too large");
   if (batch == 0 || m == 0 || n == 0) return set_error(ANNC_OK, "");
+  // packed with N < 32 is row-major [K, N] (no full panels)
+  if (b_packed && n < 32) {
+    b_packed = 0;
+    ldb = n;
+  }
   ANNC_REQUIRE(c != nullptr, "null output");
   ANNC_REQUIRE(k == 0 || (a != nullptr && b != nullptr), "null operand");
   ANNC_REQUIRE(b_packed || ldb >= n, "ldb < n");
@@ -1572,28 +1584,24 @@ int annc_hip_gemm(void* stream, int64_t batch, int64_t m, int64_t n, int64_t k, 
   const bool one_launch = split_n && round_area(n) <= round_area(nf);
   if (b_packed) {
     ANNC_REQUIRE(aligned16(b) && stride_b % 4 == 0, "packed B must be 16-byte aligned");
-    if (n % 32 == 0) {
-      // At most one round of 32x32 blocks (small batches): 32x32 blocks with
-      // K split over four waves, as for row-major B, whose results these
-      // equal bit for bit.  At 1-512 rows of configs[1]'s layer 1 this takes
-      // 6-8 us against 19 us in the pipelined kernel, whose few workgroups
-      // each stream the whole K.
-      if (ceil_div(m, 32) * ceil_div(n, 32) * batch <= 256) return launch_small<4, true>(p, batch, s);
-      return launch_packed_pipe(p, batch, s);
-    }
-    if (split_n) {
-      // one launch: the partial last panel from the format's row-major
-      // N-tail region; two: the format's first nf*K floats are the packed
-      // [K, nf] matrix of the full panels, and the N-tail region follows
-      if (one_launch) return launch_packed_pipe(p, batch, s);
-      GemmParams q = p;
-      q.n = static_cast<int>(nf);
-      q.ldb = nf;
-      const int rc = launch_packed_pipe(q, batch, s);
-      if (rc != ANNC_OK) return set_error(rc, "GEMM launch failed");
-      return launch_n_tail(p, nf, b + nf * k, n - nf, batch, s);
-    }
-    return launch_gemm<true>(p, batch, s);
+    // At most one round of 32x32 blocks (small batches): 32x32 blocks with K
+    // split over four waves, as for row-major B, whose results these equal
+    // bit for bit (a partial last panel reads the format's N-tail region).
+    // At 1-512 rows of configs[1]'s layer 1 this takes 6-8 us against 19 us
+    // in the pipelined kernel, whose few workgroups each stream the whole K;
+    // 256x1000x1024: 61 -> 10 us against the tile kernel.
+    if (ceil_div(m, 32) * ceil_div(n, 32) * batch <= 256) return launch_small<4, true>(p, batch, s);
+    if (n % 32 == 0) return launch_packed_pipe(p, batch, s);
+    // one launch: the partial last panel from the format's row-major N-tail
+    // region; two: the format's first nf*K floats are the packed [K, nf]
+    // matrix of the full panels, and the N-tail region follows
+    if (round_area(n) <= round_area(nf)) return launch_packed_pipe(p, batch, s);
+    GemmParams q = p;
+    q.n = static_cast<int>(nf);
+    q.ldb = nf;
+    const int rc = launch_packed_pipe(q, batch, s);
+    if (rc != ANNC_OK) return set_error(rc, "GEMM launch failed");
+    return launch_n_tail(p, nf, b + nf * k, n - nf, batch, s);
   }
   // Large row-major-B GEMMs (the __matmul* and __batch_matmul custom calls,
   // whose weights XLA passes row-major) run the LDS-DMA pipeline, about 1.5x

@@ -519,12 +519,15 @@ def test_row_major_b_packed_per_call(batch, m, n, k, ldb_pad):
 
 @pytest.mark.parametrize("batch,m,n,k", [(1, 1, 512, 1024), (1, 16, 512, 1024), (1, 256, 256, 512),
                                          (1, 100, 96, 64), (1, 33, 256, 845), (1, 7, 32, 20),
-                                         (3, 40, 64, 96), (1, 512, 512, 1024)])
+                                         (3, 40, 64, 96), (1, 512, 512, 1024), (1, 256, 1000, 1024),
+                                         (1, 100, 300, 845), (1, 17, 40, 33), (2, 40, 70, 96),
+                                         (1, 4096, 16, 1024), (1, 3000, 24, 100)])
 def test_packed_small_batches(batch, m, n, k):
-    """Packed GEMMs with too few 64x64 tiles for the chip (small batches) run
-    the small kernel: within the GEMM bound of OpenBLAS, and bit-identical to
-    the same GEMM on row-major B, which takes the same kernel (K tails and
-    K < 32 included)."""
+    """Packed GEMMs with at most one round of 32x32 blocks (small batches)
+    run the small kernel: within the GEMM bound of OpenBLAS, and bit-identical
+    to the same GEMM on row-major B, which takes the same kernel (K tails,
+    K < 32, a partial last panel read from the format's N-tail region, and
+    N < 32, where the format is row-major, included)."""
     note(f"packed small batch b={batch} {m}x{n}x{k}")
     g = workloads.rng(7 * m + n + k + batch)
     a = g.standard_normal((batch, m, k)).astype(np.float32)
