@@ -1281,10 +1281,11 @@ int launch_gemm(const GemmParams& p, int64_t batch, hipStream_t stream) {
   auto tiles = [&](int bm, int bn) {
     return ((int64_t)(p.m + bm - 1) / bm) * ((p.n + bn - 1) / bn) * batch;
   };
-  // Too few 64x64 tiles to occupy the chip, or one round of 32x32 blocks:
-  // 32x32 blocks with K split over four waves (eight measured slower at
-  // every K)
-  if (!PACKED && (tiles(64, 64) < cus / 2 || tiles(32, 32) <= cus))
+  // Too few 64x64 tiles to occupy the chip, one round of 32x32 blocks, or
+  // N < 32 (one 32-column block; the tile kernel would waste most of its
+  // 64-column tiles: 16384x16x1024 85 -> 12 us): 32x32 blocks with K split
+  // over four waves (eight measured slower at every K)
+  if (!PACKED && (tiles(64, 64) < cus / 2 || tiles(32, 32) <= cus || p.n < 32))
     return launch_small<4>(p, batch, stream);
   if (tiles(128, 128) >= cus) return launch_tile<2, 2, 2, 2, PACKED>(p, batch, stream);
   if (tiles(64, 128) >= cus) return launch_tile<2, 2, 1, 2, PACKED>(p, batch, stream);
@@ -1567,8 +1568,7 @@ int annc_hip_gemm(void* stream, int64_t batch, int64_t m, int64_t n, int64_t k, 
   // 73 (one); 4096x520x1024: 123 -> 46 (two; one launch needs a 5th CU
   // round of tiles: 62).
   const int64_t nf = n & ~int64_t(31);
-  const bool split_n = n % 32 != 0 && nf > 0 && k >= 32 &&
-                       ceil_div(m, 32) * (nf / 32) * batch > 256;
+  const bool split_n = n % 32 != 0 && nf > 0 && ceil_div(m, 32) * (nf / 32) * batch > 256;
   // the pipelined kernel's busiest-CU tile area over nn columns, the least
   // over the tilings its launcher picks from
   auto round_area = [&](int64_t nn) {
@@ -1612,7 +1612,7 @@ int annc_hip_gemm(void* stream, int64_t batch, int64_t m, int64_t n, int64_t k, 
   // for packed B.  N % 32 != 0 (split_n): the first nm = nf columns as below,
   // then the tail columns.
   const int64_t tiles32 = ceil_div(m, 32) * ceil_div(n, 32) * batch;
-  const bool whole = n % 32 == 0 && k >= 32 && tiles32 > 256;
+  const bool whole = n % 32 == 0 && tiles32 > 256;
   if (whole || split_n) {
     if (p.b_vec && (whole || one_launch))
       return launch_packed_pipe(p, batch, s, /*b_rowmajor=*/true);

@@ -521,7 +521,8 @@ def test_row_major_b_packed_per_call(batch, m, n, k, ldb_pad):
                                          (1, 100, 96, 64), (1, 33, 256, 845), (1, 7, 32, 20),
                                          (3, 40, 64, 96), (1, 512, 512, 1024), (1, 256, 1000, 1024),
                                          (1, 100, 300, 845), (1, 17, 40, 33), (2, 40, 70, 96),
-                                         (1, 4096, 16, 1024), (1, 3000, 24, 100)])
+                                         (1, 4096, 16, 1024), (1, 3000, 24, 100),
+                                         (1, 16384, 16, 1024), (1, 65536, 8, 40)])
 def test_packed_small_batches(batch, m, n, k):
     """Packed GEMMs with at most one round of 32x32 blocks (small batches)
     run the small kernel: within the GEMM bound of OpenBLAS, and bit-identical
@@ -581,6 +582,7 @@ N_TAIL_CASES = [
     (1, 4096, 1001, 40, "unaligned rows (pack + small tail), 1 k-block + K tail"),
     (1, 8192, 1000, 864, "256x128 tiles with a partial panel"),
     (1, 1200, 340, 512, "64x32 tiles with a partial panel"),
+    (1, 4096, 1000, 20, "K < 32 (K tail only), partial panel"),
 ]
 
 
