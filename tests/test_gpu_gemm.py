@@ -480,7 +480,8 @@ def test_batch_matmul_add_sigmoid_broadcasts(bias_shape, rhs_batched):
                                                  (64, 512, 160, 101, 4), (70, 512, 224, 64, 3),
                                                  (64, 256, 128, 256, 0), (4, 2048, 320, 845, 0),
                                                  (2, 4096, 1024, 1024, 0), (1, 8192, 1024, 845, 3),
-                                                 (3, 40, 64, 96, 0), (4, 33, 96, 845, 5)])
+                                                 (3, 40, 64, 96, 0), (4, 33, 96, 845, 5),
+                                                 (1, 500, 2048, 1024, 1), (2, 256, 2048, 512, 3)])
 def test_row_major_b_packed_per_call(batch, m, n, k, ldb_pad):
     """Large row-major-B GEMMs run the pipelined kernel, on B read in place or
     packed into the stream workspace: within tolerance of OpenBLAS, and
