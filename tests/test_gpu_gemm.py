@@ -621,6 +621,23 @@ def test_n_tail_split(batch, m, n, k, what):
             assert_gemm_close(got_b[z], ref, gemm_bound(a[z], w[z], np.broadcast_to(bias, ref.shape)))
 
 
+@pytest.mark.parametrize("m,n", [(4096, 1024), (4096, 1000), (64, 40), (8192, 16)])
+def test_k_zero_is_the_epilogue_alone(m, n):
+    """K = 0 through the C ABI with null A and B: every output is the
+    epilogue of addend + bias alone, on each path (pipelined, partial panel,
+    small kernel)."""
+    note(f"K = 0 {m}x{n}")
+    g = workloads.rng(m + n)
+    e = g.standard_normal((m, n)).astype(np.float32)
+    bias = g.standard_normal(n).astype(np.float32)
+    de, dbias = to_dev(e), to_dev(bias)
+    out = torch.empty((m, n), dtype=torch.float32, device=device())
+    _lib.check(_lib.lib().annc_hip_gemm(_lib.stream_ptr(), 1, m, n, 0, None, 0, 0, None, n, 0, 0,
+                                        _lib.ptr(de), n, 0, _lib.ptr(dbias), EPI_RELU,
+                                        _lib.ptr(out), n, 0))
+    np.testing.assert_array_equal(to_host(out), np.maximum(e + bias, np.float32(0)))
+
+
 @pytest.mark.parametrize("m,n,k,col0", [(2048, 512, 256, 1), (8192, 64, 333, 3)])
 def test_pipeline_misaligned_a_base(m, n, k, col0):
     """A starting mid-row of a wider buffer (base not 16-byte aligned, lda a
