@@ -64,16 +64,23 @@ class MLPTower:
 
     With `fuse_score` (the default) a tower whose last layer has one output
     runs its last two layers as one kernel (annc_hip_dense_score) when the
-    shapes allow: the scoring dot reads the hidden layer from registers, and
-    that hidden layer reaches memory only with `keep_hidden`.  Every other
-    layer, and the tail when it does not fit, is one GEMM launch."""
+    shapes allow and the batch has at least `fuse_min_rows` rows: the scoring
+    dot reads the hidden layer from registers, and that hidden layer reaches
+    memory only with `keep_hidden`.  Every other layer, and the tail when it
+    does not fit, is one GEMM launch.  The fused kernel gives each 16 rows a
+    workgroup that streams the whole hidden-layer weight, so its time is
+    flat up to 4096 rows; below 2049 rows the GEMM's small-batch kernels and
+    the GEMV are faster (configs[1]'s 512 -> 256 -> 1 tail: 7.7-8.9 us
+    against 10.6-10.9 up to 1024 rows, tower steps 31.8 against 32.6 us at
+    2048; fused 11.1 against 14.9 us from 2304 rows)."""
 
     def __init__(self, weights: Sequence[np.ndarray], biases: Sequence[np.ndarray],
                  device: torch.device | str = "cuda", packed: bool = True,
                  final_activation: int = _lib.EPI_SIGMOID, fuse_score: bool = True,
-                 keep_hidden: bool = False):
+                 keep_hidden: bool = False, fuse_min_rows: int = 2049):
         self.device = torch.device(device)
         self.keep_hidden = keep_hidden
+        self.fuse_min_rows = fuse_min_rows
         self.layers: list[DenseLayer] = []
         for i, (w, b) in enumerate(zip(weights, biases)):
             wt = torch.as_tensor(np.ascontiguousarray(w, dtype=np.float32)).to(self.device)
@@ -132,7 +139,8 @@ class MLPTower:
         """x: [batch, k0] (any row stride).  Returns the final [batch, 1] buffer."""
         bufs = self.buffers(x.shape[0])
         h = x
-        plain = len(self.layers) - (2 if self.fused_tail else 0)
+        fused = self.fused_tail and x.shape[0] >= self.fuse_min_rows
+        plain = len(self.layers) - (2 if fused else 0)
         for layer, out in zip(self.layers[:plain], bufs):
             dev.gemm(h, layer.weight, bias=layer.bias, epilogue=layer.activation, out=out,
                      stream=stream)

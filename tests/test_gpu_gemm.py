@@ -274,6 +274,28 @@ def test_config2_mlp_tower():
     np.testing.assert_array_equal(to_host(bench_tower(x)), ys[True])
 
 
+@pytest.mark.parametrize("batch", [64, 1024, 2048, 2049])
+def test_tower_fuses_its_tail_above_2048_rows(batch):
+    """configs[1]'s tower runs its 512 -> 256 -> 1 tail as two GEMM launches
+    up to 2048 rows (where the small-batch GEMM kernels beat the fused
+    kernel) and as one dense_score launch above: the hidden layer reaches its
+    buffer only on the first path (keep_hidden off).  Both against the
+    oracle."""
+    note(f"config2 tower tail path at batch {batch}")
+    w = workloads.config2(seed=3, batch=batch)
+    tower = MLPTower(w.weights, w.biases, device=device(), packed=True)
+    assert tower.fused_tail
+    bufs = tower.buffers(batch)
+    bufs[-2].fill_(float("nan"))
+    y = to_host(tower(to_dev(w.x)))
+    np.testing.assert_allclose(y, ora.mlp_tower(w.x, w.weights, w.biases), rtol=1e-3, atol=1e-5)
+    hidden = to_host(bufs[-2])
+    if batch >= 2049:
+        assert np.isnan(hidden).all()
+    else:
+        assert np.isfinite(hidden).all()
+
+
 @pytest.mark.parametrize("widths,offset", [((512, 256, 1), 1), ((512, 256, 1), 4), ((512, 96, 1), 0)])
 def test_tower_tail_fallbacks(widths, offset):
     """Towers whose tail the fused kernel does not take run it as two GEMM
@@ -287,7 +309,7 @@ def test_tower_tail_fallbacks(widths, offset):
     bs = [(g.standard_normal(b) * 0.01).astype(np.float32) for b in widths[1:]]
     xbuf = g.standard_normal((m, widths[0] + 8)).astype(np.float32)
     x = xbuf[:, offset:offset + widths[0]]
-    tower = MLPTower(ws, bs, device=device(), packed=True)
+    tower = MLPTower(ws, bs, device=device(), packed=True, fuse_min_rows=1)
     assert tower.fused_tail == (widths[1] in (64, 128, 256))
     y = to_host(tower(to_dev(xbuf)[:, offset:offset + widths[0]]))
     np.testing.assert_allclose(y, ora.mlp_tower(np.ascontiguousarray(x), ws, bs), rtol=1e-4,
