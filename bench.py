@@ -949,6 +949,38 @@ def gemm_sweep(device) -> None:
                   flush=True)
 
 
+TOWER_SWEEP_ROWS = (1, 16, 64, 256, 512, 1024, 2048, 4096, 8192, 16384)
+
+
+def tower_sweep(device) -> None:
+    """One JSON line per batch size: configs[1]'s tower (MLPTower: packed
+    weights, fused epilogues, the tail fused above 2048 rows) against the
+    same tower in plain torch (hipBLASLt addmm, then relu / sigmoid); best
+    of 3 graphs of 20 forwards each, in us."""
+    import torch
+    from annc_amd import workloads
+    from annc_amd.rec_graph import MLPTower
+    t = workloads.config2(seed=0, batch=1)
+    tower = MLPTower(t.weights, t.biases, device=device)
+    ws = [torch.from_numpy(w).to(device) for w in t.weights]
+    bs = [torch.from_numpy(b).to(device) for b in t.biases]
+
+    def torch_tower(x):
+        h = torch.relu(torch.addmm(bs[0], x, ws[0]))
+        h = torch.relu(torch.addmm(bs[1], h, ws[1]))
+        return torch.sigmoid(torch.addmm(bs[2], h, ws[2]))
+
+    def best(fn):
+        return min(graph_time_ms(lambda i: fn(), 20, 10) for _ in range(3)) * 1e3
+
+    g = torch.Generator().manual_seed(0)
+    for rows in TOWER_SWEEP_ROWS:
+        x = torch.randn(rows, t.weights[0].shape[0], generator=g).to(device)
+        ours, ref = best(lambda: tower.forward(x)), best(lambda: torch_tower(x))
+        print(json.dumps({"rows": rows, "tower_us": round(ours, 2), "torch_us": round(ref, 2),
+                          "tower_tflops": round(tower.flops(rows) / ours / 1e6, 2)}), flush=True)
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -968,6 +1000,8 @@ def main() -> int:
                     help="profiling mode: launch through a replayed HIP graph")
     ap.add_argument("--gemm-sweep", action="store_true",
                     help="time the tower's GEMM layers across batch sizes (one JSON line each)")
+    ap.add_argument("--tower-sweep", action="store_true",
+                    help="time configs[1]'s tower across batch sizes against plain torch")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build targets one GPU; --gpus must be 1 (GEMMs "
@@ -985,6 +1019,9 @@ def main() -> int:
         return 0
     if args.gemm_sweep:
         gemm_sweep(device)
+        return 0
+    if args.tower_sweep:
+        tower_sweep(device)
         return 0
 
     inp = Inputs()
