@@ -240,6 +240,44 @@ def test_dense_score_zero_rows_is_a_no_op():
                                     None, 0, None, 1) == _lib.OK
 
 
+# (batch, m, n, k, lda, ldb, b_packed, b_aligned, epilogue, null_c, message): each
+# rejected by annc_hip_gemm before any launch or pointer access
+GEMM_BAD_ARGS = [
+    (1, -1, 64, 64, 64, 64, 0, True, 0, False, b"negative GEMM dimension"),
+    (-1, 4, 64, 64, 64, 64, 0, True, 0, False, b"negative GEMM dimension"),
+    (1, 1 << 31, 64, 64, 64, 64, 0, True, 0, False, b"too large"),
+    (1, 64, 64, 64, 64, 32, 0, True, 0, False, b"ldb < n"),
+    (1, 64, 64, 64, 32, 64, 0, True, 0, False, b"leading dimension"),
+    (1, 64, 64, 64, 64, 64, 0, True, 8, False, b"unknown epilogue"),
+    (1, 64, 64, 64, 64, 64, 0, True, 0, True, b"null output"),
+    (1, 4096, 64, 64, 64, 64, 1, False, 0, False, b"packed B must be 16-byte aligned"),
+    (1, 64, 64, 64, 64, 64, 0, None, 0, False, b"null operand"),
+]
+
+
+@pytest.mark.parametrize("batch,m,n,k,lda,ldb,packed,aligned,epi,null_c,message", GEMM_BAD_ARGS)
+def test_gemm_rejects_bad_arguments(batch, m, n, k, lda, ldb, packed, aligned, epi, null_c,
+                                    message):
+    """annc_hip_gemm validates its arguments before any launch (these run
+    without a GPU); an empty product returns OK at once."""
+    import ctypes
+    lib = _lib.lib()
+    a = ctypes.c_void_p(16)
+    b = None if aligned is None else ctypes.c_void_p(16 if aligned else 20)
+    c = None if null_c else ctypes.c_void_p(16)
+    rc = lib.annc_hip_gemm(None, batch, m, n, k, a, lda, 0, b, ldb, 0, packed, None, 0, 0, None,
+                           epi, c, n, 0)
+    assert rc == _lib.INVALID_ARGUMENT
+    assert message in lib.annc_hip_last_error()
+
+
+@pytest.mark.parametrize("batch,m,n", [(0, 64, 64), (1, 0, 64), (1, 64, 0)])
+def test_gemm_empty_product_is_a_no_op(batch, m, n):
+    lib = _lib.lib()
+    assert lib.annc_hip_gemm(None, batch, m, n, 64, None, 64, 0, None, 64, 0, 0, None, 0, 0,
+                             None, 0, None, 64, 0) == _lib.OK
+
+
 def test_shape_info_encoding():
     # hlo_util.h:14-21 -- dims then minor_to_major; row-major [512,256] -> {512,256,1,0}
     assert xla.shape_info((512, 256)).tolist() == [512, 256, 1, 0]
