@@ -58,6 +58,9 @@ struct GemmParams {
   int a_vec;  // A rows can be read as aligned float4
   int b_vec;  // row-major B rows can be read as aligned float4
   int b_dense;  // B is a dense row-major [K, N] block (ldb == N), 16-byte aligned
+  // small kernel with K split over gridDim.y workgroups: each writes its
+  // partial sums (no epilogue) to part[split][batch][M][N]
+  float* part;
 };
 
 __device__ __forceinline__ float apply_epilogue(float v, int epilogue) {
@@ -375,7 +378,7 @@ __global__ __launch_bounds__(kThreads) void gemv_rows_kernel(GemmParams p) {
 // guarded block afterwards.  The W partial blocks meet in LDS and wave v
 // adds registers 4v..4v+3 over w = 0..W-1 in that order before the fused
 // epilogue.
-template <int W, bool AVEC, bool PACKED = false>
+template <int W, bool AVEC, bool PACKED = false, bool KSPLIT = false>
 __global__ __launch_bounds__(64 * W) void gemm_small_kernel(GemmParams p) {
   static_assert(W == 4 || W == 8, "4 or 8 waves");
   // PACKED: B in the layout_matmul format: a k-block of the workgroup's
@@ -394,6 +397,12 @@ __global__ __launch_bounds__(64 * W) void gemm_small_kernel(GemmParams p) {
   const int64_t z = blockIdx.z;
   const int M = p.m, N = p.n, K = p.k;
   const int KF = K >> 5;  // full k-blocks
+  // this workgroup's k-blocks [kb0, kb1) (all of them without a K split);
+  // the K % 32 tail goes to the last split
+  const int split = KSPLIT ? (int)blockIdx.y : 0, splits = KSPLIT ? (int)gridDim.y : 1;
+  const int kb0 = KSPLIT ? KF * split / splits : 0;
+  const int kb1 = KSPLIT ? KF * (split + 1) / splits : KF;
+  const bool last_split = !KSPLIT || split == splits - 1;
   const int col = n0 + l32;
   const bool col_ok = col < N;
   const float* __restrict__ arow = p.a + z * p.stride_a + (int64_t)min(m0 + l32, M - 1) * p.lda;
@@ -457,24 +466,24 @@ __global__ __launch_bounds__(64 * W) void gemm_small_kernel(GemmParams p) {
         acc[e & 1] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[buf][q][e], bf[buf][4 * q + e],
                                                           acc[e & 1], 0, 0, 0);
   };
-  if (wave < KF) {
-    // blocks wave, wave+W, ...; the prefetch of a block past the end
-    // re-reads the current one instead of branching
+  if (kb0 + wave < kb1) {
+    // blocks kb0+wave, kb0+wave+W, ...; the prefetch of a block past the
+    // end re-reads the current one instead of branching
     // sched_barrier keeps each prefetch issued ahead of the MFMAs it overlaps
-    load(wave, 0);
-    for (int kt = wave; kt < KF; kt += 2 * W) {
-      load(kt + W < KF ? kt + W : kt, 1);
+    load(kb0 + wave, 0);
+    for (int kt = kb0 + wave; kt < kb1; kt += 2 * W) {
+      load(kt + W < kb1 ? kt + W : kt, 1);
       __builtin_amdgcn_sched_barrier(0);
       mma(0);
       __builtin_amdgcn_sched_barrier(0);
-      if (kt + W >= KF) break;
-      load(kt + 2 * W < KF ? kt + 2 * W : kt + W, 0);
+      if (kt + W >= kb1) break;
+      load(kt + 2 * W < kb1 ? kt + 2 * W : kt + W, 0);
       __builtin_amdgcn_sched_barrier(0);
       mma(1);
       __builtin_amdgcn_sched_barrier(0);
     }
   }
-  if ((K & 31) && wave == KF % W) {
+  if ((K & 31) && last_split && wave == (KF - kb0) % W) {
     const int kb = KF * 32 + 16 * half;
 #pragma unroll
     for (int q = 0; q < 4; ++q)
@@ -503,10 +512,32 @@ __global__ __launch_bounds__(64 * W) void gemm_small_kernel(GemmParams p) {
     for (int w = 1; w < W; ++w) v += red[w][r][lane];
     const int orow = m0 + 8 * wave + 4 * half + i;  // 8*(r>>2) + 4*half + (r&3)
     if (orow >= M || !col_ok) continue;
+    if constexpr (KSPLIT) {
+      p.part[(((int64_t)split * gridDim.z + z) * M + orow) * N + col] = v;
+      continue;
+    }
     if (E) v += e_pre[i];
     if (p.bias) v += bias;
     C[(int64_t)orow * p.ldc + col] = apply_epilogue(v, p.epilogue);
   }
+}
+
+// The K-split small GEMM's second launch: each output is its splits' partial
+// sums added in split order, then the addend, the bias and the epilogue, as
+// the one-launch form adds them to its wave sum.
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmParams p, int splits,
+                                                            int64_t batch) {
+  const int64_t total = batch * p.m * p.n;
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= total) return;
+  const int64_t z = i / ((int64_t)p.m * p.n);
+  const int64_t rem = i % ((int64_t)p.m * p.n);
+  const int64_t row = rem / p.n, col = rem % p.n;
+  float v = p.part[i];
+  for (int s = 1; s < splits; ++s) v += p.part[(int64_t)s * total + i];
+  if (p.e) v += p.e[z * p.stride_e + row * p.lde + col];
+  if (p.bias) v += p.bias[col];
+  p.c[z * p.stride_c + row * p.ldc + col] = apply_epilogue(v, p.epilogue);
 }
 
 // ---------------------------------------------------------------------------
@@ -1265,12 +1296,43 @@ int launch_small(const GemmParams& p0, int64_t batch, hipStream_t stream) {
   GemmParams p = p0;
   p.tiles_m = (p.m + 31) / 32;
   p.tiles_n = (p.n + 31) / 32;
-  dim3 grid(p.tiles_m * p.tiles_n, 1, (unsigned)batch);
-  if (p.a_vec)
+  // Few 32x32 blocks and a long K (at least 16 k-blocks a wave, or 8 with at
+  // most 32 blocks): K split over up to 8 workgroups a block, each split
+  // keeping at least 2 k-blocks a wave, so that up to 256 workgroups run;
+  // their partial sums meet in a second launch, added in split order.
+  // 1x1024x4096: 23.3 -> 8.6 us; 128x1024x4096: 26.7 -> 18.7; 1x512x1024:
+  // 7.5 -> 5.9.  With shorter chains the second launch costs more than the
+  // split saves (256x512x1024, 128 blocks: 9.4 against 9.0 us; 1x256x512,
+  // 4 k-blocks a wave: 5.5 against 4.9).
+  const int64_t blocks = (int64_t)p.tiles_m * p.tiles_n * batch;
+  const int kf = p.k >> 5;
+  int splits = 1;
+  if (kf / W >= 16 || (blocks <= 32 && kf / W >= 8))
+    while (splits < 8 && blocks * splits * 2 <= 256 && kf / (splits * 2) >= 2 * W) splits *= 2;
+  p.part = nullptr;
+  if (splits > 1) {
+    const size_t bytes = (size_t)splits * batch * p.m * p.n * sizeof(float);
+    p.part = static_cast<float*>(stream_workspace(stream, bytes));
+    if (!p.part) splits = 1;
+  }
+  dim3 grid(p.tiles_m * p.tiles_n, splits, (unsigned)batch);
+  if (splits > 1) {
+    if (p.a_vec)
+      hipLaunchKernelGGL((gemm_small_kernel<W, true, PACKED, true>), grid, dim3(64 * W), 0, stream, p);
+    else
+      hipLaunchKernelGGL((gemm_small_kernel<W, false, PACKED, true>), grid, dim3(64 * W), 0, stream, p);
+  } else if (p.a_vec) {
     hipLaunchKernelGGL((gemm_small_kernel<W, true, PACKED>), grid, dim3(64 * W), 0, stream, p);
-  else
+  } else {
     hipLaunchKernelGGL((gemm_small_kernel<W, false, PACKED>), grid, dim3(64 * W), 0, stream, p);
+  }
   ANNC_HIP_TRY(hipGetLastError());
+  if (splits > 1) {
+    const int64_t total = batch * p.m * p.n;
+    hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)ceil_div(total, 256)), dim3(256), 0,
+                       stream, p, splits, batch);
+    ANNC_HIP_TRY(hipGetLastError());
+  }
   return ANNC_OK;
 }
 

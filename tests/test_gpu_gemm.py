@@ -643,6 +643,44 @@ def test_n_tail_split(batch, m, n, k, what):
             assert_gemm_close(got_b[z], ref, gemm_bound(a[z], w[z], np.broadcast_to(bias, ref.shape)))
 
 
+# Few 32x32 blocks with a long K: K split over up to 8 workgroups, partial sums
+# added in split order by a second launch (K tails in the last split)
+SPLITK_CASES = [
+    (1, 1, 1024, 4096, "8 splits"),
+    (1, 64, 512, 4096, "8 splits, 2 row blocks"),
+    (1, 16, 512, 1024, "4 splits (few blocks)"),
+    (1, 100, 1000, 2100, "partial panel, K tail"),
+    (3, 20, 96, 3000, "batched, K tail"),
+    (1, 128, 1024, 4096, "2 splits"),
+]
+
+
+@pytest.mark.parametrize("batch,m,n,k,what", SPLITK_CASES)
+def test_split_k_small_gemm(batch, m, n, k, what):
+    """Within the GEMM bound of OpenBLAS with an addend, bias and ReLU, on
+    packed and row-major B (bit-identical: the same kernels), batched through
+    one call."""
+    note(f"split-K small GEMM b={batch} {m}x{n}x{k}: {what}")
+    g = workloads.rng(m + 3 * n + k + batch)
+    a = g.standard_normal((batch, m, k)).astype(np.float32)
+    w = (g.standard_normal((batch, k, n)) / np.sqrt(k)).astype(np.float32)
+    e = g.standard_normal((batch, m, n)).astype(np.float32)
+    bias = (g.standard_normal(n) * 0.1).astype(np.float32)
+    da, de, dbias = to_dev(a), to_dev(e), to_dev(bias)
+    for z in range(batch):
+        got = to_host(dev.gemm(da[z], dev.pack_weight(to_dev(w[z])), addend=de[z], bias=dbias,
+                               epilogue=EPI_RELU))
+        ref = np.maximum(ora.matmul_add(e[z] + bias, a[z], w[z]), 0)
+        assert_gemm_close(got, ref, gemm_bound(a[z], w[z], np.abs(e[z]) + np.abs(bias)))
+        if n % 4 == 0:
+            rm = to_host(dev.gemm(da[z], to_dev(w[z]), addend=de[z], bias=dbias, epilogue=EPI_RELU))
+            np.testing.assert_array_equal(got, rm)
+    got_b = to_host(dev.gemm(da, to_dev(w), addend=de, bias=dbias, epilogue=EPI_RELU))
+    for z in range(batch):
+        ref = np.maximum(ora.matmul_add(e[z] + bias, a[z], w[z]), 0)
+        assert_gemm_close(got_b[z], ref, gemm_bound(a[z], w[z], np.abs(e[z]) + np.abs(bias)))
+
+
 @pytest.mark.parametrize("m,n", [(4096, 1024), (4096, 1000), (64, 40), (8192, 16)])
 def test_k_zero_is_the_epilogue_alone(m, n):
     """K = 0 through the C ABI with null A and B: every output is the
