@@ -336,6 +336,34 @@ def test_config2_tower_graph_replays(fuse):
         torch.cuda.synchronize()
 
 
+@pytest.mark.parametrize("batch_rows", [1, 64])
+def test_small_batch_tower_graph_replays(batch_rows):
+    """A small-batch tower with a long-K first layer (4096 -> 1024, K split
+    across workgroups and reduced in a second launch) and the unfused tail,
+    captured into a HIP graph: three replays, each after new inputs were
+    copied into the captured input buffer and after eager forwards of other
+    inputs on the same buffers, each equal to an eager forward of the same
+    input and within the oracle's tolerance."""
+    note(f"small-batch tower graph, {batch_rows} rows")
+    widths = (4096, 1024, 256, 1)
+    g = workloads.rng(batch_rows + 11)
+    ws = [workloads.glorot_uniform(g, a, b) for a, b in zip(widths[:-1], widths[1:])]
+    bs = [(g.standard_normal(b) * 0.01).astype(np.float32) for b in widths[1:]]
+    tower = MLPTower(ws, bs, device=device(), packed=True)
+    xs = [g.standard_normal((batch_rows, widths[0])).astype(np.float32) for _ in range(4)]
+    x = to_dev(xs[0])
+    graph = CapturedGraph(tower, x)
+    for r in range(1, 4):
+        x.copy_(to_dev(xs[r]))
+        y = to_host(graph.replay()).copy()
+        torch.cuda.synchronize()
+        eager = to_host(tower(to_dev(xs[r]))).copy()
+        np.testing.assert_array_equal(y, eager, err_msg=f"replay {r}")
+        np.testing.assert_allclose(y, ora.mlp_tower(xs[r], ws, bs), rtol=1e-3, atol=1e-5)
+        to_host(tower(to_dev(xs[(r + 1) % 4])))  # eager work on the same buffers
+        torch.cuda.synchronize()
+
+
 def test_config5_wide_deep_graph():
     note("config5 wide&deep")
     w = workloads.config5(seed=0)
