@@ -70,6 +70,13 @@ void* stream_workspace(hipStream_t stream, size_t bytes) {
   std::lock_guard<std::mutex> lock(g_mu);
   StreamState& st = g_streams[{current_device(), stream}];
   if (bytes <= st.workspace_bytes) return st.workspace;
+  // No allocation while the stream is being captured into a graph (hipMalloc
+  // and hipFree would break the capture): callers then take a path that
+  // needs no workspace
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  if (stream && hipStreamIsCapturing(stream, &cap) == hipSuccess &&
+      cap != hipStreamCaptureStatusNone)
+    return nullptr;
   if (st.workspace) {
     (void)hipFree(st.workspace);  // synchronises the device: prior users are done
     st.workspace = nullptr;

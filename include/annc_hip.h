@@ -198,8 +198,10 @@ int annc_hip_layout_matmul_pack_rhs(void* stream, int64_t k, int64_t n, const fl
 /* addend (lde, stride_e) and bias (length n) may be NULL.  All device.      */
 /* Workspace: row-major B whose rows are not 16-byte aligned (packed per     */
 /* call) and small products with a long K (K split across workgroups) use a  */
-/* per-stream workspace that the library allocates, or grows, on first use; */
-/* run such a shape once on a stream before capturing it into a HIP graph.   */
+/* per-stream workspace that the library allocates, or grows, on first use.  */
+/* It never allocates while the stream is being captured into a HIP graph:   */
+/* such a call then takes a path without workspace (slower, same results to  */
+/* the GEMM tolerance), or uses the workspace an earlier call left.          */
 /* Tuning: the environment variable ANNC_GEMM_PIPE = "mi16" or "mi16w8"      */
 /* runs one-batch packed GEMMs with K % 32 == 0 on 16x16 MFMA blocks          */
 /* (v_mfma_f32_16x16x4f32) instead of the default 32x32 tiling.               */

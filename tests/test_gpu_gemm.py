@@ -364,6 +364,33 @@ def test_small_batch_tower_graph_replays(batch_rows):
         torch.cuda.synchronize()
 
 
+@pytest.mark.parametrize("m,n,k,ldb_pad", [(1, 1024, 4096, 0), (4096, 512, 256, 1)])
+def test_gemm_captured_without_warm_up(m, n, k, ldb_pad):
+    """GEMMs that use the per-stream workspace (a K-split small product, a
+    row-major B with unaligned rows) captured on a fresh stream with no call
+    before: no allocation happens under capture (the library takes a path
+    without workspace), and the replays give the oracle's result."""
+    note(f"GEMM captured without warm-up {m}x{n}x{k} ldb+{ldb_pad}")
+    g = workloads.rng(m + n + k)
+    a = g.standard_normal((m, k)).astype(np.float32)
+    wide = (g.standard_normal((k, n + ldb_pad)) / np.sqrt(k)).astype(np.float32)
+    w = np.ascontiguousarray(wide[:, :n])
+    bias = (g.standard_normal(n) * 0.1).astype(np.float32)
+    da, dbias = to_dev(a), to_dev(bias)
+    b = to_dev(wide)[:, :n] if ldb_pad else dev.pack_weight(to_dev(w))
+    out = torch.empty((m, n), dtype=torch.float32, device=device())
+    stream = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        dev.gemm(da, b, bias=dbias, epilogue=EPI_RELU, out=out)
+    ref = ora.dense_layer(a, w, bias, 1)
+    for _ in range(2):
+        out.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert_gemm_close(to_host(out), ref, gemm_bound(a, w, np.broadcast_to(bias, ref.shape)))
+
+
 def test_config5_wide_deep_graph():
     note("config5 wide&deep")
     w = workloads.config5(seed=0)
