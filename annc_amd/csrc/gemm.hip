@@ -541,7 +541,8 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmParams p, int sp
 }
 
 // ---------------------------------------------------------------------------
-// Packed-B pipelined kernel (the __layout_matmul path, N % 32 == 0).
+// Packed-B pipelined kernel (the __layout_matmul path; row-major B with BRM;
+// a partial last 32-column panel with NTAIL).
 //
 // Operand tiles stream global -> LDS through gfx950's 16-byte LDS-DMA loads
 // (global_load_lds_dwordx4: lane i of a wave writes bytes [16i, 16i+16) of a
@@ -572,7 +573,10 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmParams p, int sp
 //     itself (wait_vmcnt) and fences the barrier as asm as well.
 //   * Rows past M and panels past N are clamped for loading and never
 //     stored; a K tail (K % 32) is folded in after the loop from the
-//     packed format's row-major tail region with guarded loads.
+//     packed format's row-major tail regions with guarded loads.
+//   * NTAIL: the partial panel's B blocks load with four 4-byte DMAs each
+//     (the packed format's N-tail region, or the row-major rows), columns
+//     clamped to N - 1.
 // ---------------------------------------------------------------------------
 namespace pipe {
 
