@@ -192,6 +192,11 @@ def embedding_bag(table: torch.Tensor, ids: torch.Tensor, offsets: torch.Tensor,
     if out is None:
         out = torch.empty((nbags, dim), dtype=torch.float32, device=table.device)
     ldo = _row_major_2d(out, "out")
+    if ids.numel() == 0:
+        # no ids (a null data pointer, which the C entry rejects): offsets
+        # consistent with them leave every bag empty, i.e. 0 under both
+        # combiners
+        return out.zero_()
     check(_lib.lib().annc_hip_embedding_bag(stream_ptr(stream), ptr(table), rows, dim, ptr(ids),
                                             1 if ids.dtype == torch.int64 else 0, ptr(offsets),
                                             nbags, combiner, ptr(out), ldo))

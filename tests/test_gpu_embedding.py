@@ -46,6 +46,39 @@ def test_bag_dims_bit_exact(dim):
         np.testing.assert_array_equal(to_host(out), ref)
 
 
+@pytest.mark.parametrize("seed", range(48))
+def test_bag_random_configurations(seed):
+    """Seeded random bags: dims of every lane-group width and the scalar
+    path, 1 to 20000 bags of Poisson or heavy-tailed lengths (empty bags
+    included), uniform or Zipf ids, int32 and int64 ids, both combiners, an
+    output with padded rows; bit-exact against the sequential loop, the
+    padding untouched."""
+    g = np.random.default_rng(5000 + seed)
+    dim = int(g.choice([1, 2, 3, 4, 6, 8, 12, 16, 20, 32, 60, 64, 100, 128, 256, 260, 512]))
+    rows = min(int(g.integers(1, 200_000)), 20_000_000 // dim)
+    nbags = int(g.choice([1, 5, 300, 4096, 20000]))
+    lens = (g.poisson(g.choice([0.3, 3, 20, 200]), size=nbags) if seed % 3 else
+            np.minimum(g.zipf(1.4, size=nbags) - 1, 2000))
+    offsets = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    n = int(offsets[-1])
+    ids = (g.integers(0, rows, size=n) if seed % 2 else
+           np.minimum(g.zipf(1.2, size=n) - 1, rows - 1))
+    ids = ids.astype(np.int64 if seed % 4 < 2 else np.int32)
+    table = g.standard_normal((rows, dim)).astype(np.float32)
+    pad = int(g.choice([0, 3]))
+    note(f"bag random config seed={seed}: dim {dim} rows {rows} bags {nbags} ids {n} "
+         f"{ids.dtype} pad {pad}")
+    dt, di, do = to_dev(table), to_dev(ids), to_dev(offsets)
+    for combiner in (0, 1):
+        obuf = torch.full((nbags, dim + pad), float("nan"), device=device())
+        dev.embedding_bag(dt, di, do, combiner, out=obuf[:, :dim])
+        dev.stream_status()
+        got = to_host(obuf)
+        np.testing.assert_array_equal(got[:, :dim],
+                                      ora.embedding_bag(table, ids, offsets, combiner, threads=8))
+        assert np.isnan(got[:, dim:]).all()
+
+
 def test_bag_strided_output_and_no_bags():
     note("bag strided output")
     g = workloads.rng(1)
@@ -285,7 +318,7 @@ def test_device_segment_reduce_any_order_dims(dim, idx64):
                                                                        combiner))
 
 
-@pytest.mark.parametrize("seed", range(24))
+@pytest.mark.parametrize("seed", range(64))
 def test_device_segment_reduce_random_configurations(seed):
     """Seeded random configurations across both paths (sorted promise or
     not): dims of every lane-group width and the scalar path, int32 and

@@ -770,6 +770,81 @@ def test_pipeline_misaligned_a_base(m, n, k, col0):
     np.testing.assert_array_equal(to_host(dev.gemm(da, to_dev(w))), got)
 
 
+def _log_uniform(g, lo, hi):
+    return int(np.exp(g.uniform(np.log(lo), np.log(hi + 1))))
+
+
+def _sweep_case(seed):
+    """A seeded random GEMM call: shape, batch, B layout, operand strides and
+    epilogue drawn so that every dispatch path turns up over the seeds (GEMV,
+    small kernel with and without K split, 64x32, 128x64, 128x128 and
+    256x128 tiles, partial panels, N < 32, K tails, per-call packing)."""
+    g = workloads.rng(1000 + seed)
+    batch = int(g.choice([1, 1, 1, 2, 3]))
+    m = _log_uniform(g, 1, 9000) if g.random() < 0.5 else _log_uniform(g, 512, 9000)
+    n = _log_uniform(g, 1, 1100) if g.random() < 0.5 else _log_uniform(g, 64, 1100)
+    k = _log_uniform(g, 1, 4500)
+    if g.random() < 0.3:
+        n = max(32, n // 32 * 32)
+    if g.random() < 0.3:
+        k = max(32, k // 32 * 32)
+    while batch * m * n * k > 1_500_000_000:
+        m = max(1, m // 2)
+    return dict(
+        batch=batch, m=m, n=n, k=k,
+        packed=batch == 1 and bool(g.random() < 0.5),
+        ldb_pad=int(g.choice([0, 0, 1, 3, 4, 33])),
+        col0=int(g.choice([0, 0, 1, 4])),
+        ldc_pad=int(g.choice([0, 0, 5])),
+        addend=bool(g.random() < 0.5),
+        bias=bool(g.random() < 0.5),
+        epi=int(g.choice([EPI_NONE, EPI_RELU, EPI_SIGMOID])),
+    )
+
+
+@pytest.mark.parametrize("seed", range(256))
+def test_gemm_random_shapes(seed):
+    """Seeded random calls through annc_hip_gemm: within the GEMM bound of
+    OpenBLAS (sigmoid: within 1e-4 relative, 1e-5 absolute of the logistic of
+    OpenBLAS's sum), padding columns of the output untouched."""
+    c = _sweep_case(seed)
+    batch, m, n, k = c["batch"], c["m"], c["n"], c["k"]
+    note(f"random GEMM seed={seed} {c}")
+    g = workloads.rng(seed)
+    abuf = g.standard_normal((batch, m, k + c["col0"] + 3)).astype(np.float32)
+    a = abuf[:, :, c["col0"]:c["col0"] + k]
+    w = (g.standard_normal((batch, k, n + c["ldb_pad"])) / np.sqrt(max(k, 1))).astype(np.float32)
+    wv = w[:, :, :n]
+    e = g.standard_normal((batch, m, n)).astype(np.float32) if c["addend"] else None
+    bias = (g.standard_normal(n) * 0.1).astype(np.float32) if c["bias"] else None
+    da = to_dev(abuf)[:, :, c["col0"]:c["col0"] + k]
+    dw = to_dev(w)[:, :, :n]
+    obuf = torch.full((batch, m, n + c["ldc_pad"]), float("nan"), device=device())
+    if batch == 1:
+        b_arg = dev.pack_weight(dw[0]) if c["packed"] else dw[0]
+        dev.gemm(da[0], b_arg, addend=None if e is None else to_dev(e[0]),
+                 bias=None if bias is None else to_dev(bias), epilogue=c["epi"],
+                 out=obuf[0, :, :n])
+    else:
+        dev.gemm(da, dw, addend=None if e is None else to_dev(e),
+                 bias=None if bias is None else to_dev(bias), epilogue=c["epi"],
+                 out=obuf[:, :, :n])
+    got = to_host(obuf)
+    assert np.isnan(got[:, :, n:]).all(), "padding columns of the output were written"
+    for z in range(batch):
+        add = np.zeros((m, n), np.float32) if e is None else e[z]
+        if bias is not None:
+            add = add + bias
+        lin = ora.matmul_add(add, np.ascontiguousarray(a[z]), np.ascontiguousarray(wv[z]))
+        gz = got[z, :, :n]
+        if c["epi"] == EPI_SIGMOID:
+            np.testing.assert_allclose(gz, 1.0 / (1.0 + np.exp(-lin.astype(np.float64))),
+                                       rtol=1e-4, atol=1e-5)
+        else:
+            ref = np.maximum(lin, 0) if c["epi"] == EPI_RELU else lin
+            assert_gemm_close(gz, ref, gemm_bound(a[z], wv[z], np.abs(add)))
+
+
 def test_custom_calls_from_concurrent_threads():
     """The synchronous custom calls run on a stream of the calling thread:
     threads calling __matmul_add_relu at once (host buffers staged through
