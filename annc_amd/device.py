@@ -339,6 +339,10 @@ def hashed_embedding_bags(tables: Sequence[torch.Tensor], num_buckets: Sequence[
     if out is None:
         out = torch.empty((batch, nf * dim), dtype=torch.float32, device=ids.device)
     ldo = _row_major_2d(out, "out")
+    if ids.numel() == 0 and nf * batch > 0:
+        # no ids (a null data pointer, which the C entry rejects): every bag
+        # is empty, 0 under both combiners
+        return out.zero_()
     tptrs = (ctypes_array_u64([t.data_ptr() for t in tables]))
     rows = np.asarray([t.shape[0] for t in tables], dtype=np.int64)
     nb = np.asarray(list(num_buckets), dtype=np.int64)

@@ -94,6 +94,38 @@ def test_bag_strided_output_and_no_bags():
     assert empty.shape == (0, 16)
 
 
+def test_empty_inputs_through_the_device_wrappers():
+    """No ids, keys or strings: empty tensors (torch gives them null data
+    pointers) through every device wrapper give empty results, or all-zero
+    bags and segments, and leave no error on the stream."""
+    note("empty inputs through the device wrappers")
+    d = device()
+    table = to_dev(np.arange(40, dtype=np.float32).reshape(10, 4))
+    none64 = torch.empty(0, dtype=torch.int64, device=d)
+    for combiner in (0, 1):
+        out = dev.embedding_bag(table, none64, torch.zeros(3, dtype=torch.int64, device=d),
+                                combiner)
+        np.testing.assert_array_equal(to_host(out), np.zeros((2, 4), np.float32))
+        out = dev.hashed_embedding_bags([table, table], [10, 7], none64,
+                                        torch.zeros(2 * 3 + 1, dtype=torch.int64, device=d), 3,
+                                        combiner)
+        np.testing.assert_array_equal(to_host(out), np.zeros((3, 8), np.float32))
+        out = dev.segment_reduce(table, none64, none64, 3, combiner)
+        np.testing.assert_array_equal(to_host(out), np.zeros((3, 4), np.float32))
+    assert dev.sparse_embedding2(table, none64).shape == (0, 4)
+    assert dev.hash_bucket_int64(none64, 100).shape == (0,)
+    u, idx, rows = dev.unique_gather(table, none64)
+    assert u.shape == (0,) and idx.shape == (0,) and rows.shape == (0, 4)
+    pooled = dev.pooling(torch.empty((0, 3), dtype=torch.int64, device=d),
+                         torch.empty((0, 3, 4), dtype=torch.float32, device=d), [0, 0, 0],
+                         [0, 3, 4])
+    assert pooled.shape == (0, 4)
+    data, offs = dev.strings_to_device([""], d)
+    got = to_host(dev.fingerprint64(data, offs))
+    np.testing.assert_array_equal(got.view(np.uint64), ora.fingerprint64_batch([b""]))
+    dev.stream_status()
+
+
 def test_bag_out_of_range_ids_flagged():
     note("bag out-of-range ids")
     table = np.ones((10, 8), dtype=np.float32)
