@@ -24,8 +24,10 @@ void clear_error();
 // into it when they meet an out-of-range row id.
 int* stream_status(hipStream_t stream);
 
-// Grow-only device scratch owned by the library, one per stream.  Growing
-// frees the previous buffer (hipFree synchronises the device first).
+// Grow-only device scratch owned by the library, one per (device, stream,
+// calling thread).  An outgrown buffer is kept until the process ends (graphs
+// captured with it replay with its address).  nullptr while the stream is
+// being captured and the buffer is too small, or when hipMalloc fails.
 void* stream_workspace(hipStream_t stream, size_t bytes);
 
 // The library's own stream of the calling thread on the current device

@@ -7,6 +7,7 @@
 #include <mutex>
 #include <string>
 #include <utility>
+#include <vector>
 
 #include "common.h"
 
@@ -17,16 +18,26 @@ thread_local std::string g_last_error;
 
 struct StreamState {
   int* status = nullptr;
-  void* workspace = nullptr;
-  size_t workspace_bytes = 0;
 };
 
 std::mutex g_mu;
 // Keyed by (device, stream): the NULL stream exists once per device.
 std::map<std::pair<int, hipStream_t>, StreamState> g_streams;
+
+// Workspace per (device, stream) and calling thread: threads that enqueue on
+// one stream interleave their launches, so each call's partials need a
+// buffer no other thread writes.
+struct Workspace {
+  void* ptr = nullptr;
+  size_t bytes = 0;
+};
+thread_local std::map<std::pair<int, hipStream_t>, Workspace> t_workspaces;
+// Outgrown workspaces, kept until the process ends: a HIP graph captured with
+// one replays with its address (guarded by g_mu).
+std::vector<void*> g_retired;
 // The synchronous XLA/TF entries run on a library stream of the calling
 // thread: concurrent callers never share a stream, so their kernels cannot
-// interleave and each stream's workspace has a single user.
+// interleave.
 thread_local std::map<int, hipStream_t> t_lib_streams;
 
 int current_device() {
@@ -67,28 +78,30 @@ int* stream_status(hipStream_t stream) {
 }
 
 void* stream_workspace(hipStream_t stream, size_t bytes) {
-  std::lock_guard<std::mutex> lock(g_mu);
-  StreamState& st = g_streams[{current_device(), stream}];
-  if (bytes <= st.workspace_bytes) return st.workspace;
+  Workspace& w = t_workspaces[{current_device(), stream}];
+  if (bytes <= w.bytes) return w.ptr;
   // No allocation while the stream is being captured into a graph (hipMalloc
-  // and hipFree would break the capture): callers then take a path that
-  // needs no workspace
+  // would break the capture): callers then take a path that needs no
+  // workspace
   hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
   if (stream && hipStreamIsCapturing(stream, &cap) == hipSuccess &&
       cap != hipStreamCaptureStatusNone)
     return nullptr;
-  if (st.workspace) {
-    (void)hipFree(st.workspace);  // synchronises the device: prior users are done
-    st.workspace = nullptr;
-    st.workspace_bytes = 0;
-  }
-  size_t want = bytes < (1u << 20) ? (1u << 20) : bytes + bytes / 4;
-  if (hipMalloc(&st.workspace, want) != hipSuccess) {
-    st.workspace = nullptr;
+  // At least twice the outgrown size, so the retired buffers together stay
+  // below the live one.
+  const size_t want = std::max({size_t(1) << 20, bytes + bytes / 4, 2 * w.bytes});
+  void* p = nullptr;
+  if (hipMalloc(&p, want) != hipSuccess) {
+    (void)hipGetLastError();
     return nullptr;
   }
-  st.workspace_bytes = want;
-  return st.workspace;
+  if (w.ptr) {
+    std::lock_guard<std::mutex> lock(g_mu);
+    g_retired.push_back(w.ptr);
+  }
+  w.ptr = p;
+  w.bytes = want;
+  return p;
 }
 
 hipStream_t lib_stream() {

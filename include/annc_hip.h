@@ -198,7 +198,13 @@ int annc_hip_layout_matmul_pack_rhs(void* stream, int64_t k, int64_t n, const fl
 /* addend (lde, stride_e) and bias (length n) may be NULL.  All device.      */
 /* Workspace: row-major B whose rows are not 16-byte aligned (packed per     */
 /* call) and small products with a long K (K split across workgroups) use a  */
-/* per-stream workspace that the library allocates, or grows, on first use.  */
+/* workspace per stream and calling thread (threads that share a stream     */
+/* interleave their launches), which the library allocates, or grows, on     */
+/* first use.  An outgrown one is kept until the process ends, since a HIP   */
+/* graph captured with it replays with its address; each growth at least    */
+/* doubles it, so those kept add up to less than the live one.  A captured   */
+/* graph uses the workspace on every replay: its replays and other calls of  */
+/* the capturing thread on that stream must not overlap.                     */
 /* It never allocates while the stream is being captured into a HIP graph:   */
 /* such a call then takes a path without workspace (slower, same results to  */
 /* the GEMM tolerance), or uses the workspace an earlier call left.          */

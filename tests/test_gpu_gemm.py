@@ -391,6 +391,88 @@ def test_gemm_captured_without_warm_up(m, n, k, ldb_pad):
         assert_gemm_close(to_host(out), ref, gemm_bound(a, w, np.broadcast_to(bias, ref.shape)))
 
 
+def test_graph_replays_after_the_workspace_grows():
+    """A GEMM that packs unaligned B rows into the workspace, captured after a
+    warm-up on the capture stream; eager calls of the same thread on that
+    stream then need a larger workspace (it grows; the outgrown one, which
+    the graph holds, is kept): later replays equal the first bit for bit and
+    stay within the GEMM bound."""
+    note("graph replay after the workspace grows")
+    g = workloads.rng(77)
+    m, n, k = 600, 1024, 512
+    a = g.standard_normal((m, k)).astype(np.float32)
+    wide = (g.standard_normal((k, n + 1)) / np.sqrt(k)).astype(np.float32)
+    w = np.ascontiguousarray(wide[:, :n])
+    bias = (g.standard_normal(n) * 0.1).astype(np.float32)
+    da, db, dbias = to_dev(a), to_dev(wide)[:, :n], to_dev(bias)
+    out = torch.empty((m, n), dtype=torch.float32, device=device())
+    graph = CapturedGraph(lambda: dev.gemm(da, db, bias=dbias, epilogue=EPI_RELU, out=out))
+    first = to_host(graph.replay()).copy()
+    ref = ora.dense_layer(a, w, bias, 1)
+    assert_gemm_close(first, ref, gemm_bound(a, w, np.broadcast_to(bias, ref.shape)))
+    big_k = 4096
+    a2 = g.standard_normal((m, big_k)).astype(np.float32)
+    wide2 = (g.standard_normal((big_k, 2 * n + 1)) / np.sqrt(big_k)).astype(np.float32)
+    with torch.cuda.stream(graph.stream):
+        big = dev.gemm(to_dev(a2), to_dev(wide2)[:, :2 * n])
+    torch.cuda.synchronize()
+    assert_gemm_close(to_host(big), ora.matmul(a2, np.ascontiguousarray(wide2[:, :2 * n])),
+                      gemm_bound(a2, wide2[:, :2 * n]))
+    for _ in range(3):
+        out.zero_()
+        np.testing.assert_array_equal(to_host(graph.replay()), first)
+
+
+def test_workspace_calls_from_two_threads_on_one_stream():
+    """Two threads enqueue workspace-using calls (per-call packing of
+    unaligned B rows, K split, the any-order segment reduction) on one stream
+    at once, each in its own order, so their launches interleave and each
+    thread's workspace grows meanwhile: every result equals the same call's
+    single-threaded result bit for bit."""
+    import threading
+    note("workspace calls from two threads on one stream")
+    g = workloads.rng(78)
+    stream = torch.cuda.Stream()
+    calls = []
+    for m, n, k, pad in [(600, 2048, 1024, 1), (1, 1024, 4096, 0), (300, 1000, 2100, 3),
+                         (64, 512, 4096, 0), (600, 2048, 2048, 1)]:
+        a = to_dev(g.standard_normal((m, k)).astype(np.float32))
+        b = to_dev((g.standard_normal((k, n + pad)) / np.sqrt(k)).astype(np.float32))[:, :n]
+        calls.append(lambda a=a, b=b: dev.gemm(a, b, epilogue=EPI_RELU))
+    table = to_dev(g.standard_normal((100_000, 64)).astype(np.float32))
+    idx = to_dev(g.integers(0, 100_000, size=80_000).astype(np.int64))
+    seg = to_dev(g.permutation(np.repeat(np.arange(4096), 20)[:80_000]).astype(np.int64))
+    calls.append(lambda: dev.segment_reduce(table, idx, seg, 4096, 1))
+    with torch.cuda.stream(stream):
+        expected = [to_host(c()).copy() for c in calls]
+    got = {0: [], 1: []}
+    errors = []
+
+    def run(t):
+        try:
+            order = list(range(len(calls)))
+            if t:
+                order.reverse()
+            with torch.cuda.stream(stream):
+                for _ in range(4):
+                    for i in order:
+                        got[t].append((i, calls[i]()))
+        except Exception as e:  # reported by the main thread
+            errors.append(e)
+
+    threads = [threading.Thread(target=run, args=(t,)) for t in (0, 1)]
+    for th in threads:
+        th.start()
+    for th in threads:
+        th.join()
+    assert not errors, errors
+    torch.cuda.synchronize()
+    for t in (0, 1):
+        assert len(got[t]) == 4 * len(calls)
+        for i, y in got[t]:
+            np.testing.assert_array_equal(to_host(y), expected[i], err_msg=f"thread {t} call {i}")
+
+
 def test_config5_wide_deep_graph():
     note("config5 wide&deep")
     w = workloads.config5(seed=0)
