@@ -280,6 +280,32 @@ def make_case(name: str, device, inp: Inputs) -> Case:
                     2.0 * 512 * 256 * 256, "mfma",
                     "configs[0] __matmul_add_relu 512x256x256, row-major B, materialised addend",
                     "gemm_small_config1_512x256x256", launches=100)
+    if name == "gemm_l1_b64":
+        # configs[1] layer 1 at a serving batch of 64 rows: 32 blocks of
+        # 32x32, K split over 4 workgroups, then the ordered reduction
+        w = inp.get("config2")
+        x = t(w.x[:64])
+        wt = dev.pack_weight(t(w.weights[0]))
+        bias = t(w.biases[0])
+        out = torch.empty((64, wt.n), dtype=torch.float32, device=device)
+        return Case(name, lambda i: dev.gemm(x, wt, bias=bias, epilogue=EPI_RELU, out=out),
+                    2.0 * 64 * wt.n * wt.k, "mfma",
+                    f"configs[1] layer 1 at 64 rows: [64x{wt.k}] . packed [{wt.k}x{wt.n}] + bias, "
+                    "ReLU (small kernel, K split in 4, then the reduction)",
+                    "gemm_small_splitk_64x512x1024", launches=100)
+    if name == "gemm_ntail":
+        # a layer whose width is not a multiple of 32: the pipelined kernel
+        # with a partial last panel (4-byte LDS DMAs of the packed N tail)
+        g = workloads.rng(9)
+        m, k, n = 4096, 1024, 1000
+        x = t(g.standard_normal((m, k)).astype(np.float32))
+        wt = dev.pack_weight(t(workloads.glorot_uniform(g, k, n)))
+        bias = t((g.standard_normal(n) * 0.01).astype(np.float32))
+        out = torch.empty((m, n), dtype=torch.float32, device=device)
+        return Case(name, lambda i: dev.gemm(x, wt, bias=bias, epilogue=EPI_RELU, out=out),
+                    2.0 * m * n * k, "mfma",
+                    f"[{m}x{k}] . packed [{k}x{n}] + bias, ReLU (31 full panels and a partial "
+                    "one of 8 columns)", "gemm_ntail_4096x1000x1024")
     if name == "gemm_e2e_l1":
         w = inp.get("config5")
         k0 = w.weights[0].shape[0]
@@ -508,7 +534,8 @@ def make_case(name: str, device, inp: Inputs) -> Case:
     raise ValueError(f"unknown case {name!r}; choose from {CASES}")
 
 
-CASES = ("tower", "widedeep", "gemm_l1", "tower_tail", "gemm_l2", "gemm_l3", "gemm_small", "gemm_e2e_l1", "batch_matmul",
+CASES = ("tower", "widedeep", "gemm_l1", "tower_tail", "gemm_l2", "gemm_l3", "gemm_small",
+         "gemm_l1_b64", "gemm_ntail", "gemm_e2e_l1", "batch_matmul",
          "bag_sum", "bag_mean", "bag_sum_cold", "bag_phase_empty", "bag_phase_hotrow", "hashed",
          "hashed_cold", "hashed_nohash", "hashed_dim32", "sparse_embedding2", "pooling",
          "segment_reduce_sorted",
