@@ -1,6 +1,7 @@
-"""The CPU test suite against the host-code AddressSanitizer build of the
-library (the host C++ -- custom calls, TF-op entries, flags, rewriter,
-packers, runtime -- instrumented; device code is not).
+"""The CPU test suite against the host-code AddressSanitizer and
+UndefinedBehaviorSanitizer build of the library (the host C++ -- custom
+calls, TF-op entries, flags, rewriter, packers, runtime -- instrumented;
+device code is not).  UBSan reports print as "runtime error" lines.
 
     make -C annc_amd/csrc asan
     ASAN_OPTIONS=detect_leaks=0 \\
