@@ -14,7 +14,7 @@ GEMM + bias + ReLU): 2*M*N*K flops per launch over its average duration,
 timed with HIP events on the stream the launches run on.
 
 `components` reports every other configuration and operator of the path,
-one entry per case of CASES (kernel time from HIP events over back-to-back
+one entry per case of COMPONENT_CASES (kernel time from HIP events over back-to-back
 launches in HIP graphs, the rate on algorithmic bytes or flops, and the
 rocprofv3 kernel average and PMC traffic of the committed summary in
 profiles/<profile>.md), the cold-cache variants of configs[2] and configs[3]
