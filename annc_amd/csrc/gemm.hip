@@ -1262,7 +1262,9 @@ int launch_pipe_tiles(const GemmParams& p, int64_t batch, hipStream_t stream) {
   // of a 1024->512 layer: 12.4 us against 19.6), and where up to three of
   // them per CU all run at once while 64x64 tiles would need a second round
   // (3072 rows of 1024->512: 31.0 us against 36.0 in 128x64 tiles)
-  if (tiles(64, 32) <= cus || (tiles(64, 64) > cus && tiles(64, 32) <= 3 * cus))
+  // (N < 32, one partial panel: wider tiles would only compute padding)
+  if (tiles(64, 32) <= cus || (tiles(64, 64) > cus && tiles(64, 32) <= 3 * cus) ||
+      (NT && p.n < 32))
     return launch_pipe<2, 1, 1, 1, 4, 1, 2, BRM, false, NT>(p, batch, stream);
   auto cost = [&](int bm, int bn) { return ceil_div(tiles(bm, bn), cus) * bm * bn; };
   const int64_t c128 = cost(128, 128), c128x64 = cost(128, 64), c64 = cost(64, 64);
@@ -1281,6 +1283,18 @@ int launch_pipe_tiles(const GemmParams& p, int64_t batch, hipStream_t stream) {
                    : launch_pipe<4, 2, 1, 2, 3, 1, 1, BRM, false, NT>(p, batch, stream);
   if (tiles(128, 64) >= 2 * cus) return launch_pipe<4, 2, 1, 1, 3, 2, 1, BRM, false, NT>(p, batch, stream);
   return launch_pipe<4, 2, 1, 1, 4, 2, 1, BRM, false, NT>(p, batch, stream);
+}
+
+// 4 < N < 32 (one partial panel) with more than one round of 32x32 blocks:
+// 64x32 pipelined tiles, whose B blocks load by 4-byte DMAs (any ldb) while
+// A streams through the LDS-DMA stages, instead of a second round of the
+// small kernel, whose waves each walk a quarter of K over 32 rows.  Same
+// box, the two libraries alternating, us: 9216x16x1024 20.8 -> 17.2,
+// 16384x16x1024 22.2 -> 18.2, 32768x16x1024 44.7 -> 26.6, 65536x8x256
+// 27.8 -> 21.0, 9216x20x845 19.1 -> 14.5, 9216x24x512 12.1 -> 9.9; with one
+// round (8192 rows) the small kernel stays ahead (9.6 against 16.6).
+bool skinny_pipe(const GemmParams& p, int64_t batch) {
+  return p.n > 4 && p.n < 32 && ((int64_t)(p.m + 31) / 32) * batch > 256;
 }
 
 // b_rowmajor: B is row-major with 16-byte aligned rows (p.b_vec), read in
@@ -1349,8 +1363,10 @@ int launch_gemm(const GemmParams& p, int64_t batch, hipStream_t stream) {
   };
   // Too few 64x64 tiles to occupy the chip, one round of 32x32 blocks, or
   // N < 32 (one 32-column block; the tile kernel would waste most of its
-  // 64-column tiles: 16384x16x1024 85 -> 12 us): 32x32 blocks with K split
-  // over four waves (eight measured slower at every K)
+  // 64-column tiles: 16384x16x1024 85 -> 22 us, and 18 us in the pipelined
+  // kernel, which annc_hip_gemm picks first beyond one round: skinny_pipe):
+  // 32x32 blocks with K split over four waves (eight measured slower at
+  // every K)
   if (!PACKED && (tiles(64, 64) < cus / 2 || tiles(32, 32) <= cus || p.n < 32))
     return launch_small<4>(p, batch, stream);
   if (tiles(128, 128) >= cus) return launch_tile<2, 2, 2, 2, PACKED>(p, batch, stream);
@@ -1388,7 +1404,9 @@ int launch_n_tail(const GemmParams& p, int64_t nf, const float* b_tail, int64_t 
   if (p.bias) t.bias = p.bias + nf;
   t.b_vec = ldb_tail % 4 == 0 && p.stride_b % 4 == 0 && aligned16(b_tail);
   t.b_dense = ldb_tail == t.n && p.stride_b % 4 == 0 && aligned16(b_tail);
-  return t.n <= 4 ? launch_gemv(t, batch, s) : launch_small<4>(t, batch, s);
+  if (t.n <= 4) return launch_gemv(t, batch, s);
+  if (skinny_pipe(t, batch)) return launch_packed_pipe(t, batch, s, /*b_rowmajor=*/true);
+  return launch_small<4>(t, batch, s);
 }
 
 // ---------------------------------------------------------------------------
@@ -1624,6 +1642,7 @@ int annc_hip_gemm(void* stream, int64_t batch, int64_t m, int64_t n, int64_t k, 
     const int rc = launch_gemv(p, batch, s);
     return set_error(rc, rc == ANNC_OK ? "" : "GEMV launch failed");
   }
+  if (n < 32 && skinny_pipe(p, batch)) return launch_packed_pipe(p, batch, s, /*b_rowmajor=*/true);
   // N % 32 != 0 with more than one round of 32x32 blocks in its full
   // 32-column panels: the pipelined kernel with a partial last panel (B
   // packed, or row-major with 16-byte aligned rows) where the extra column

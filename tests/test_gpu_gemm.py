@@ -780,6 +780,55 @@ def test_n_tail_split(batch, m, n, k, what):
             assert_gemm_close(got_b[z], ref, gemm_bound(a[z], w[z], np.broadcast_to(bias, ref.shape)))
 
 
+# 4 < N < 32 with more than one round of 32x32 blocks: 64x32 pipelined tiles
+# with one partial panel and no full ones (B by 4-byte DMAs from any ldb);
+# also the tail columns of a two-launch GEMM at such M
+SKINNY_PIPE_CASES = [
+    (1, 16384, 16, 1024, 0, 0, "one round of 64x32 tiles"),
+    (1, 9216, 20, 845, 0, 0, "K tail, partial round"),
+    (1, 65536, 8, 256, 0, 0, "1024 tiles: several rounds of three a CU"),
+    (1, 20000, 31, 100, 0, 0, "partial M tile, K tail"),
+    (1, 12000, 7, 300, 0, 0, "ldb = 7 (rows not 16-byte aligned)"),
+    (1, 10000, 12, 96, 3, 1, "ldb padded, A from a column offset (4-byte A DMAs)"),
+    (3, 4000, 12, 64, 0, 0, "batched: 375 blocks over the batch"),
+    (1, 9000, 5, 40, 0, 0, "N = 5, one k-block and a K tail"),
+    (1, 16384, 1009, 64, 1, 0, "row-major, unaligned rows: pipelined full panels, tail of 17 columns pipelined"),
+]
+
+
+@pytest.mark.parametrize("batch,m,n,k,ldb_pad,col0,what", SKINNY_PIPE_CASES)
+def test_skinny_n_pipelined(batch, m, n, k, ldb_pad, col0, what):
+    """Within the GEMM bound of OpenBLAS with bias and ReLU, and with an
+    addend and sigmoid; packed B (the format is row-major below 32 columns)
+    bit-identical to row-major B."""
+    note(f"skinny N pipelined b={batch} {m}x{n}x{k} ldb+{ldb_pad} col0={col0}: {what}")
+    g = workloads.rng(5 * m + n + k + batch)
+    abuf = g.standard_normal((batch, m, k + col0 + 3)).astype(np.float32)
+    a = np.ascontiguousarray(abuf[:, :, col0:col0 + k])
+    wide = (g.standard_normal((batch, k, n + ldb_pad)) / np.sqrt(k)).astype(np.float32)
+    w = np.ascontiguousarray(wide[:, :, :n])
+    bias = (g.standard_normal(n) * 0.1).astype(np.float32)
+    e = g.standard_normal((batch, m, n)).astype(np.float32)
+    da = to_dev(abuf)[:, :, col0:col0 + k]
+    dw = to_dev(wide)[:, :, :n]
+    dbias, de = to_dev(bias), to_dev(e)
+    if batch == 1:
+        got = to_host(dev.gemm(da[0], dw[0], bias=dbias, epilogue=EPI_RELU))[None]
+        sg = to_host(dev.gemm(da[0], dw[0], addend=de[0], epilogue=EPI_SIGMOID))[None]
+        if n < 32:
+            pk = to_host(dev.gemm(da[0], dev.pack_weight(dw[0]), bias=dbias, epilogue=EPI_RELU))
+            np.testing.assert_array_equal(pk, got[0])
+    else:
+        got = to_host(dev.gemm(da, dw, bias=dbias, epilogue=EPI_RELU))
+        sg = to_host(dev.gemm(da, dw, addend=de, epilogue=EPI_SIGMOID))
+    for z in range(batch):
+        ref = ora.dense_layer(a[z], w[z], bias, 1)
+        assert_gemm_close(got[z], ref, gemm_bound(a[z], w[z], np.broadcast_to(bias, ref.shape)))
+        lin = ora.matmul_add(e[z], a[z], w[z])
+        np.testing.assert_allclose(sg[z], 1.0 / (1.0 + np.exp(-lin.astype(np.float64))),
+                                   rtol=1e-4, atol=1e-5)
+
+
 # Few 32x32 blocks with a long K: K split over up to 8 workgroups, partial sums
 # added in split order by a second launch (K tails in the last split)
 SPLITK_CASES = [
