@@ -1297,8 +1297,9 @@ bool skinny_pipe(const GemmParams& p, int64_t batch) {
   return p.n > 4 && p.n < 32 && ((int64_t)(p.m + 31) / 32) * batch > 256;
 }
 
-// b_rowmajor: B is row-major with 16-byte aligned rows (p.b_vec), read in
-// place; otherwise B is in the layout_matmul packed format.
+// b_rowmajor: B is row-major, read in place, with 16-byte aligned rows
+// (p.b_vec) unless N < 32 (then every B block is the partial panel's, loaded
+// by 4-byte DMAs); otherwise B is in the layout_matmul packed format.
 int launch_packed_pipe(const GemmParams& p, int64_t batch, hipStream_t stream,
                        bool b_rowmajor = false) {
   const bool nt = (p.n & 31) != 0;
