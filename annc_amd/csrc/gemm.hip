@@ -339,6 +339,26 @@ __global__ __launch_bounds__(kThreads) void gemv_rows_kernel(GemmParams p) {
       chunk(av, bv);
     }
   }
+  // other layouts (B rows not dense or not aligned, A rows not aligned):
+  // scalar loads in the same k order, four chunks in flight per lane
+  for (; kk + 195 < K; kk += 256) {
+    float av[4][4], bv[4][4][N];
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int k = kk + 64 * u + e;
+        av[u][e] = A[k];
+#pragma unroll
+        for (int j = 0; j < N; ++j) bv[u][e][j] = B[(int64_t)k * p.ldb + j];
+      }
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+#pragma unroll
+        for (int j = 0; j < N; ++j) part[j] += av[u][e] * bv[u][e][j];
+  }
   for (; kk < K; kk += 64) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -1114,7 +1134,8 @@ __global__ void broadcast3_kernel(const float* __restrict__ src, int64_t s0, int
 // row-major tail region.
 __global__ __launch_bounds__(256) void pack_rhs_rowmajor_kernel(const float* __restrict__ src,
                                                                 int64_t ldb, int64_t stride_b,
-                                                                float* __restrict__ dst, int K,
+                                                                float* __restrict__ dst,
+                                                                int64_t dst_stride, int K,
                                                                 int N, int ppw) {
   __shared__ float tile[32][128 + 4];
   const int kb = K >> 5, t = blockIdx.x;
@@ -1122,7 +1143,7 @@ __global__ __launch_bounds__(256) void pack_rhs_rowmajor_kernel(const float* __r
   const int np = min(ppw, (N >> 5) - p0);
   const int n0 = 32 * p0, width = 32 * np;
   const float* __restrict__ bz = src + (int64_t)blockIdx.z * stride_b;
-  float* __restrict__ dz = dst + (int64_t)blockIdx.z * K * N;
+  float* __restrict__ dz = dst + (int64_t)blockIdx.z * dst_stride;
   const int tid = threadIdx.x;
   if (t < kb) {
     const int c = tid & 31, r = tid >> 5;
@@ -1158,6 +1179,21 @@ __global__ __launch_bounds__(256) void pack_rhs_rowmajor_kernel(const float* __r
     const int k = kf + i / width, n = n0 + i % width;
     dz[(int64_t)N * kf + (int64_t)(k - kf) * N + n] = bz[(int64_t)k * ldb + n];
   }
+}
+
+// The N % 32 tail columns [nf, nf + nt) of row-major B into the packed
+// format's N-tail region: row-major [K, nt] at offset nf*K of each batch's
+// dst_stride floats.
+__global__ __launch_bounds__(256) void pack_rhs_tail_kernel(const float* __restrict__ src,
+                                                            int64_t ldb, int64_t stride_b,
+                                                            float* __restrict__ dst,
+                                                            int64_t dst_stride, int64_t K,
+                                                            int64_t nf, int nt) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= K * nt) return;
+  const int64_t k = i / nt, c = i % nt;
+  dst[(int64_t)blockIdx.y * dst_stride + nf * K + i] =
+      src[(int64_t)blockIdx.y * stride_b + k * ldb + nf + c];
 }
 
 __global__ void pack_rhs_kernel(const float* __restrict__ src, float* __restrict__ dst, int64_t K,
@@ -1712,22 +1748,42 @@ int annc_hip_gemm(void* stream, int64_t batch, int64_t m, int64_t n, int64_t k, 
     };
     if (p.b_vec) return then_tail(launch_packed_pipe(q, batch, s, /*b_rowmajor=*/true));
     const int64_t tiles64 = ceil_div(m, 64) * ceil_div(nm, 64) * batch;
-    const int64_t packed_bytes = batch * k * nm * static_cast<int64_t>(sizeof(float));
+    // each batch's packed matrix starts 16-byte aligned (the packed kernels'
+    // 16-byte DMAs)
+    const int64_t bstride = (k * n + 3) & ~int64_t(3);
+    const int64_t packed_bytes = batch * bstride * static_cast<int64_t>(sizeof(float));
     if (tiles64 >= 128 && packed_bytes <= (int64_t(1) << 31)) {
       float* bp = static_cast<float*>(stream_workspace(s, static_cast<size_t>(packed_bytes)));
       if (bp) {
+        // B into the layout_matmul format, which then runs as packed B.  Where
+        // the partial panel costs no extra CU round of tiles (one_launch) the
+        // tail columns go into the format's row-major N-tail region too and
+        // run in the same launch, instead of a second launch that streams A
+        // again; otherwise the full panels run, then the tail columns from
+        // B itself (a copy would only add a launch).
         // Panels per workgroup: the widest that still gives >= 512 workgroups.
         const int64_t kcols = (k >> 5) + ((k & 31) ? 1 : 0), panels = nm >> 5;
         int ppw = 4;
         while (ppw > 1 && kcols * ceil_div(panels, ppw) * batch < 512) ppw >>= 1;
         const dim3 grid((unsigned)kcols, (unsigned)ceil_div(panels, ppw), (unsigned)batch);
         hipLaunchKernelGGL(pack_rhs_rowmajor_kernel, grid, dim3(256), 0, s, b, ldb, stride_b, bp,
-                           (int)k, (int)nm, ppw);
+                           bstride, (int)k, (int)nm, ppw);
         ANNC_HIP_TRY(hipGetLastError());
-        q.b = bp;
-        q.ldb = nm;
-        q.stride_b = k * nm;
-        return then_tail(launch_packed_pipe(q, batch, s));
+        if (nm < n && one_launch) {
+          const dim3 tgrid((unsigned)ceil_div(k * (n - nm), 256), (unsigned)batch);
+          hipLaunchKernelGGL(pack_rhs_tail_kernel, tgrid, dim3(256), 0, s, b, ldb, stride_b, bp,
+                             bstride, k, nm, (int)(n - nm));
+          ANNC_HIP_TRY(hipGetLastError());
+        }
+        GemmParams r = p;
+        r.b = bp;
+        r.ldb = n;
+        r.stride_b = bstride;
+        if (nm == n || one_launch) return launch_packed_pipe(r, batch, s);
+        GemmParams f = r;
+        f.n = static_cast<int>(nm);
+        f.ldb = nm;
+        return then_tail(launch_packed_pipe(f, batch, s));
       }
     }
   }

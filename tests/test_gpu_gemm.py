@@ -729,28 +729,31 @@ def test_packed_mid_batches(m, n, k, col0):
 
 # N % 32 != 0 with more than one round of 32x32 blocks in the full panels:
 # the pipelined kernel with a partial last panel (packed B, and row-major B
-# with 16-byte aligned rows), or, for other row-major B, the full panels
-# pipelined and the tail columns through the small kernel (N % 32 > 4) or
-# the GEMV kernel (N % 32 <= 4).
+# with 16-byte aligned rows read in place; other row-major B is packed per
+# call, tail columns included, and runs as packed B), or, where the extra
+# column of tiles costs a CU round, the full panels and then the tail
+# columns through the small kernel (N % 32 > 4) or the GEMV kernel.
 N_TAIL_CASES = [
     (1, 4096, 1000, 1024, "8 tail columns"),
-    (1, 4096, 515, 845, "3 tail columns; row-major rows unaligned (pack + GEMV tail), K tail"),
+    (1, 4096, 515, 845, "3 tail columns; row-major rows unaligned (packed per call), K tail"),
     (1, 2048, 300, 845, "12 tail columns, K tail"),
     (3, 1024, 100, 64, "batched, 4 tail columns"),
-    (1, 8200, 33, 256, "one full panel, 1 tail column (row-major: pack + GEMV tail)"),
+    (1, 8200, 33, 256, "one full panel, 1 tail column (row-major: packed per call)"),
     (2, 777, 620, 100, "batched, partial M tile, 12 tail columns, K tail"),
-    (1, 4096, 1001, 40, "unaligned rows (pack + small tail), 1 k-block + K tail"),
+    (1, 4096, 1001, 40, "unaligned rows (packed per call), 1 k-block + K tail"),
     (1, 8192, 1000, 864, "256x128 tiles with a partial panel"),
     (1, 1200, 340, 512, "64x32 tiles with a partial panel"),
     (1, 4096, 1000, 20, "K < 32 (K tail only), partial panel"),
+    (1, 4096, 521, 1024, "unaligned rows, two launches (a fifth round of tiles)"),
+    (2, 2048, 1001, 97, "batched, unaligned rows: K*N odd, batch strides of the per-call pack aligned"),
 ]
 
 
 @pytest.mark.parametrize("batch,m,n,k,what", N_TAIL_CASES)
 def test_n_tail_split(batch, m, n, k, what):
     """Within the GEMM bound of OpenBLAS with bias and ReLU, and with an
-    addend and sigmoid; packed B and row-major B with 16-byte aligned rows
-    (the same kernel) bit-identical."""
+    addend and sigmoid; packed B and row-major B (read in place, or packed
+    per call) bit-identical."""
     note(f"N-tail split b={batch} {m}x{n}x{k}: {what}")
     g = workloads.rng(3 * m + n + k + batch)
     a = g.standard_normal((batch, m, k)).astype(np.float32)
@@ -769,10 +772,7 @@ def test_n_tail_split(batch, m, n, k, what):
                                    atol=1e-5)
         if batch == 1:
             rm = to_host(dev.gemm(da[z], to_dev(w[z]), bias=dbias, epilogue=EPI_RELU))
-            if n % 4 == 0:
-                np.testing.assert_array_equal(got, rm)
-            else:
-                assert_gemm_close(rm, ref, gemm_bound(a[z], w[z], np.broadcast_to(bias, ref.shape)))
+            np.testing.assert_array_equal(got, rm)
     if batch > 1:  # one batched row-major call: the same per-batch results
         got_b = to_host(dev.gemm(da, to_dev(w), bias=dbias, epilogue=EPI_RELU))
         for z in range(batch):
