@@ -306,6 +306,19 @@ def make_case(name: str, device, inp: Inputs) -> Case:
                     2.0 * m * n * k, "mfma",
                     f"[{m}x{k}] . packed [{k}x{n}] + bias, ReLU (31 full panels and a partial "
                     "one of 8 columns)", "gemm_ntail_4096x1000x1024")
+    if name == "gemm_skinny":
+        # a 16-wide layer over many rows: 64x32 pipelined tiles with one
+        # partial panel (row-major B by 4-byte DMAs)
+        g = workloads.rng(10)
+        m, k, n = 16384, 1024, 16
+        x = t(g.standard_normal((m, k)).astype(np.float32))
+        w = t(workloads.glorot_uniform(g, k, n))
+        bias = t((g.standard_normal(n) * 0.01).astype(np.float32))
+        out = torch.empty((m, n), dtype=torch.float32, device=device)
+        return Case(name, lambda i: dev.gemm(x, w, bias=bias, epilogue=EPI_RELU, out=out),
+                    2.0 * m * n * k, "mfma",
+                    f"[{m}x{k}] . row-major [{k}x{n}] + bias, ReLU (64x32 pipelined tiles, one "
+                    "partial panel; HBM-bound on A's 67 MB)", "gemm_skinny_16384x16x1024")
     if name == "gemm_e2e_l1":
         w = inp.get("config5")
         k0 = w.weights[0].shape[0]
@@ -535,7 +548,7 @@ def make_case(name: str, device, inp: Inputs) -> Case:
 
 
 CASES = ("tower", "widedeep", "gemm_l1", "tower_tail", "gemm_l2", "gemm_l3", "gemm_small",
-         "gemm_l1_b64", "gemm_ntail", "gemm_e2e_l1", "batch_matmul",
+         "gemm_l1_b64", "gemm_ntail", "gemm_skinny", "gemm_e2e_l1", "batch_matmul",
          "bag_sum", "bag_mean", "bag_sum_cold", "bag_phase_empty", "bag_phase_hotrow", "hashed",
          "hashed_cold", "hashed_nohash", "hashed_dim32", "sparse_embedding2", "pooling",
          "segment_reduce_sorted",
